@@ -1,0 +1,23 @@
+"""MI355X-native speculative verify/accept path and paged KV cache.
+
+gfx950 HIP kernels (libcoopt_amd.so, C ABI in include/coopt_amd.h) behind the Python call
+surface of mohsinmubarak/iitj-llm-coopt's engine:
+  spec_decode   sample / verify / batched accept      (engine/spec_decode.py)
+  kv_cache      quantize / dequantize / paged write   (engine/kv_tier_manager.py, model.py:242)
+  attention     flash_attn_varlen_func-compatible paged verification attention (model.py:244)
+  block_manager BlockManager slot / block-table contract (engine/block_manager.py)
+  batch         WorkItem / Batch / build_batch varlen layout (engine/batch.py)
+"""
+from . import _lib  # noqa: F401  (imports torch first, then binds the library lazily)
+from .attention import flash_attn_varlen_func, paged_attention
+from .batch import Batch, WorkItem, build_batch, build_padded_batch
+from .block_manager import BlockManager, OutOfBlocks
+from .kv_cache import allocate_kv_cache, dequantize, quantize, reshape_and_cache_flash
+from .spec_decode import AcceptResult, accept, sample, softmax, verify
+
+__all__ = [
+    "flash_attn_varlen_func", "paged_attention", "Batch", "WorkItem", "build_batch",
+    "build_padded_batch", "BlockManager", "OutOfBlocks", "allocate_kv_cache", "dequantize",
+    "quantize", "reshape_and_cache_flash", "AcceptResult", "accept", "sample", "softmax",
+    "verify",
+]

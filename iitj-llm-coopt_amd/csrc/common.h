@@ -1,0 +1,106 @@
+// Shared helpers for the gfx950 kernels of libcoopt_amd.so: number formats, wave-level
+// reductions, and the host-side error plumbing of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/coopt_amd.h"
+
+#define COOPT_WAVE 64
+
+// ---------------------------------------------------------------------------------------
+// Host side: per-thread error text and argument checks.
+// ---------------------------------------------------------------------------------------
+namespace coopt {
+
+void set_error(const std::string& msg);
+void clear_error();
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Checks hipGetLastError() after a launch; records the message on failure.
+int check_launch(const char* what);
+
+}  // namespace coopt
+
+#define COOPT_REQUIRE(cond, msg)                                 \
+  do {                                                           \
+    if (!(cond)) {                                               \
+      coopt::set_error(std::string(__func__) + ": " + (msg));   \
+      return COOPT_EINVAL;                                       \
+    }                                                            \
+  } while (0)
+
+// ---------------------------------------------------------------------------------------
+// Device side: number formats.  bf16 values travel as raw uint16_t bit patterns.
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// fp32 -> bf16, round to nearest even (NaN stays NaN), as torch's .to(torch.bfloat16).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// fp32 -> fp16, round to nearest even with fp16 subnormals (v_cvt_f16_f32 in the default
+// rounding mode), as torch's .to(torch.float16).
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_shfl_xor(T v, int mask) {
+  return __shfl_xor(v, mask, COOPT_WAVE);
+}
+
+// Max over aligned groups of `G` consecutive lanes (G a power of two <= 64).
+template <int G>
+__device__ __forceinline__ uint32_t group_max_u32(uint32_t v) {
+#pragma unroll
+  for (int m = 1; m < G; m <<= 1) {
+    uint32_t o = __shfl_xor(v, m, COOPT_WAVE);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+  for (int m = 1; m < COOPT_WAVE; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, COOPT_WAVE));
+  return v;
+}
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int m = 1; m < COOPT_WAVE; m <<= 1) v += __shfl_xor(v, m, COOPT_WAVE);
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+  for (int m = 1; m < COOPT_WAVE; m <<= 1) v += __shfl_xor(v, m, COOPT_WAVE);
+  return v;
+}
+
+// Device-scope atomics used by the "last block finishes the reduction" pattern.
+__device__ __forceinline__ unsigned atomic_add_acq_rel(unsigned* p, unsigned v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void atomic_store_relaxed(unsigned* p, unsigned v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T load_agent(const T* p) {
+  return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}

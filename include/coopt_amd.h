@@ -1,0 +1,172 @@
+/*
+ * coopt_amd.h -- C ABI of libcoopt_amd.so, the MI355X (gfx950) kernels behind the
+ * speculative verify/accept path and the paged KV cache it reads.
+ *
+ * Conventions shared by every entry point:
+ *   - Plain pointers to device memory, element strides (not bytes), int sizes.
+ *     The last dimension of every tensor argument (head_dim, vocab) is contiguous.
+ *   - Every call is enqueued on `stream` (a hipStream_t; NULL = the null stream),
+ *     allocates nothing, never synchronises the host, and is safe to record into a
+ *     HIP graph. Calls are reentrant; the only global is the per-thread error text.
+ *   - Return value: COOPT_OK (0) or a negative COOPT_E* code; coopt_last_error()
+ *     then holds a message for the calling thread.
+ *   - Workspaces are caller-owned device buffers of at least the size the matching
+ *     *_workspace() function returns; they must be zero-filled once before their first
+ *     use and are left zero-filled on return (so they can be reused across calls and
+ *     graph replays without a memset). Two calls that overlap in time on the same
+ *     workspace race.
+ *
+ * Reference interfaces replaced (paths under mohsinmubarak/iitj-llm-coopt):
+ *   coopt_kv_write          vLLM reshape_and_cache_flash   engine/model.py:242-243
+ *                           (semantics: engine/model.py:190,201-203; tests/kv_write_check.py:26-30)
+ *   coopt_verify_attention  vLLM flash_attn_varlen_func    engine/model.py:244-247 (and :204-207)
+ *   coopt_accept_sample     spec_decode.verify / sample     engine/spec_decode.py:12-49,
+ *                           batched as at engine/engine.py:421-446
+ *   coopt_quantize /        kv_tier_manager.quantize /     engine/kv_tier_manager.py:21-41
+ *   coopt_dequantize        dequantize
+ *   coopt_softmax           torch.softmax(logits / T)       engine/spec_decode.py:16
+ */
+#ifndef COOPT_AMD_H
+#define COOPT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* coopt_stream_t; /* hipStream_t */
+
+enum {
+  COOPT_OK = 0,
+  COOPT_EINVAL = -1,     /* bad argument (null pointer, unsupported shape, misalignment) */
+  COOPT_EHIP = -2,       /* the HIP runtime reported an error (launch failure) */
+  COOPT_EWORKSPACE = -3  /* workspace smaller than the *_workspace() size */
+};
+
+enum {
+  COOPT_DT_F32 = 0,
+  COOPT_DT_BF16 = 1,
+  COOPT_DT_F16 = 2,
+  COOPT_DT_I8 = 3
+};
+
+/* Message describing the last failed call on this thread ("" if none). */
+const char* coopt_last_error(void);
+
+/* hipRuntimeGetVersion() of the HIP runtime this library is bound to. */
+int coopt_hip_runtime_version(int* version);
+
+/*
+ * Paged KV write.  Replaces reshape_and_cache_flash(k, v, k_cache, v_cache, slot_mapping,
+ * "auto", k_scale, v_scale) at engine/model.py:242-243; the reference defines it as
+ *   k_cache[slot // block_size, slot % block_size] = k   (engine/model.py:190, 201-203).
+ *
+ *   k, v        [T, Hkv, D] bf16, strides (in_tok_stride, in_head_stride, 1), shared by k and v
+ *   cache_dtype COOPT_DT_BF16: k_cache/v_cache are bf16 [NB, block_size, Hkv, D]
+ *               COOPT_DT_I8:   k_cache/v_cache are int8 codes of the same shape and
+ *                              k_scale/v_scale are fp16 [NB, block_size, Hkv]; each (token, head)
+ *                              vector is quantised as kv_tier_manager.quantize(x, 8) does
+ *                              (engine/kv_tier_manager.py:21-31), codes and scales bit-exact.
+ *   cache strides (c_blk, c_tok, c_head, 1) may describe a strided per-layer view of a
+ *   block-major buffer (engine/elastic.py:74-77); scale strides (s_blk, s_tok, s_head).
+ *   slot_mapping [T] int64.  A slot < 0 or >= num_blocks * block_size is skipped (padding).
+ *   D must be a multiple of 8 with D/8 a power of two <= 64; k/v/cache rows 16-byte aligned.
+ */
+int coopt_kv_write(int cache_dtype,
+                   const void* k, const void* v, int64_t in_tok_stride, int64_t in_head_stride,
+                   void* k_cache, void* v_cache,
+                   int64_t c_blk_stride, int64_t c_tok_stride, int64_t c_head_stride,
+                   void* k_scale, void* v_scale,
+                   int64_t s_blk_stride, int64_t s_tok_stride, int64_t s_head_stride,
+                   const int64_t* slot_mapping, int T, int Hkv, int D, int block_size,
+                   int64_t num_blocks, coopt_stream_t stream);
+
+/*
+ * Symmetric absmax codec over contiguous rows, kv_tier_manager.quantize / dequantize
+ * (engine/kv_tier_manager.py:21-41).
+ *   coopt_quantize:   x [rows, D] (in_dtype BF16/F16/F32) -> q, scale [rows] fp16.
+ *                     bits 8: q int8 [rows, D];  bits 4: q uint8 [rows, D/2], even element in
+ *                     the low nibble, odd element in the high nibble, both offset by +8.
+ *   coopt_dequantize: q, scale -> out [rows, D] in out_dtype (BF16/F16/F32).
+ * D must be even and <= 4096.
+ */
+int coopt_quantize(int bits, int in_dtype, const void* x, int64_t rows, int D,
+                   void* q, void* scale, coopt_stream_t stream);
+int coopt_dequantize(int bits, const void* q, const void* scale, int64_t rows, int D,
+                     int out_dtype, void* out, coopt_stream_t stream);
+
+/*
+ * Paged GQA verification attention.  Replaces flash_attn_varlen_func(q, k_cache, v_cache,
+ * cu_seqlens_q, max_seqlen_q, seqused_k=seq_lens, max_seqlen_k, softmax_scale, causal=True,
+ * block_table) at engine/model.py:244-247.  For sequence b with n = cu[b+1]-cu[b] query rows
+ * and L = seq_lens[b] keys, query j and head h attend to keys [0, L - n + j] of KV head
+ * h / (Hq/Hkv) (causal mask aligned bottom-right, engine/model.py:8-10).
+ *
+ *   q      [T, Hq, D] bf16 (q_tok_stride, q_head_stride, 1);  out likewise (o_tok_stride, ...)
+ *   kv_dtype COOPT_DT_BF16: caches bf16 [NB, block_size, Hkv, D], k_scale/v_scale unused
+ *            COOPT_DT_I8:   caches int8 codes, k_scale/v_scale fp16 [NB, block_size, Hkv];
+ *                           dequantisation code * scale is fused into the kernel.
+ *   block_table [B, bt_stride] int32; entries past ceil(L/block_size) are never read.
+ *   Supported: D in {64, 128}; (Hq/Hkv) * max_seqlen_q <= 64; block_size a power of two.
+ *   workspace: coopt_verify_attention_workspace() bytes, zero-filled once (see above).
+ */
+size_t coopt_verify_attention_workspace(int B, int Hq, int Hkv, int D, int max_seqlen_q,
+                                        int max_seqlen_k);
+int coopt_verify_attention(int kv_dtype,
+                           const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                           const void* k_cache, const void* v_cache,
+                           int64_t c_blk_stride, int64_t c_tok_stride, int64_t c_head_stride,
+                           const void* k_scale, const void* v_scale,
+                           int64_t s_blk_stride, int64_t s_tok_stride, int64_t s_head_stride,
+                           const int32_t* block_table, int64_t bt_stride,
+                           const int32_t* cu_seqlens_q, const int32_t* seq_lens,
+                           int B, int Hq, int Hkv, int D, int block_size, int64_t num_blocks,
+                           int max_seqlen_q, int max_seqlen_k, float softmax_scale,
+                           void* out, int64_t o_tok_stride, int64_t o_head_stride,
+                           void* workspace, size_t workspace_bytes, coopt_stream_t stream);
+
+/*
+ * Fused speculative acceptance for a batch (engine/spec_decode.py:20-49, looped over the
+ * batch at engine/engine.py:437-446), with the random draws made explicit:
+ *   temperature > 0:  p_i = softmax(target_i * (1/T)), q_i = softmax(draft_i * (1/T))
+ *     (draft_kind 1: draft rows already hold q_i, fp32).  Draft i is accepted while
+ *     u_accept[b,i] < min(1, p_i[d_i] / max(q_i[d_i], 1e-20)); k = first rejection (or g_b).
+ *     The emitted token is drawn by inverse CDF with u_resample[b] from max(0, p_k - q_k)
+ *     (normalised; p_k if it sums to 0) or, when all g_b drafts are accepted, from p_{g_b}:
+ *     the smallest index j with cumsum(w)[j] > u * sum(w).
+ *   temperature <= 0: greedy; argmax (first index on ties) per row, accept while equal.
+ * Rows: sequence b's target rows are target_row0[b] + i (i <= g_b) of a row-major
+ * [*, V] array with row stride target_row_stride (target_row0 NULL: b*(gamma_max+1));
+ * its draft rows are draft_row0[b] + i (i < g_b) (NULL: b*gamma_max).
+ * g_b = gamma_per_seq[b] (NULL: gamma_max), 0 <= g_b <= gamma_max.
+ * Outputs: accepted_len[b] = k; out_tokens[b, 0..k] = d_0..d_{k-1}, token; the rest -1.
+ * margin[b] (optional) = the smallest distance between a uniform and the boundary that
+ * decided it (|u_i - ratio_i| for i <= k, and the inverse-CDF distance in probability
+ * mass), so callers can report decisions within rounding of a boundary as ties.
+ * logits_dtype COOPT_DT_F32 or COOPT_DT_BF16 (target and draft logits alike).
+ */
+size_t coopt_accept_sample_workspace(int B, int gamma_max, int V);
+int coopt_accept_sample(int logits_dtype,
+                        const void* target, int64_t target_row_stride, const int32_t* target_row0,
+                        int draft_kind, const void* draft, int64_t draft_row_stride,
+                        const int32_t* draft_row0,
+                        const int32_t* draft_tokens, const int32_t* gamma_per_seq,
+                        const float* u_accept, const float* u_resample, float temperature,
+                        int B, int gamma_max, int V,
+                        int32_t* accepted_len, int32_t* out_tokens, float* margin,
+                        void* workspace, size_t workspace_bytes, coopt_stream_t stream);
+
+/*
+ * probs[r, :] = softmax(logits[r, :] * (1/T)) in fp32 (engine/spec_decode.py:16), for the
+ * probabilities sample() returns.  logits F32 or BF16 with row stride in_stride.
+ */
+int coopt_softmax(int logits_dtype, const void* logits, int64_t in_stride, int64_t rows, int V,
+                  float temperature, float* probs, int64_t out_stride, coopt_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* COOPT_AMD_H */

@@ -1,0 +1,219 @@
+"""GPU parity: paged GQA verification attention vs oracle.paged (float64 closed form).
+
+Bar (north star): max-abs error <= 2e-2 with bf16 KV and <= 5e-2 with INT8 KV (against
+attention over dequantize(quantize(KV)) in bf16, eval/quality.py:48-52).
+"""
+import numpy as np
+import pytest
+import torch
+
+import iitj_llm_coopt_amd as M
+from oracle import paged as OP
+
+pytestmark = pytest.mark.gpu
+TOL_BF16, TOL_INT8 = 2e-2, 5e-2
+
+
+def report(msg):
+    print(msg, flush=True)
+
+
+class Pool:
+    """A shared block pool with randomly permuted block tables (the configs' layout)."""
+
+    def __init__(self, ctx, q_lens, Hq, Hkv, D, dev, kv="auto", bs=16, seed=0, slack=3,
+                 outlier=0.0):
+        self.ctx, self.q_lens, self.bs, self.dev, self.kv = list(ctx), list(q_lens), bs, dev, kv
+        B = len(ctx)
+        seq = [c + n for c, n in zip(ctx, q_lens)]
+        nblk = sum(-(-L // bs) for L in seq) + slack
+        rng = np.random.default_rng(seed)
+        self.bm = M.BlockManager(nblk, bs, free_order=rng.permutation(nblk))
+        for s in range(B):
+            self.bm.ensure(s, seq[s])
+        self.kc, self.vc, self.ks, self.vs = M.allocate_kv_cache(nblk, bs, Hkv, D, kv, device=dev)
+        gen = torch.Generator(device=dev).manual_seed(seed)
+        # every position of every sequence gets K/V through the product write path
+        slots = torch.cat([self.bm.slot_mapping(s, 0, seq[s]) for s in range(B)]).to(dev)
+        T = slots.numel()
+        k = torch.randn(T, Hkv, D, generator=gen, device=dev)
+        v = torch.randn(T, Hkv, D, generator=gen, device=dev)
+        if outlier:
+            k = torch.where(torch.rand(k.shape, generator=gen, device=dev) < outlier, k * 20, k)
+            v = torch.where(torch.rand(v.shape, generator=gen, device=dev) < outlier, v * 20, v)
+        M.reshape_and_cache_flash(k.to(torch.bfloat16), v.to(torch.bfloat16), self.kc, self.vc,
+                                  slots, kv, self.ks, self.vs)
+        self.cu = torch.tensor(np.concatenate([[0], np.cumsum(q_lens)]), dtype=torch.int32,
+                               device=dev)
+        self.seq_lens = torch.tensor(seq, dtype=torch.int32, device=dev)
+        self.table = self.bm.block_table_tensor(list(range(B))).to(dev)
+        self.q = torch.randn(int(sum(q_lens)), Hq, D, generator=gen, device=dev).to(torch.bfloat16)
+        self.D = D
+
+    def run(self, q=None, **kw):
+        return M.flash_attn_varlen_func(
+            q=self.q if q is None else q, k=self.kc, v=self.vc, cu_seqlens_q=self.cu,
+            max_seqlen_q=max(self.q_lens), seqused_k=self.seq_lens,
+            max_seqlen_k=int(max(c + n for c, n in zip(self.ctx, self.q_lens))),
+            softmax_scale=self.D ** -0.5, causal=True, block_table=self.table,
+            k_scale=self.ks, v_scale=self.vs, **kw)
+
+    def oracle_seq(self, b):
+        """float64 attention of sequence b from the cache contents (dequantised if INT8)."""
+        L = int(self.seq_lens[b])
+        rows = self.table[b, : -(-L // self.bs)].long()
+        pos = torch.arange(L, device=self.dev)
+        blk, off = rows[pos // self.bs], pos % self.bs
+        if self.kv == "int8":
+            K = OP.dequantized_cache(self.kc[blk, off].cpu().numpy(), self.ks[blk, off].cpu().numpy())
+            V = OP.dequantized_cache(self.vc[blk, off].cpu().numpy(), self.vs[blk, off].cpu().numpy())
+        else:
+            K = self.kc[blk, off].float().cpu().numpy()
+            V = self.vc[blk, off].float().cpu().numpy()
+        q0, q1 = int(self.cu[b]), int(self.cu[b + 1])
+        return OP.attention_seq(self.q[q0:q1].float().cpu().numpy(), K, V, self.D ** -0.5)
+
+    def max_err(self, out, seqs=None):
+        seqs = range(len(self.ctx)) if seqs is None else seqs
+        err = 0.0
+        o = out.float().cpu().numpy()
+        for b in seqs:
+            q0, q1 = int(self.cu[b]), int(self.cu[b + 1])
+            err = max(err, float(np.abs(o[q0:q1] - self.oracle_seq(b)).max()))
+        return err
+
+
+def test_strided_kv_check_shapes_and_block_major_view(dev):
+    """tests/strided_kv_check.py: seq_lens [37, 200, 5], q_lens [1, 3, 5], HKV 8, HQ 32, D 128
+    in a 64-block pool; a per-layer view of a block-major buffer gives identical output."""
+    NB, L, BS, HKV, HQ, D = 64, 4, 16, 8, 32, 128
+    gen = torch.Generator(device=dev).manual_seed(0)
+    buf = torch.randn(NB, L, 2, BS, HKV, D, generator=gen, device=dev).to(torch.bfloat16)
+    ks, vs = buf[:, 2, 0], buf[:, 2, 1]
+    kc, vc = ks.contiguous(), vs.contiguous()
+    seq_lens = torch.tensor([37, 200, 5], dtype=torch.int32, device=dev)
+    cu = torch.tensor([0, 1, 4, 9], dtype=torch.int32, device=dev)
+    table = torch.randperm(NB, generator=gen, device=dev)[:48].view(3, 16).to(torch.int32)
+    q = torch.randn(9, HQ, D, generator=gen, device=dev).to(torch.bfloat16)
+    kw = dict(q=q, cu_seqlens_q=cu, max_seqlen_q=5, seqused_k=seq_lens, max_seqlen_k=200,
+              softmax_scale=D ** -0.5, causal=True, block_table=table, fa_version=2)
+    a = M.flash_attn_varlen_func(k=kc, v=vc, **kw)
+    b = M.flash_attn_varlen_func(k=ks, v=vs, **kw)
+    assert torch.equal(a, b)
+    ref = OP.attention(q.float().cpu().numpy(), kc.float().cpu().numpy(), vc.float().cpu().numpy(),
+                       cu.cpu().numpy(), seq_lens.cpu().numpy(), table.cpu().numpy(), BS, D ** -0.5)
+    err = float(np.abs(a.float().cpu().numpy() - ref).max())
+    report(f"[strided] max-abs {err:.3g}")
+    assert err <= TOL_BF16
+
+
+def test_config3_bf16_verify(dev):
+    """Config 3: B 32, Hq 32 / Hkv 8, D 128, q_len 5, ctx U[512, 4096], bs 16, bf16."""
+    rng = np.random.default_rng(3)
+    ctx = rng.integers(512, 4097, 32)
+    pool = Pool(ctx, [5] * 32, 32, 8, 128, dev, "auto", seed=3)
+    out = pool.run()
+    err = pool.max_err(out)
+    report(f"[config3] max-abs {err:.3g}")
+    assert err <= TOL_BF16
+
+
+@pytest.mark.parametrize("gamma", [2, 4, 8])
+def test_config4_int8_verify(dev, gamma):
+    """Config 4: B 64, ctx U[4096, 16384], q_len gamma+1, INT8 KV quantised from N(0,1) with
+    1% x20 outliers, dequantisation fused.  Checked on 16 of the 64 sequences (and all rows
+    of those) to keep the float64 oracle within seconds."""
+    rng = np.random.default_rng(4 + gamma)
+    ctx = rng.integers(4096, 16385, 64)
+    pool = Pool(ctx, [gamma + 1] * 64, 32, 8, 128, dev, "int8", seed=gamma, outlier=0.01)
+    out = pool.run()
+    assert bool(torch.isfinite(out.float()).all())
+    seqs = list(range(0, 64, 4))
+    err = pool.max_err(out, seqs)
+    report(f"[config4 gamma={gamma}] max-abs {err:.3g} on {len(seqs)} sequences")
+    assert err <= TOL_INT8
+
+
+def test_int8_equals_bf16_kernel_on_dequantised_cache(dev):
+    """INT8 path vs the bf16 path over the bf16 dequantisation of the same cache."""
+    rng = np.random.default_rng(5)
+    ctx = rng.integers(100, 3000, 8)
+    pool = Pool(ctx, [5] * 8, 32, 8, 128, dev, "int8", seed=5, outlier=0.01)
+    a = pool.run()
+    kd = M.dequantize(pool.kc, pool.ks, 8, torch.bfloat16)
+    vd = M.dequantize(pool.vc, pool.vs, 8, torch.bfloat16)
+    b = M.flash_attn_varlen_func(q=pool.q, k=kd, v=vd, cu_seqlens_q=pool.cu,
+                                 max_seqlen_q=5, seqused_k=pool.seq_lens,
+                                 max_seqlen_k=int(pool.seq_lens.max()), softmax_scale=128 ** -0.5,
+                                 block_table=pool.table)
+    assert float((a.float() - b.float()).abs().max()) <= 2e-2
+
+
+@pytest.mark.parametrize("kv", ["auto", "int8"])
+def test_head_dim_64_decode_and_catch_up_shapes(dev, kv):
+    """Draft-model shapes (Llama-3.2-1B: Hq 32, Hkv 8, D 64): q_len 1 and 2, ragged contexts,
+    including a sequence whose keys are only its own new tokens (ctx 0)."""
+    ctx = [0, 1, 15, 16, 17, 300, 1000, 4099]
+    ql = [1, 2, 1, 2, 1, 2, 1, 2]
+    pool = Pool(ctx, ql, 32, 8, 64, dev, kv, seed=6)
+    out = pool.run()
+    err = pool.max_err(out)
+    report(f"[D=64 {kv}] max-abs {err:.3g}")
+    assert err <= (TOL_BF16 if kv == "auto" else TOL_INT8)
+
+
+def test_noncontiguous_q_and_out_views(dev):
+    rng = np.random.default_rng(7)
+    ctx = rng.integers(10, 2000, 5)
+    pool = Pool(ctx, [3] * 5, 32, 8, 128, dev, "auto", seed=7)
+    T = pool.q.shape[0]
+    qkv = torch.zeros(T, (32 + 16) * 128, device=dev, dtype=torch.bfloat16)
+    qkv[:, : 32 * 128] = pool.q.reshape(T, -1)
+    qv = qkv[:, : 32 * 128].view(T, 32, 128)
+    big = torch.zeros(T, 2, 32, 128, device=dev, dtype=torch.bfloat16)
+    out = pool.run(q=qv, out=big[:, 1])
+    assert out.data_ptr() == big[:, 1].data_ptr()
+    assert torch.equal(big[:, 1], pool.run()) and bool((big[:, 0] == 0).all())
+
+
+def test_padded_graph_layout_leaves_real_rows_unchanged(dev):
+    """engine/cuda_graphs.py:7-16: stride-S padding with seq_len = start + S, padding slots in
+    a scratch block and dummy sequences; real rows equal the unpadded result."""
+    Hq, Hkv, D, bs, S = 32, 8, 128, 16, 5
+    starts, n = [40, 700, 3], [3, 5, 1]
+    nblk = 200
+    kc, vc, _, _ = M.allocate_kv_cache(nblk, bs, Hkv, D, "auto", device=dev)
+    gen = torch.Generator(device=dev).manual_seed(8)
+    kc.copy_(torch.randn(kc.shape, generator=gen, device=dev).to(torch.bfloat16))
+    vc.copy_(torch.randn(vc.shape, generator=gen, device=dev).to(torch.bfloat16))
+    bm = M.BlockManager(nblk - 1, bs)  # the last block is the scratch block
+    items = [M.WorkItem(i, [1] * n[i], starts[i], all_logits=True) for i in range(3)]
+    real, _ = M.build_batch(items, bm, device=dev)
+    qr = torch.randn(sum(n), Hq, D, generator=gen, device=dev).to(torch.bfloat16)
+    ref = M.flash_attn_varlen_func(q=qr, k=kc, v=vc, cu_seqlens_q=real.cu_seqlens_q,
+                                   max_seqlen_q=real.max_seqlen_q, seqused_k=real.seq_lens,
+                                   max_seqlen_k=real.max_seqlen_k, block_table=real.block_table)
+    pad, spans = M.build_padded_batch(items, bm, S, 4, 64, (nblk - 1) * bs, device=dev)
+    qp = torch.randn(4 * S, Hq, D, generator=gen, device=dev).to(torch.bfloat16)
+    off = 0
+    for i, (row, cnt) in enumerate(spans):
+        qp[row:row + cnt] = qr[off:off + cnt]
+        off += cnt
+    got = M.flash_attn_varlen_func(q=qp, k=kc, v=vc, cu_seqlens_q=pad.cu_seqlens_q,
+                                   max_seqlen_q=S, seqused_k=pad.seq_lens,
+                                   max_seqlen_k=pad.max_seqlen_k, block_table=pad.block_table)
+    off = 0
+    for row, cnt in spans:
+        assert float((got[row:row + cnt].float() - ref[off:off + cnt].float()).abs().max()) <= 1e-2
+        off += cnt
+
+
+def test_workspace_is_reusable_across_calls_and_shapes(dev):
+    """Counters are left at zero: repeated calls, and a smaller call after a larger one on
+    the same workspace, give the same results as fresh workspaces."""
+    rng = np.random.default_rng(9)
+    big = Pool(rng.integers(2000, 9000, 16), [5] * 16, 32, 8, 128, dev, "auto", seed=9)
+    small = Pool(rng.integers(100, 3000, 4), [3] * 4, 32, 8, 128, dev, "auto", seed=10)
+    a1, b1 = big.run(), small.run()
+    a2, b2 = big.run(), small.run()
+    assert torch.equal(a1, a2) and torch.equal(b1, b2)

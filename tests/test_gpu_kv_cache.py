@@ -1,0 +1,178 @@
+"""GPU parity: paged KV write (bf16 copy, fused INT8 quantise) and the INT8/INT4 codec.
+
+Bar: bit-exact codes, fp16 scales and bf16 copies against oracle.codec / oracle.paged, and
+against the reference's codec lines (engine/kv_tier_manager.py:21-31) executed by torch on
+the same GPU.
+"""
+import numpy as np
+import pytest
+import torch
+
+import iitj_llm_coopt_amd as M
+from oracle import codec as OC
+from oracle import paged as OP
+
+pytestmark = pytest.mark.gpu
+
+
+def report(msg):
+    print(msg, flush=True)
+
+
+def bf16_kv(gen, T, H, D, dev, outlier=0.01):
+    x = torch.randn(T, H, D, generator=gen, device=dev)
+    mask = torch.rand(T, H, D, generator=gen, device=dev) < outlier
+    return torch.where(mask, x * 20, x).to(torch.bfloat16)
+
+
+def reference_quantize_on_device(x, bits):
+    """engine/kv_tier_manager.py:21-31, run by torch on the GPU."""
+    qmax = 127 if bits == 8 else 7
+    scale = x.abs().amax(-1, keepdim=True).float().clamp_min(1e-8) / qmax
+    q = torch.round(x.float() / scale).clamp(-qmax, qmax).to(torch.int8)
+    if bits == 4:
+        q = q + 8
+        q = (q[..., 0::2] | (q[..., 1::2] << 4)).to(torch.uint8)
+    return q, scale.squeeze(-1).to(torch.float16)
+
+
+def test_kv_write_bf16_contiguous_and_block_major_view(dev):
+    """tests/kv_write_check.py: fused write == index_put, and no other layer is touched."""
+    gen = torch.Generator(device=dev).manual_seed(0)
+    NB, L, BS, H, D, T = 64, 4, 16, 8, 128, 37
+    slots = torch.randperm(NB * BS, generator=gen, device=dev)[:T]
+    k = torch.randn(T, H, D, generator=gen, device=dev).to(torch.bfloat16)
+    v = torch.randn(T, H, D, generator=gen, device=dev).to(torch.bfloat16)
+    for strided in (False, True):
+        if strided:
+            buf = torch.zeros(NB, L, 2, BS, H, D, device=dev, dtype=torch.bfloat16)
+            kc, vc = buf[:, 2, 0], buf[:, 2, 1]
+        else:
+            kc = torch.zeros(NB, BS, H, D, device=dev, dtype=torch.bfloat16)
+            vc = torch.zeros_like(kc)
+        ref_k, ref_v = kc.clone(), vc.clone()
+        ref_k[slots // BS, slots % BS] = k
+        ref_v[slots // BS, slots % BS] = v
+        M.reshape_and_cache_flash(k, v, kc, vc, slots, "auto", None, None)
+        torch.cuda.synchronize()
+        assert torch.equal(kc, ref_k) and torch.equal(vc, ref_v)
+        if strided:
+            others = torch.cat([buf[:, l] for l in range(L) if l != 2])
+            assert bool((others == 0).all())
+
+
+def test_kv_write_from_strided_qkv_slices_and_head_dim_64(dev):
+    gen = torch.Generator(device=dev).manual_seed(1)
+    T, H, Hkv, D, NB, BS = 50, 32, 8, 64, 40, 16
+    qkv = torch.randn(T, (H + 2 * Hkv) * D, generator=gen, device=dev).to(torch.bfloat16)
+    _, k, v = qkv.split([H * D, Hkv * D, Hkv * D], dim=-1)
+    k, v = k.view(T, Hkv, D), v.view(T, Hkv, D)  # non-contiguous views, as in the model
+    slots = torch.randperm(NB * BS, generator=gen, device=dev)[:T]
+    kc = torch.zeros(NB, BS, Hkv, D, device=dev, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    M.reshape_and_cache_flash(k, v, kc, vc, slots, "auto")
+    assert torch.equal(kc[slots // BS, slots % BS], k) and torch.equal(vc[slots // BS, slots % BS], v)
+
+
+def test_kv_write_skips_padding_and_out_of_pool_slots(dev):
+    NB, BS, H, D = 8, 16, 8, 128
+    k = torch.ones(4, H, D, device=dev, dtype=torch.bfloat16)
+    slots = torch.tensor([-1, 5, NB * BS, 7], device=dev)
+    for mode in ("auto", "int8"):
+        kc, vc, ks, vs = M.allocate_kv_cache(NB, BS, H, D, mode, device=dev)
+        M.reshape_and_cache_flash(k, k, kc, vc, slots, mode, ks, vs)
+        written = kc.view(NB * BS, H * D).ne(0).any(1).nonzero().flatten().tolist()
+        assert written == [5, 7], (mode, written)
+
+
+def test_kv_write_int8_config2_bit_exact(dev):
+    """Config 2: Hkv 8, D 128, bs 16, 256 sequences x 5 new tokens, N(0,1) with 1% x20
+    outliers, slots from a seeded random free-block list of a 65,536-block pool."""
+    NB, BS, Hkv, D, nseq, new = 65536, 16, 8, 128, 256, 5
+    rng = np.random.default_rng(2)
+    bm = M.BlockManager(NB, BS, free_order=rng.permutation(NB))
+    existing = rng.integers(0, 4096, nseq)
+    slots = []
+    for s in range(nseq):
+        bm.ensure(s, int(existing[s]) + new)
+        slots.append(bm.slot_mapping(s, int(existing[s]), int(existing[s]) + new).numpy())
+    slots = torch.from_numpy(np.concatenate(slots)).to(dev)
+    T = slots.numel()
+    gen = torch.Generator(device=dev).manual_seed(2)
+    k, v = bf16_kv(gen, T, Hkv, D, dev), bf16_kv(gen, T, Hkv, D, dev)
+    kc, vc, ks, vs = M.allocate_kv_cache(NB, BS, Hkv, D, "int8", device=dev)
+    M.reshape_and_cache_flash(k, v, kc, vc, slots, "int8", ks, vs)
+    torch.cuda.synchronize()
+    blk, off = slots // BS, slots % BS
+    got = [x[blk, off] for x in (kc, vc, ks, vs)]
+    # vs the reference lines executed by torch on this GPU
+    rq_k, rs_k = reference_quantize_on_device(k, 8)
+    rq_v, rs_v = reference_quantize_on_device(v, 8)
+    assert torch.equal(got[0], rq_k) and torch.equal(got[1], rq_v)
+    assert torch.equal(got[2], rs_k) and torch.equal(got[3], rs_v)
+    # vs the CPU oracle
+    oq, osc = OC.quantize(k.float().cpu().numpy(), 8)
+    assert np.array_equal(got[0].cpu().numpy(), oq) and np.array_equal(got[2].cpu().numpy(), osc)
+    # nothing else in the pool was written
+    assert int((kc != 0).sum()) == int((got[0] != 0).sum())
+    report(f"[kv-int8] T={T}: codes+scales bit-exact vs torch-on-GPU and oracle")
+
+
+def test_kv_write_int8_edge_vectors(dev):
+    """zeros -> scale 0 and codes 0; amax 127 -> scale exactly 1 and .5 ties to even;
+    a single x20 outlier crushes the rest; |x| = amax -> +-127."""
+    H, D = 4, 128
+    x = torch.zeros(1, H, D, dtype=torch.float32)
+    x[0, 1, 0] = 127.0
+    x[0, 1, 1:8] = torch.tensor([0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5])
+    x[0, 2, :] = 0.01
+    x[0, 2, 9] = -50.0
+    x[0, 3] = torch.linspace(-3, 3, D)
+    xb = x.to(torch.bfloat16).to(dev)
+    kc, vc, ks, vs = M.allocate_kv_cache(2, 16, H, D, "int8", device=dev)
+    M.reshape_and_cache_flash(xb, xb, kc, vc, torch.tensor([3], device=dev), "int8", ks, vs)
+    codes, scales = kc[0, 3].cpu(), ks[0, 3].cpu()
+    oq, osc = OC.quantize(xb.float().cpu().numpy()[0], 8)
+    assert np.array_equal(codes.numpy(), oq) and np.array_equal(scales.numpy(), osc)
+    assert (codes[0] == 0).all() and scales[0] == 0
+    assert codes[1, :8].tolist() == [127, 0, 2, 2, 0, -2, -2, 126] and scales[1] == 1.0
+    assert codes[2, 9] == -127 and (codes[2, :9] == 0).all()
+    assert codes[3, 0] == -127 and codes[3, -1] == 127
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_codec_round_trip_bit_exact(dev, bits, dtype):
+    gen = torch.Generator(device=dev).manual_seed(3)
+    x = bf16_kv(gen, 333, 8, 128, dev).to(dtype)
+    q, s = M.quantize(x, bits)
+    rq, rs = reference_quantize_on_device(x, bits)
+    assert torch.equal(q, rq) and torch.equal(s, rs)
+    oq, osc = OC.quantize(x.float().cpu().numpy(), bits)
+    assert np.array_equal(q.cpu().numpy(), oq) and np.array_equal(s.cpu().numpy(), osc)
+    for out_dtype in (torch.bfloat16, torch.float32):
+        y = M.dequantize(q, s, bits, out_dtype)
+        ref = (OC.dequantize(oq, osc, bits))
+        ref = torch.from_numpy(ref).to(out_dtype)
+        assert torch.equal(y.cpu(), ref)
+
+
+def test_codec_bits16_is_passthrough(dev):
+    x = torch.randn(3, 128, device=dev).to(torch.bfloat16)
+    q, s = M.quantize(x, 16)
+    assert s is None and torch.equal(q, x) and q.data_ptr() != x.data_ptr()
+    assert M.dequantize(q, None, 16) is q
+
+
+def test_swap_round_trip_of_paged_blocks(dev):
+    """engine/kv_tier_manager.py:99,119 and eval/quality.py:51-52: quantize(cache[blocks])
+    then cache[blocks] = dequantize(...) equals the oracle's round trip."""
+    gen = torch.Generator(device=dev).manual_seed(4)
+    cache = bf16_kv(gen, 64 * 16, 8, 128, dev).view(64, 16, 8, 128)
+    blocks = torch.tensor([3, 17, 5, 40], device=dev)
+    for bits in (8, 4):
+        q, s = M.quantize(cache[blocks], bits)
+        back = M.dequantize(q, s, bits, torch.bfloat16)
+        oq, osc = OC.quantize(cache[blocks].float().cpu().numpy(), bits)
+        ref = OC.bf16_round(OC.dequantize(oq, osc, bits))
+        assert np.array_equal(back.float().cpu().numpy(), ref)

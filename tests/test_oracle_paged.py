@@ -1,0 +1,176 @@
+"""CPU: host-side paged-KV contract (product BlockManager / build_batch) and oracle.paged.
+
+The block-manager tests port tests/test_units.py:19-37 of the reference; the attention tests
+pin the oracle with closed forms and a brute-force loop.
+"""
+import numpy as np
+import pytest
+import torch
+
+from iitj_llm_coopt_amd import BlockManager, OutOfBlocks, WorkItem, build_batch, build_padded_batch
+from oracle import paged
+
+
+# ---- reference known-answer tests (tests/test_units.py:19-37) ---------------------------------
+def test_alloc_slots_truncate_free():
+    bm = BlockManager(num_blocks=8, block_size=16)
+    bm.ensure(1, 20)
+    assert len(bm.tables[1]) == 2 and bm.num_free == 6
+    b0, b1 = bm.tables[1]
+    assert bm.slot_mapping(1, 14, 18).tolist() == [b0 * 16 + 14, b0 * 16 + 15, b1 * 16, b1 * 16 + 1]
+    bm.ensure(1, 33)
+    bm.truncate(1, 16)
+    assert len(bm.tables[1]) == 1 and bm.num_free == 7
+    assert bm.free(1) == 1 and bm.num_free == 8
+
+
+def test_out_of_blocks():
+    bm = BlockManager(num_blocks=2, block_size=16)
+    bm.ensure(1, 32)
+    assert not bm.can_fit(2, 1)
+    with pytest.raises(OutOfBlocks):
+        bm.ensure(2, 1)
+
+
+# ---- slot mapping / block tables vs the closed form -------------------------------------------
+def test_slot_mapping_matches_closed_form_on_permuted_pool():
+    rng = np.random.default_rng(0)
+    order = rng.permutation(4096)
+    bm = BlockManager(4096, 16, free_order=order)
+    lens = rng.integers(1, 900, size=40)
+    for s, n in enumerate(lens):
+        bm.ensure(s, int(n))
+    for s, n in enumerate(lens):
+        a, b = sorted(rng.integers(0, int(n) + 1, size=2))
+        got = bm.slot_mapping(s, int(a), int(b)).numpy()
+        assert np.array_equal(got, paged.slot_mapping(bm.tables[s], int(a), int(b), 16))
+    # blocks come out in the given order and no block is handed out twice
+    flat = [b for s in range(len(lens)) for b in bm.tables[s]]
+    assert flat == list(order[:len(flat)]) and len(set(flat)) == len(flat)
+    bt = bm.block_table_tensor(list(range(len(lens)))).numpy()
+    assert np.array_equal(bt, paged.block_table([bm.tables[s] for s in range(len(lens))]))
+
+
+def test_free_order_must_be_a_permutation():
+    with pytest.raises(ValueError):
+        BlockManager(4, 16, free_order=[0, 1, 1, 2])
+
+
+def test_build_batch_layout_for_verify_items():
+    bm = BlockManager(64, 16)
+    items = [WorkItem(0, [5, 6, 7], 30, all_logits=True), WorkItem(1, [9], 3),
+             WorkItem(2, list(range(20)), 0)]
+    batch, spans = build_batch(items, bm, device="cpu")
+    assert batch.cu_seqlens_q.tolist() == [0, 3, 4, 24]
+    assert batch.seq_lens.tolist() == [33, 4, 20]
+    assert batch.positions[:4].tolist() == [30, 31, 32, 3]
+    assert batch.logits_indices.tolist() == [0, 1, 2, 3, 23]
+    assert spans == [(0, 3), (3, 1), (4, 1)]
+    assert batch.max_seqlen_q == 20 and batch.max_seqlen_k == 33
+    exp = np.concatenate([paged.slot_mapping(bm.tables[0], 30, 33, 16),
+                          paged.slot_mapping(bm.tables[1], 3, 4, 16),
+                          paged.slot_mapping(bm.tables[2], 0, 20, 16)])
+    assert np.array_equal(batch.slot_mapping.numpy(), exp)
+    assert batch.block_table.dtype == torch.int32 and batch.cu_seqlens_q.dtype == torch.int32
+
+
+def test_padded_layout_semantics():
+    """engine/cuda_graphs.py:7-16: rows i*S.., seq_len = start + S, padding -> scratch slot."""
+    bm = BlockManager(64, 16)
+    scratch = 63 * 16
+    items = [WorkItem(0, [1, 2], 10, all_logits=True), WorkItem(1, [3], 40)]
+    batch, spans = build_padded_batch(items, bm, stride=5, batch_size=4, width=8,
+                                      scratch_slot=scratch, device="cpu")
+    assert batch.cu_seqlens_q.tolist() == [0, 5, 10, 15, 20]
+    assert batch.seq_lens.tolist() == [15, 45, 5, 5]
+    sm = batch.slot_mapping.numpy()
+    assert (sm[2:5] == scratch).all() and (sm[6:] == scratch).all()
+    assert sm[0] == paged.slot_mapping(bm.tables[0], 10, 11, 16)[0]
+    assert batch.positions[:5].tolist() == [10, 11, 12, 13, 14]
+    assert spans == [(0, 2), (5, 1)]
+
+
+# ---- oracle attention -------------------------------------------------------------------------
+def _random_paged(rng, B, Hq, Hkv, D, lens, qlens, bs=16, nb=None):
+    nb = nb or sum(-(-L // bs) for L in lens) + 3
+    kc = rng.standard_normal((nb, bs, Hkv, D)).astype(np.float32)
+    vc = rng.standard_normal((nb, bs, Hkv, D)).astype(np.float32)
+    perm = rng.permutation(nb)
+    tables, o = [], 0
+    for L in lens:
+        nbk = -(-L // bs)
+        tables.append(list(perm[o:o + nbk]))
+        o += nbk
+    cu = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
+    q = rng.standard_normal((int(cu[-1]), Hq, D)).astype(np.float32)
+    return q, kc, vc, cu, np.asarray(lens, np.int32), paged.block_table(tables)
+
+
+def test_attention_matches_brute_force_loop():
+    rng = np.random.default_rng(3)
+    Hq, Hkv, D = 8, 2, 16
+    lens, qlens = [37, 5, 70], [1, 3, 5]
+    q, kc, vc, cu, sl, bt = _random_paged(rng, 3, Hq, Hkv, D, lens, qlens)
+    out = paged.attention(q, kc, vc, cu, sl, bt, 16, scale=0.3)
+    for b in range(3):
+        n, L = qlens[b], lens[b]
+        K = paged.gather(kc, bt[b], L, 16)
+        V = paged.gather(vc, bt[b], L, 16)
+        for j in range(n):
+            t = cu[b] + j
+            for h in range(Hq):
+                kv = h // (Hq // Hkv)
+                vis = L - n + j + 1
+                s = [0.3 * float(np.dot(q[t, h].astype(np.float64), K[i, kv].astype(np.float64)))
+                     for i in range(vis)]
+                m = max(s)
+                w = [np.exp(x - m) for x in s]
+                ref = sum(wi * V[i, kv].astype(np.float64) for i, wi in enumerate(w)) / sum(w)
+                assert np.allclose(out[t, h], ref, atol=1e-9)
+
+
+def test_attention_single_visible_key_returns_that_value():
+    rng = np.random.default_rng(4)
+    q, kc, vc, cu, sl, bt = _random_paged(rng, 1, 4, 1, 8, [1], [1])
+    out = paged.attention(q, kc, vc, cu, sl, bt, 16)
+    assert np.allclose(out[0, :], vc[bt[0][0], 0, 0][None, :])
+
+
+def test_attention_equal_scores_average_the_visible_values():
+    rng = np.random.default_rng(5)
+    q, kc, vc, cu, sl, bt = _random_paged(rng, 1, 2, 1, 8, [20], [4])
+    q[:] = 0.0  # all scores equal -> uniform weights over the causal window
+    out = paged.attention(q, kc, vc, cu, sl, bt, 16)
+    V = paged.gather(vc, bt[0], 20, 16)[:, 0]
+    for j in range(4):
+        assert np.allclose(out[j, 0], V[: 20 - 4 + j + 1].mean(0))
+
+
+def test_strided_block_major_view_equals_contiguous():
+    """tests/strided_kv_check.py: a per-layer view of [NB, L, 2, bs, H, D] reads the same."""
+    rng = np.random.default_rng(6)
+    NB, Lyr, bs, Hkv, Hq, D = 64, 4, 16, 8, 32, 32
+    buf = rng.standard_normal((NB, Lyr, 2, bs, Hkv, D)).astype(np.float32)
+    ks, vs = buf[:, 2, 0], buf[:, 2, 1]
+    lens, qlens = [37, 200, 5], [1, 3, 5]
+    cu = np.array([0, 1, 4, 9], np.int32)
+    bt = rng.permutation(NB)[:48].reshape(3, 16).astype(np.int32)
+    q = rng.standard_normal((9, Hq, D)).astype(np.float32)
+    a = paged.attention(q, np.ascontiguousarray(ks), np.ascontiguousarray(vs), cu, lens, bt, bs)
+    b = paged.attention(q, ks, vs, cu, lens, bt, bs)
+    assert np.array_equal(a, b)
+
+
+def test_kv_write_index_put_and_no_leak_into_other_layers():
+    rng = np.random.default_rng(7)
+    NB, Lyr, bs, H, D, T = 64, 4, 16, 8, 16, 37
+    buf = np.zeros((NB, Lyr, 2, bs, H, D), np.float32)
+    kc, vc = buf[:, 2, 0], buf[:, 2, 1]
+    slots = rng.permutation(NB * bs)[:T]
+    k = rng.standard_normal((T, H, D)).astype(np.float32)
+    v = rng.standard_normal((T, H, D)).astype(np.float32)
+    paged.kv_write(kc, vc, k, v, slots, bs)
+    assert np.array_equal(kc[slots // bs, slots % bs], k)
+    assert np.array_equal(vc[slots // bs, slots % bs], v)
+    others = np.concatenate([buf[:, l] for l in range(Lyr) if l != 2])
+    assert (others == 0).all()
