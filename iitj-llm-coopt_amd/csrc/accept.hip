@@ -96,8 +96,10 @@ __host__ __device__ inline size_t carve(Workspace* w, uintptr_t base, int B, int
     off += align256(bytes);
     return p;
   };
-  w->cnt1 = reinterpret_cast<unsigned*>(take(sizeof(unsigned) * B));
-  w->cnt2 = reinterpret_cast<unsigned*>(take(sizeof(unsigned) * B));
+  // two counters per sequence inside the fixed counter region (B <= kMaxCounters / 2)
+  w->cnt1 = reinterpret_cast<unsigned*>(base);
+  w->cnt2 = reinterpret_cast<unsigned*>(base + kCounterRegionBytes / 2);
+  off = kCounterRegionBytes;
   w->part1 = reinterpret_cast<Partial1*>(take(sizeof(Partial1) * B * slots * L.nch1));
   w->rows = reinterpret_cast<RowStat*>(take(sizeof(RowStat) * B * slots));
   w->dec = reinterpret_cast<Decision*>(take(sizeof(Decision) * B));
@@ -643,6 +645,7 @@ extern "C" int coopt_accept_sample(int logits_dtype, const void* target, int64_t
   COOPT_REQUIRE(logits_dtype == COOPT_DT_F32 || logits_dtype == COOPT_DT_BF16,
                 "logits_dtype must be F32 or BF16");
   COOPT_REQUIRE(B >= 0 && gamma_max >= 0 && gamma_max <= 64 && V > 0, "bad sizes");
+  COOPT_REQUIRE(B <= kMaxCounters / 2, "B must be <= 65536");
   if (B == 0) return COOPT_OK;
   const bool greedy = !(temperature > 0.0f);
   COOPT_REQUIRE(target && accepted_len && out_tokens && workspace, "null pointer");

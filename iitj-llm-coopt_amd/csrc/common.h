@@ -93,6 +93,13 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
   return v;
 }
 
+// Every workspace starts with a fixed 512 KiB region of completion counters (128Ki uint32),
+// whatever the call's shape; kernels leave them at zero.  Scratch data always lives after it,
+// so calls of different shapes can share one workspace without a counter ever landing on
+// another call's scratch bytes.
+constexpr size_t kCounterRegionBytes = 512 * 1024;
+constexpr int kMaxCounters = static_cast<int>(kCounterRegionBytes / sizeof(unsigned));
+
 // Device-scope atomics used by the "last block finishes the reduction" pattern.
 __device__ __forceinline__ unsigned atomic_add_acq_rel(unsigned* p, unsigned v) {
   return __hip_atomic_fetch_add(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);

@@ -19,8 +19,10 @@
 //           A = V^T: d = l%16, the same 8 keys, read from the LDS copy of the V tile.
 //   Every lane's accumulators therefore belong to a single query row, so the online-softmax
 //   rescale is a per-lane scalar.
-// INT8 KV: codes are widened to bf16 exactly (|code| <= 127); the per-token K scale multiplies
-// the score, the per-token V scale multiplies P before it is rounded to bf16.
+// INT8 KV: every code is dequantised to bf16(float(code) * scale) -- the values the reference
+// attends over after dequantize(quantize(KV)) (eval/quality.py:48-52) -- K in registers as it
+// is loaded, V before it is staged in LDS, so the MFMA stages are those of the bf16 path and
+// the INT8 result equals the bf16 kernel run on the dequantised cache.
 #include <math.h>
 
 #include "common.h"
@@ -67,26 +69,22 @@ __device__ __forceinline__ f32x4_t mfma_bf16(u32x4_t a, u32x4_t b, f32x4_t c) {
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> packed bf16x2, round to nearest even (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
 }
 
-// int8 code -> bf16 bits (exact for |code| <= 255).
-__device__ __forceinline__ uint32_t i8_to_bf16_bits(int c) {
-  return __float_as_uint(static_cast<float>(c)) >> 16;
-}
-
-__device__ __forceinline__ u32x4_t widen_i8x8(u32x2_t w) {
-  u32x4_t r;
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const uint32_t word = w[p / 2];
-    const int sh = (p & 1) * 16;
-    const int c0 = static_cast<int8_t>((word >> sh) & 0xff);
-    const int c1 = static_cast<int8_t>((word >> (sh + 8)) & 0xff);
-    r[p] = i8_to_bf16_bits(c0) | (i8_to_bf16_bits(c1) << 16);
-  }
-  return r;
+// Four int8 codes of one word -> bf16(float(code) * scale), as dequantize(q, s, 8, bf16)
+// computes them (engine/kv_tier_manager.py:41): the fp32 product is exact, then one RNE.
+__device__ __forceinline__ u32x2_t dequant4(uint32_t w, float sc) {
+  const float c0 = static_cast<float>(static_cast<int8_t>(w & 0xff));
+  const float c1 = static_cast<float>(static_cast<int8_t>((w >> 8) & 0xff));
+  const float c2 = static_cast<float>(static_cast<int8_t>((w >> 16) & 0xff));
+  const float c3 = static_cast<float>(static_cast<int8_t>(w >> 24));
+  return u32x2_t{pack_bf16x2(c0 * sc, c1 * sc), pack_bf16x2(c2 * sc, c3 * sc)};
 }
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -103,9 +101,9 @@ struct Tile {
   static constexpr int kChunkElems = 16 / kElt;        // elements per 16-byte chunk
   static constexpr int kChunksPerKey = D / kChunkElems;
   static constexpr int kVLoads = kTileKeys * kChunksPerKey / 64;  // 16-byte V loads per lane
-  // LDS pitch of one staged V row (bytes): padded so the transposed reads of four key groups
-  // land in different banks.
-  static constexpr int kPitch = INT8 ? D + 4 : 2 * D + 8;
+  // LDS pitch of one staged (bf16) V row in bytes: padded so the transposed reads of the
+  // four key groups land in different banks.
+  static constexpr int kPitch = 2 * D + 8;
   static constexpr int kWaveLds = kTileKeys * kPitch;
 };
 
@@ -181,19 +179,24 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void verify_attn_kerne
   for (int tile = wave; tile < ntiles; tile += kWaves) {
     const int kb = k_begin + tile * kTileKeys;
 
-    // K operand: lane's key for each 16-key sub-tile, 8 d values per k-step.
+    // K operand: lane's key for each 16-key sub-tile, 8 d values per k-step (INT8: the
+    // codes dequantised to bf16 with that key's scale).
     u32x4_t kreg[2][TL::kKs];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
       const int key = min(kb + kt * 16 + l16, L - 1);
       const int64_t page = clamp_page(table[key >> a.bs_shift], a.num_blocks);
-      const int64_t row = page * a.c_bs + static_cast<int64_t>(key & bs_mask) * a.c_ts +
-                          static_cast<int64_t>(hkv) * a.c_hs;
+      const int64_t tok = static_cast<int64_t>(key & bs_mask);
+      const int64_t row = page * a.c_bs + tok * a.c_ts + static_cast<int64_t>(hkv) * a.c_hs;
+      float ksc = 0.0f;
+      if constexpr (INT8) ksc = f16_to_f32(a.ks[page * a.s_bs + tok * a.s_ts + hkv * a.s_hs]);
 #pragma unroll
       for (int ks = 0; ks < TL::kKs; ++ks) {
         const int64_t e = row + ks * 32 + grp * 8;
         if constexpr (INT8) {
-          kreg[kt][ks] = widen_i8x8(*reinterpret_cast<const u32x2_t*>(kbase + e));
+          const u32x2_t w = *reinterpret_cast<const u32x2_t*>(kbase + e);
+          const u32x2_t lo = dequant4(w[0], ksc), hi = dequant4(w[1], ksc);
+          kreg[kt][ks] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
         } else {
           kreg[kt][ks] = *reinterpret_cast<const u32x4_t*>(kbase + 2 * e);
         }
@@ -201,31 +204,18 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void verify_attn_kerne
     }
     // V tile: coalesced 16-byte chunks, staged through LDS below.
     u32x4_t vreg[TL::kVLoads];
+    float vsc[TL::kVLoads];
 #pragma unroll
     for (int it = 0; it < TL::kVLoads; ++it) {
       const int id = it * 64 + lane;
       const int kk = id / TL::kChunksPerKey, c = id % TL::kChunksPerKey;
       const int key = min(kb + kk, L - 1);
       const int64_t page = clamp_page(table[key >> a.bs_shift], a.num_blocks);
-      const int64_t row = page * a.c_bs + static_cast<int64_t>(key & bs_mask) * a.c_ts +
-                          static_cast<int64_t>(hkv) * a.c_hs;
+      const int64_t tok = static_cast<int64_t>(key & bs_mask);
+      const int64_t row = page * a.c_bs + tok * a.c_ts + static_cast<int64_t>(hkv) * a.c_hs;
       vreg[it] = *reinterpret_cast<const u32x4_t*>(vbase + TL::kElt * row + c * 16);
-    }
-    // Per-token scales of the keys this lane's score registers hold (INT8 only).
-    float ksc[2][4], vsc[2][4];
-    if constexpr (INT8) {
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = min(kb + kt * 16 + grp * 4 + i, L - 1);
-          const int64_t page = clamp_page(table[key >> a.bs_shift], a.num_blocks);
-          const int64_t so = page * a.s_bs + static_cast<int64_t>(key & bs_mask) * a.s_ts +
-                             static_cast<int64_t>(hkv) * a.s_hs;
-          ksc[kt][i] = f16_to_f32(a.ks[so]);
-          vsc[kt][i] = f16_to_f32(a.vs[so]);
-        }
-      }
+      vsc[it] = 0.0f;
+      if constexpr (INT8) vsc[it] = f16_to_f32(a.vs[page * a.s_bs + tok * a.s_ts + hkv * a.s_hs]);
     }
 
     // ---- scores and online softmax ----
@@ -241,8 +231,7 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void verify_attn_kerne
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int key = kb + kt * 16 + grp * 4 + i;
-          float s = acc[i] * a.scale_log2;
-          if constexpr (INT8) s *= ksc[kt][i];
+          const float s = acc[i] * a.scale_log2;
           sv[kt][i] = (key > lim[rt] || key >= k_end) ? -INFINITY : s;
         }
       }
@@ -265,12 +254,6 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void verify_attn_kerne
       m_run[rt] = m_new;
 #pragma unroll
       for (int dt = 0; dt < TL::kDt; ++dt) o[rt][dt] *= alpha;
-      if constexpr (INT8) {
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) p[kt][i] *= vsc[kt][i];
-      }
       pb[rt][0] = pack_bf16x2(p[0][0], p[0][1]);
       pb[rt][1] = pack_bf16x2(p[0][2], p[0][3]);
       pb[rt][2] = pack_bf16x2(p[1][0], p[1][1]);
@@ -282,13 +265,11 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void verify_attn_kerne
     for (int it = 0; it < TL::kVLoads; ++it) {
       const int id = it * 64 + lane;
       const int kk = id / TL::kChunksPerKey, c = id % TL::kChunksPerKey;
-      unsigned char* dst = stage + kk * TL::kPitch + c * 16;
+      unsigned char* dst = stage + kk * TL::kPitch + c * 2 * TL::kChunkElems;
       if constexpr (INT8) {
-        uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
-        d32[0] = vreg[it][0];
-        d32[1] = vreg[it][1];
-        d32[2] = vreg[it][2];
-        d32[3] = vreg[it][3];
+        u32x2_t* d64 = reinterpret_cast<u32x2_t*>(dst);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) d64[w] = dequant4(vreg[it][w], vsc[it]);
       } else {
         u32x2_t* d64 = reinterpret_cast<u32x2_t*>(dst);
         d64[0] = u32x2_t{vreg[it][0], vreg[it][1]};
@@ -311,12 +292,7 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void verify_attn_kerne
         for (int h = 0; h < 2; ++h) {
           const int e = e2 * 2 + h;
           const int kk = e < 4 ? grp * 4 + e : 16 + grp * 4 + (e - 4);
-          if constexpr (INT8) {
-            const int c = static_cast<int8_t>(stage[kk * TL::kPitch + d]);
-            half[h] = i8_to_bf16_bits(c);
-          } else {
-            half[h] = *reinterpret_cast<const uint16_t*>(stage + kk * TL::kPitch + 2 * d);
-          }
+          half[h] = *reinterpret_cast<const uint16_t*>(stage + kk * TL::kPitch + 2 * d);
         }
         va[e2] = half[0] | (half[1] << 16);
       }
@@ -471,7 +447,7 @@ AttnWs attn_ws_layout(int B, int Hkv, int D, int rmax, int max_splits) {
   AttnWs w;
   const size_t items = static_cast<size_t>(B) * Hkv;
   w.cnt_off = 0;
-  w.ml_off = al(items * sizeof(unsigned));
+  w.ml_off = kCounterRegionBytes;
   w.o_off = w.ml_off + al(items * max_splits * rmax * sizeof(float2));
   w.total = w.o_off + al(items * max_splits * rmax * static_cast<size_t>(D) * sizeof(float));
   return w;
@@ -523,6 +499,7 @@ extern "C" int coopt_verify_attention(int kv_dtype, const void* q, int64_t q_tok
   COOPT_REQUIRE(max_seqlen_q > 0 && max_seqlen_k > 0, "max_seqlen_q/k must be positive");
   const int G = Hq / Hkv;
   COOPT_REQUIRE(G * max_seqlen_q <= 64, "(Hq/Hkv) * max_seqlen_q must be <= 64");
+  COOPT_REQUIRE(static_cast<int64_t>(B) * Hkv <= kMaxCounters, "B * Hkv must be <= 131072");
   COOPT_REQUIRE(bt_stride >= (max_seqlen_k + block_size - 1) / block_size,
                 "block_table narrower than ceil(max_seqlen_k / block_size)");
   if (B == 0) return COOPT_OK;
