@@ -119,10 +119,9 @@ def require_cuda(*tensors):
 
 
 class WorkspaceCache:
-    """Zero-filled device workspaces, grown on demand and reused (kernels leave them zeroed).
-
-    One buffer per (device, stream): calls that overlap in time must not share a workspace.
-    """
+    """Device scratch buffers, grown on demand and reused (the kernels need no initialised
+    workspace).  One buffer per (device, stream): calls that overlap in time must not share
+    a workspace, and stream order keeps calls on one stream from overlapping."""
 
     def __init__(self):
         self._bufs = {}
@@ -132,6 +131,6 @@ class WorkspaceCache:
         key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
         buf = self._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
-            buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=dev)
+            buf = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=dev)
             self._bufs[key] = buf
         return buf

@@ -1,22 +1,26 @@
 // Fused speculative acceptance: vocab-wide softmax of target and draft rows, the p/q accept
 // test, first rejection, the max(0, p - q) residual and inverse-CDF resampling, for a whole
-// batch in two launches.  Semantics: engine/spec_decode.py:20-49 (sampling) and :30-35
-// (greedy), looped over the batch at engine/engine.py:421-446, with the uniforms explicit.
+// batch.  Semantics: engine/spec_decode.py:20-49 (sampling) and :30-35 (greedy), looped over
+// the batch at engine/engine.py:421-446, with the uniforms explicit.
 //
-// Launch 1 (row_stats_kernel), grid (chunk, row slot, sequence): every block reduces one
-// chunk of one row -- max and an fp64 sum of exp(x/T - max) (sampling), or max and first
-// argmax (greedy).  The last block to finish for a sequence (device-scope counter) combines
-// the chunk partials into row statistics and runs the accept loop, which needs only the
-// logits at the draft tokens; it writes the accepted prefix and the decision (k, which
-// distribution to resample from).
-// Launch 2 (resample_kernel), grid (chunk, sequence): partial fp64 sums of the resampling
-// weights w_j; the last block of a sequence locates the chunk where the cumulative weight
-// crosses u * sum(w), scans that chunk and writes the emitted token.
+// Launches (each reads what the previous one wrote; no cross-block fences or counters):
+//   1. row_stats_kernel, grid (chunk, row slot, sequence): one chunk of one row per block --
+//      max of x/T and an fp64 sum of exp(x/T - max) (sampling), or max and first argmax
+//      (greedy).  Full chunks are read with unconditional 16-byte loads, all issued before use.
+//   2. greedy_kernel, grid (sequence): combines the argmax partials and applies the prefix
+//      rule.  -- or, sampling --
+//      decide_kernel, grid (chunk, sequence): every block combines its sequence's row
+//      statistics and runs the accept loop (it needs only the logits at the draft tokens),
+//      then sums the resampling weights w_j of its chunk; block 0 of each sequence publishes
+//      the accepted prefix and the decision.
+//   3. select_kernel, grid (sequence): finds the chunk where the cumulative weight crosses
+//      u * sum(w), scans it and writes the emitted token.
 //
-// Numerics.  Row maxima are exact; sum(exp) is accumulated in fp64 from fp32 expf terms; the
-// probabilities at the draft tokens are formed in fp64 and rounded once to fp32, so p_i[d_i]
-// and q_i[d_i] agree with an exactly rounded fp32 softmax except within an ulp of a rounding
-// boundary.  Cumulative weights are fp64 sums of fp32 w_j.
+// Numerics.  Row maxima are exact and sum(exp) is accumulated in fp64.  The probabilities at
+// the draft tokens, which decide acceptance, are formed with an fp64 exp and rounded once to
+// fp32, so p_i[d_i] / q_i[d_i] agree with an exactly rounded fp32 softmax except within an
+// ulp of a rounding boundary.  The vocab-wide terms use exp2(fma(x, log2 e, -max log2 e))
+// (relative error < 1e-6); cumulative weights are fp64 sums of fp32 w_j.
 #include <math.h>
 
 #include "common.h"
@@ -24,9 +28,11 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kMaxPerThread = 64;                  // elements a phase-1 thread keeps in VGPRs
+constexpr int kMaxPerThread = 64;                    // elements a phase-1 thread keeps in VGPRs
 constexpr int kMaxChunk = kThreads * kMaxPerThread;  // 16384
 constexpr int kMinChunk = 1024;
+constexpr int kMaxSlots = 2 * 64 + 1;                // 2 * gamma_max + 1 rows per sequence
+constexpr float kLog2e = 1.4426950408889634f;
 
 enum : int { kModeResidual = 0, kModeBonus = 1 };
 
@@ -45,6 +51,7 @@ struct Decision {
   int mode;
   float margin;
   int pad;
+  RowStat rt, rq;  // statistics of the target / draft row the token is drawn from
 };
 struct Partial2 {
   double w;  // sum of resampling weights over the chunk
@@ -60,7 +67,7 @@ __host__ __device__ inline int imax(int a, int b) { return a > b ? a : b; }
 __host__ __device__ inline int imin(int a, int b) { return a < b ? a : b; }
 
 // Chunking is a pure function of (B, gamma_max, V) so the workspace size can be computed
-// without the data.
+// without the data.  Chunks are multiples of 8 elements; at most kThreads resampling chunks.
 __host__ __device__ inline Layout make_layout(int B, int gmax, int V) {
   Layout L;
   const int rows = B * (2 * gmax + 1);
@@ -70,19 +77,16 @@ __host__ __device__ inline Layout make_layout(int B, int gmax, int V) {
   L.chunk1 = ceil_div(ceil_div(V, nch), 8) * 8;
   L.nch1 = ceil_div(V, L.chunk1);
   int nch2 = ceil_div(1024, B > 0 ? B : 1);
-  nch2 = imax(1, imin(nch2, ceil_div(V, kMinChunk)));
+  nch2 = imax(1, imin(nch2, imin(kThreads, ceil_div(V, kMinChunk))));
   L.chunk2 = ceil_div(ceil_div(V, nch2), 8) * 8;
   L.nch2 = ceil_div(V, L.chunk2);
   return L;
 }
 
 struct Workspace {
-  unsigned* cnt1;    // [B]
-  unsigned* cnt2;    // [B]
-  Partial1* part1;   // [B][2*gmax+1][nch1]
-  RowStat* rows;     // [B][2*gmax+1]
-  Decision* dec;     // [B]
-  Partial2* part2;   // [B][nch2]
+  Partial1* part1;  // [B][2*gmax+1][nch1]
+  Decision* dec;    // [B]
+  Partial2* part2;  // [B][nch2]
 };
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
@@ -96,12 +100,7 @@ __host__ __device__ inline size_t carve(Workspace* w, uintptr_t base, int B, int
     off += align256(bytes);
     return p;
   };
-  // two counters per sequence inside the fixed counter region (B <= kMaxCounters / 2)
-  w->cnt1 = reinterpret_cast<unsigned*>(base);
-  w->cnt2 = reinterpret_cast<unsigned*>(base + kCounterRegionBytes / 2);
-  off = kCounterRegionBytes;
   w->part1 = reinterpret_cast<Partial1*>(take(sizeof(Partial1) * B * slots * L.nch1));
-  w->rows = reinterpret_cast<RowStat*>(take(sizeof(RowStat) * B * slots));
   w->dec = reinterpret_cast<Decision*>(take(sizeof(Decision) * B));
   w->part2 = reinterpret_cast<Partial2*>(take(sizeof(Partial2) * B * L.nch2));
   return off;
@@ -122,8 +121,8 @@ struct Args {
   int32_t* out_tok;
   float* margin;
   float inv_t;
-  int greedy;
   int draft_probs;
+  int vec_t, vec_d;  // rows may be read with 16-byte loads
   int B, gmax, V;
   Layout L;
   Workspace ws;
@@ -148,36 +147,22 @@ __device__ __forceinline__ float ld(const void* base, int64_t row, int64_t strid
   }
 }
 
-// Loads elements [lo, hi) of a row into vals[], thread-strided in groups of 4 (fp32) or 8
-// (bf16) consecutive elements so that every wave instruction reads one contiguous span.
+// Loads 8 consecutive elements starting at j (16 bytes of bf16, or two 16-byte fp32 loads).
 template <bool BF16>
-__device__ __forceinline__ void load_chunk(const void* base, int64_t row, int64_t stride, int lo,
-                                           int hi, bool vec_ok, float (&vals)[kMaxPerThread]) {
-  constexpr int W = BF16 ? 8 : 4;
-  const int tid = threadIdx.x;
+__device__ __forceinline__ void ld8(const void* base, int64_t row, int64_t stride, int j, float* v) {
+  if constexpr (BF16) {
+    const uint4 r = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + row * stride + j);
+    const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
-  for (int it = 0; it < kMaxPerThread / W; ++it) {
-    const int j0 = lo + (it * kThreads + tid) * W;
-    if (vec_ok && j0 + W <= hi) {
-      if constexpr (BF16) {
-        const uint4 r = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + row * stride + j0);
-        const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) vals[it * W + e] = bf16_to_f32(static_cast<uint16_t>(w4[e / 2] >> (16 * (e & 1))));
-      } else {
-        const float4 r = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + row * stride + j0);
-        vals[it * W + 0] = r.x;
-        vals[it * W + 1] = r.y;
-        vals[it * W + 2] = r.z;
-        vals[it * W + 3] = r.w;
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < W; ++e) {
-        const int j = j0 + e;
-        vals[it * W + e] = j < hi ? ld<BF16>(base, row, stride, j) : -INFINITY;
-      }
+    for (int e = 0; e < 4; ++e) {
+      v[2 * e] = __uint_as_float(w4[e] << 16);
+      v[2 * e + 1] = __uint_as_float(w4[e] & 0xffff0000u);
     }
+  } else {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + row * stride + j);
+    const float4 r0 = p[0], r1 = p[1];
+    v[0] = r0.x; v[1] = r0.y; v[2] = r0.z; v[3] = r0.w;
+    v[4] = r1.x; v[5] = r1.y; v[6] = r1.z; v[7] = r1.w;
   }
 }
 
@@ -187,7 +172,7 @@ __device__ __forceinline__ float block_max(float v, float* sh) {
   const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) sh[w] = v;
   __syncthreads();
-  float r = fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+  const float r = fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
   __syncthreads();
   return r;
 }
@@ -196,7 +181,7 @@ __device__ __forceinline__ double block_sum(double v, double* sh) {
   const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) sh[w] = v;
   __syncthreads();
-  double r = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+  const double r = (sh[0] + sh[1]) + (sh[2] + sh[3]);
   __syncthreads();
   return r;
 }
@@ -209,153 +194,73 @@ __device__ __forceinline__ void amax_merge(float& v, int& i, float ov, int oi) {
   }
 }
 
+// exp(x - m) for the vocab-wide terms: one fma and v_exp_f32.
+__device__ __forceinline__ float exp_shift(float x, float m_l2) {
+  return __builtin_amdgcn_exp2f(fmaf(x, kLog2e, -m_l2));
+}
+
 // Accurate p = exp(x' - m) / s rounded once to fp32 (x' = fl32(x * inv_t)).
 __device__ __forceinline__ float prob_at(float xs, float m, double s) {
   return static_cast<float>(exp(static_cast<double>(xs) - static_cast<double>(m)) / s);
 }
 
-template <bool BF16>
-__device__ void finalize_sequence(const Args& a, int b) {
-  const int g = gamma_of(a, b);
-  const int slots = 2 * a.gmax + 1;
-  const int nrow_t = g + 1;
-  const int nrow_d = (a.greedy || a.draft_probs) ? 0 : g;
-  const int tid = threadIdx.x;
-  // Combine chunk partials into row statistics, one thread per row, in chunk order.
-  if (tid < nrow_t + nrow_d) {
-    const int slot = tid < nrow_t ? tid : (a.gmax + 1) + (tid - nrow_t);
-    const Partial1* p = a.ws.part1 + (static_cast<int64_t>(b) * slots + slot) * a.L.nch1;
-    RowStat rs;
-    if (a.greedy) {
-      float v = -INFINITY;
-      int idx = 0x7fffffff;
-      for (int c = 0; c < a.L.nch1; ++c) {
-        const float pv = load_agent(&p[c].m);
-        const int pi = load_agent(&p[c].idx);
-        amax_merge(v, idx, pv, pi);
-      }
-      rs.m = v;
-      rs.argmax = idx;
-      rs.s = 0.0;
-    } else {
-      float m = -INFINITY;
-      for (int c = 0; c < a.L.nch1; ++c) m = fmaxf(m, load_agent(&p[c].m));
-      double s = 0.0;
-      for (int c = 0; c < a.L.nch1; ++c) {
-        const float pm = load_agent(&p[c].m);
-        const double ps = load_agent(&p[c].s);
-        if (ps > 0.0) s += ps * exp(static_cast<double>(pm) - static_cast<double>(m));
-      }
-      rs.m = m;
-      rs.argmax = -1;
-      rs.s = s;
-    }
-    a.ws.rows[static_cast<int64_t>(b) * slots + slot] = rs;
-  }
-  __syncthreads();
-  __threadfence_block();
-  if (tid != 0) return;
-
-  const RowStat* rows = a.ws.rows + static_cast<int64_t>(b) * slots;
-  const int32_t* d = a.dtok + static_cast<int64_t>(b) * a.gmax;
-  int32_t* out = a.out_tok + static_cast<int64_t>(b) * (a.gmax + 1);
-  int k = g;
-  float margin = INFINITY;
-  if (a.greedy) {
-    for (int i = 0; i < g; ++i) {
-      if (rows[i].argmax != d[i]) {
-        k = i;
-        break;
-      }
-    }
-    for (int i = 0; i < k; ++i) out[i] = d[i];
-    out[k] = rows[k].argmax;
-    for (int i = k + 1; i <= a.gmax; ++i) out[i] = -1;
-    a.acc_len[b] = k;
-    if (a.margin) a.margin[b] = INFINITY;
-    return;
-  }
-  const float* u = a.u_acc + static_cast<int64_t>(b) * a.gmax;
-  int mode = kModeBonus;
-  for (int i = 0; i < g; ++i) {
-    const int tok = d[i];
-    float ratio = 0.0f;
-    if (tok >= 0 && tok < a.V) {
-      const float xt = ld<BF16>(a.tgt, tgt_row(a, b, i), a.tgt_stride, tok) * a.inv_t;
-      const float p = prob_at(xt, rows[i].m, rows[i].s);
-      float q;
-      if (a.draft_probs) {
-        q = static_cast<const float*>(a.drf)[drf_row(a, b, i) * a.drf_stride + tok];
-      } else {
-        const float xq = ld<BF16>(a.drf, drf_row(a, b, i), a.drf_stride, tok) * a.inv_t;
-        const RowStat& rq = rows[a.gmax + 1 + i];
-        q = prob_at(xq, rq.m, rq.s);
-      }
-      ratio = fminf(p / fmaxf(q, 1e-20f), 1.0f);
-    }
-    margin = fminf(margin, fabsf(u[i] - ratio));
-    if (u[i] >= ratio) {
-      k = i;
-      mode = kModeResidual;
-      break;
-    }
-  }
-  for (int i = 0; i < k; ++i) out[i] = d[i];
-  for (int i = k + 1; i <= a.gmax; ++i) out[i] = -1;
-  a.acc_len[b] = k;
-  Decision dec;
-  dec.k = k;
-  dec.mode = mode;
-  dec.margin = margin;
-  dec.pad = 0;
-  a.ws.dec[b] = dec;
-}
-
-template <bool BF16>
+// ---------------------------------------------------------------------------------------
+// Launch 1: per-chunk row statistics.
+// ---------------------------------------------------------------------------------------
+template <bool BF16, bool GREEDY>
 __global__ __launch_bounds__(kThreads) void row_stats_kernel(Args a) {
   __shared__ float shf[4];
   __shared__ double shd[4];
   __shared__ float shv[4];
   __shared__ int shi[4];
-  __shared__ int last;
   const int c = blockIdx.x, slot = blockIdx.y, b = blockIdx.z;
   const int g = gamma_of(a, b);
   const bool is_draft = slot > a.gmax;
   const int i = is_draft ? slot - a.gmax - 1 : slot;
   if (!is_draft && i > g) return;
-  if (is_draft && (a.greedy || a.draft_probs || i >= g)) return;
+  if (is_draft && (GREEDY || a.draft_probs || i >= g)) return;
 
   const void* base = is_draft ? a.drf : a.tgt;
   const int64_t stride = is_draft ? a.drf_stride : a.tgt_stride;
   const int64_t row = is_draft ? drf_row(a, b, i) : tgt_row(a, b, i);
   const int lo = c * a.L.chunk1;
   const int hi = min(a.V, lo + a.L.chunk1);
-  constexpr int W = BF16 ? 8 : 4;
-  const bool vec_ok = (stride % W == 0) &&
-                      ((reinterpret_cast<uintptr_t>(base) & (BF16 ? 15u : 15u)) == 0);
+  const int tid = threadIdx.x;
+  // Element (it, e) of this thread is lo + (it * kThreads + tid) * 8 + e.  Chunks are
+  // multiples of 8, so in a full chunk a group is either wholly inside or wholly past hi.
+  const bool full = (is_draft ? a.vec_d : a.vec_t) != 0 && hi - lo == a.L.chunk1;
   float vals[kMaxPerThread];
-  load_chunk<BF16>(base, row, stride, lo, hi, vec_ok, vals);
+#pragma unroll
+  for (int it = 0; it < kMaxPerThread / 8; ++it) {
+    const int j0 = lo + (it * kThreads + tid) * 8;
+    if (full && j0 < hi) {
+      ld8<BF16>(base, row, stride, j0, vals + it * 8);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        vals[it * 8 + e] = (j0 + e < hi) ? ld<BF16>(base, row, stride, j0 + e) : -INFINITY;
+    }
+  }
 
   Partial1 part;
-  if (a.greedy) {
+  if constexpr (GREEDY) {
     float v = -INFINITY;
     int idx = 0x7fffffff;
 #pragma unroll
-    for (int it = 0; it < kMaxPerThread / W; ++it) {
+    for (int it = 0; it < kMaxPerThread / 8; ++it)
 #pragma unroll
-      for (int e = 0; e < W; ++e) {
-        const int j = lo + (it * kThreads + static_cast<int>(threadIdx.x)) * W + e;
-        if (j < hi) amax_merge(v, idx, vals[it * W + e], j);
+      for (int e = 0; e < 8; ++e) {
+        const int j = lo + (it * kThreads + tid) * 8 + e;
+        if (j < hi) amax_merge(v, idx, vals[it * 8 + e], j);
       }
-    }
 #pragma unroll
     for (int m = 1; m < 64; m <<= 1) {
       const float ov = __shfl_xor(v, m, 64);
       const int oi = __shfl_xor(idx, m, 64);
       amax_merge(v, idx, ov, oi);
     }
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) {
+    const int w = tid >> 6;
+    if ((tid & 63) == 0) {
       shv[w] = v;
       shi[w] = idx;
     }
@@ -376,50 +281,234 @@ __global__ __launch_bounds__(kThreads) void row_stats_kernel(Args a) {
     m = block_max(m, shf);
     double s = 0.0;
     if (m > -INFINITY) {
+      const float m_l2 = m * kLog2e;
 #pragma unroll
-      for (int e = 0; e < kMaxPerThread; ++e) s += static_cast<double>(expf(vals[e] - m));
+      for (int it = 0; it < kMaxPerThread / 8; ++it) {
+        float acc = 0.0f;  // 8 terms <= 1 each in fp32, then fp64
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc += exp_shift(vals[it * 8 + e], m_l2);
+        s += static_cast<double>(acc);
+      }
     }
     s = block_sum(s, shd);
     part.m = m;
     part.idx = -1;
     part.s = s;
   }
-
-  const int slots = 2 * a.gmax + 1;
-  if (threadIdx.x == 0) {
-    a.ws.part1[(static_cast<int64_t>(b) * slots + slot) * a.L.nch1 + c] = part;
-    const int nrows = (g + 1) + ((a.greedy || a.draft_probs) ? 0 : g);
-    const unsigned expected = static_cast<unsigned>(nrows * a.L.nch1);
-    __threadfence();
-    const unsigned prev = atomic_add_acq_rel(&a.ws.cnt1[b], 1u);
-    last = (prev == expected - 1);
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  finalize_sequence<BF16>(a, b);
-  if (threadIdx.x == 0) atomic_store_relaxed(&a.ws.cnt1[b], 0u);
+  if (tid == 0) a.ws.part1[(static_cast<int64_t>(b) * (2 * a.gmax + 1) + slot) * a.L.nch1 + c] = part;
 }
 
-// Resampling weight of element j (bit-identical wherever it is evaluated).
-template <bool BF16>
-__device__ __forceinline__ void weight_at(const Args& a, int64_t trow, int64_t drow, int j,
-                                          const RowStat& rt, const RowStat& rq, int mode,
-                                          float& w, float& p) {
-  const float xt = ld<BF16>(a.tgt, trow, a.tgt_stride, j) * a.inv_t;
-  p = static_cast<float>(static_cast<double>(expf(xt - rt.m)) / rt.s);
-  if (mode == kModeBonus) {
-    w = p;
-    return;
-  }
-  float q;
-  if (a.draft_probs) {
-    q = static_cast<const float*>(a.drf)[drow * a.drf_stride + j];
+// Combines the chunk partials of row slot `slot` of sequence b (chunk order).
+__device__ __forceinline__ RowStat combine_row(const Args& a, int b, int slot, bool greedy) {
+  const Partial1* p = a.ws.part1 + (static_cast<int64_t>(b) * (2 * a.gmax + 1) + slot) * a.L.nch1;
+  RowStat rs;
+  if (greedy) {
+    float v = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int c = 0; c < a.L.nch1; ++c) amax_merge(v, idx, p[c].m, p[c].idx);
+    rs.m = v;
+    rs.argmax = idx;
+    rs.s = 0.0;
   } else {
-    const float xq = ld<BF16>(a.drf, drow, a.drf_stride, j) * a.inv_t;
-    q = static_cast<float>(static_cast<double>(expf(xq - rq.m)) / rq.s);
+    float m = -INFINITY;
+    for (int c = 0; c < a.L.nch1; ++c) m = fmaxf(m, p[c].m);
+    double s = 0.0;
+    for (int c = 0; c < a.L.nch1; ++c) {
+      const Partial1 q = p[c];
+      if (q.s > 0.0) s += q.s * exp(static_cast<double>(q.m) - static_cast<double>(m));
+    }
+    rs.m = m;
+    rs.argmax = -1;
+    rs.s = s;
   }
-  w = fmaxf(p - q, 0.0f);
+  return rs;
+}
+
+// ---------------------------------------------------------------------------------------
+// Launch 2 (greedy): argmax prefix rule, one block per sequence.
+// ---------------------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void greedy_kernel(Args a) {
+  __shared__ int argm[kMaxSlots];
+  const int b = blockIdx.x;
+  const int g = gamma_of(a, b);
+  if (static_cast<int>(threadIdx.x) <= g) argm[threadIdx.x] = combine_row(a, b, threadIdx.x, true).argmax;
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  const int32_t* d = a.dtok + static_cast<int64_t>(b) * a.gmax;
+  int32_t* out = a.out_tok + static_cast<int64_t>(b) * (a.gmax + 1);
+  int k = g;
+  for (int i = 0; i < g; ++i) {
+    if (argm[i] != d[i]) {
+      k = i;
+      break;
+    }
+  }
+  for (int i = 0; i < k; ++i) out[i] = d[i];
+  out[k] = argm[k];
+  for (int i = k + 1; i <= a.gmax; ++i) out[i] = -1;
+  a.acc_len[b] = k;
+  if (a.margin) a.margin[b] = INFINITY;
+}
+
+// Resampling weights of up to 8 elements j.. (bit-identical wherever evaluated).
+template <bool BF16>
+struct WeightRow {
+  const Args* a;
+  int64_t trow, drow;
+  int mode;
+  float mt_l2, mq_l2;
+  double inv_st, inv_sq;
+
+  __device__ __forceinline__ void at(int j, int n, bool vec, float* w, float* p) const {
+    float xt[8], xq[8];
+    if (vec) {
+      ld8<BF16>(a->tgt, trow, a->tgt_stride, j, xt);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xt[e] = e < n ? ld<BF16>(a->tgt, trow, a->tgt_stride, j + e) : -INFINITY;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      p[e] = static_cast<float>(static_cast<double>(exp_shift(xt[e] * a->inv_t, mt_l2)) * inv_st);
+    if (mode == kModeBonus) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) w[e] = p[e];
+      return;
+    }
+    float q[8];
+    if (a->draft_probs) {
+      const float* qr = static_cast<const float*>(a->drf) + drow * a->drf_stride;
+      if (vec) {
+        const float4 q0 = *reinterpret_cast<const float4*>(qr + j);
+        const float4 q1 = *reinterpret_cast<const float4*>(qr + j + 4);
+        q[0] = q0.x; q[1] = q0.y; q[2] = q0.z; q[3] = q0.w;
+        q[4] = q1.x; q[5] = q1.y; q[6] = q1.z; q[7] = q1.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q[e] = e < n ? qr[j + e] : 0.0f;
+      }
+    } else {
+      if (vec) {
+        ld8<BF16>(a->drf, drow, a->drf_stride, j, xq);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xq[e] = e < n ? ld<BF16>(a->drf, drow, a->drf_stride, j + e) : -INFINITY;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        q[e] = static_cast<float>(static_cast<double>(exp_shift(xq[e] * a->inv_t, mq_l2)) * inv_sq);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) w[e] = fmaxf(p[e] - q[e], 0.0f);
+  }
+};
+
+template <bool BF16>
+__device__ __forceinline__ WeightRow<BF16> make_weight_row(const Args& a, int b, const Decision& dec) {
+  WeightRow<BF16> wr;
+  wr.a = &a;
+  wr.mode = dec.mode;
+  wr.trow = tgt_row(a, b, dec.k);
+  wr.drow = dec.mode == kModeResidual ? drf_row(a, b, dec.k) : 0;
+  wr.mt_l2 = dec.rt.m * kLog2e;
+  wr.mq_l2 = dec.rq.m * kLog2e;
+  wr.inv_st = 1.0 / dec.rt.s;
+  wr.inv_sq = dec.mode == kModeResidual && !a.draft_probs ? 1.0 / dec.rq.s : 0.0;
+  return wr;
+}
+
+// ---------------------------------------------------------------------------------------
+// Launch 2 (sampling): accept decision (recomputed by every block of the sequence) and the
+// chunk sums of the resampling weights.
+// ---------------------------------------------------------------------------------------
+template <bool BF16>
+__global__ __launch_bounds__(kThreads) void decide_kernel(Args a) {
+  __shared__ RowStat rows[kMaxSlots];
+  __shared__ Decision sdec;
+  __shared__ double shd[4], shd2[4];
+  const int c = blockIdx.x, b = blockIdx.y;
+  const int g = gamma_of(a, b);
+  const int tid = threadIdx.x;
+  const int nrow_t = g + 1, nrow_d = a.draft_probs ? 0 : g;
+  if (tid < nrow_t + nrow_d) {
+    const int slot = tid < nrow_t ? tid : (a.gmax + 1) + (tid - nrow_t);
+    rows[slot] = combine_row(a, b, slot, false);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const int32_t* d = a.dtok + static_cast<int64_t>(b) * a.gmax;
+    const float* u = a.u_acc + static_cast<int64_t>(b) * a.gmax;
+    int k = g, mode = kModeBonus;
+    float margin = INFINITY;
+    for (int i = 0; i < g; ++i) {
+      const int tok = d[i];
+      float ratio = 0.0f;
+      if (tok >= 0 && tok < a.V) {
+        const float xt = ld<BF16>(a.tgt, tgt_row(a, b, i), a.tgt_stride, tok) * a.inv_t;
+        const float p = prob_at(xt, rows[i].m, rows[i].s);
+        float q;
+        if (a.draft_probs) {
+          q = static_cast<const float*>(a.drf)[drf_row(a, b, i) * a.drf_stride + tok];
+        } else {
+          const float xq = ld<BF16>(a.drf, drf_row(a, b, i), a.drf_stride, tok) * a.inv_t;
+          const RowStat& rq = rows[a.gmax + 1 + i];
+          q = prob_at(xq, rq.m, rq.s);
+        }
+        ratio = fminf(p / fmaxf(q, 1e-20f), 1.0f);
+      }
+      margin = fminf(margin, fabsf(u[i] - ratio));
+      if (u[i] >= ratio) {
+        k = i;
+        mode = kModeResidual;
+        break;
+      }
+    }
+    Decision dec;
+    dec.k = k;
+    dec.mode = mode;
+    dec.margin = margin;
+    dec.pad = 0;
+    dec.rt = rows[k];
+    dec.rq = (mode == kModeResidual && !a.draft_probs) ? rows[a.gmax + 1 + k] : rows[k];
+    sdec = dec;
+    if (c == 0) {
+      a.ws.dec[b] = dec;
+      int32_t* out = a.out_tok + static_cast<int64_t>(b) * (a.gmax + 1);
+      for (int i = 0; i < k; ++i) out[i] = d[i];
+      for (int i = k + 1; i <= a.gmax; ++i) out[i] = -1;
+      a.acc_len[b] = k;
+    }
+  }
+  __syncthreads();
+  const Decision dec = sdec;
+  const WeightRow<BF16> wr = make_weight_row<BF16>(a, b, dec);
+  const int lo = c * a.L.chunk2;
+  const int hi = min(a.V, lo + a.L.chunk2);
+  const bool vec = a.vec_t && (dec.mode == kModeBonus || a.vec_d);
+  double sw = 0.0, sp = 0.0;
+  for (int j = lo + tid * 8; j < hi; j += kThreads * 8) {
+    float w[8], p[8];
+    const int n = min(8, hi - j);
+    wr.at(j, n, vec && n == 8, w, p);
+    float fw = 0.0f, fp = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (e < n) {
+        fw += w[e];
+        fp += p[e];
+      }
+    }
+    sw += static_cast<double>(fw);
+    sp += static_cast<double>(fp);
+  }
+  sw = block_sum(sw, shd);
+  sp = block_sum(sp, shd2);
+  if (tid == 0) {
+    Partial2 pp;
+    pp.w = sw;
+    pp.p = sp;
+    a.ws.part2[static_cast<int64_t>(b) * a.L.nch2 + c] = pp;
+  }
 }
 
 // Inclusive block scan of one fp64 value per thread (4 waves).
@@ -438,67 +527,56 @@ __device__ __forceinline__ double block_inclusive_scan(double v, double* sh) {
   return off + v;
 }
 
+// ---------------------------------------------------------------------------------------
+// Launch 3 (sampling): inverse-CDF draw, one block per sequence.
+// ---------------------------------------------------------------------------------------
 template <bool BF16>
-__global__ __launch_bounds__(kThreads) void resample_kernel(Args a) {
+__global__ __launch_bounds__(kThreads) void select_kernel(Args a) {
   __shared__ double shd[4];
-  __shared__ double shd2[4];
-  __shared__ int last;
-  __shared__ int sh_chunk;
+  __shared__ double wave_last[4];
+  __shared__ int sh_chunk, sh_use_p, sh_tok_min;
   __shared__ double sh_acc, sh_tau, sh_total;
-  __shared__ int sh_use_p;
-  __shared__ int sh_tok_min;
   __shared__ float sh_margin;
-  const int c = blockIdx.x, b = blockIdx.y;
-  const int slots = 2 * a.gmax + 1;
+  __shared__ double csum[kThreads];
+  const int b = blockIdx.x, tid = threadIdx.x;
   const Decision dec = a.ws.dec[b];
-  const int k = dec.k;
-  const int mode = dec.mode;
-  const RowStat rt = a.ws.rows[static_cast<int64_t>(b) * slots + k];
-  RowStat rq = rt;
-  if (mode == kModeResidual && !a.draft_probs) rq = a.ws.rows[static_cast<int64_t>(b) * slots + a.gmax + 1 + k];
-  const int64_t trow = tgt_row(a, b, k);
-  const int64_t drow = mode == kModeResidual ? drf_row(a, b, k) : 0;
-
-  const int lo = c * a.L.chunk2;
-  const int hi = min(a.V, lo + a.L.chunk2);
-  double sw = 0.0, sp = 0.0;
-  for (int j = lo + threadIdx.x; j < hi; j += kThreads) {
-    float w, p;
-    weight_at<BF16>(a, trow, drow, j, rt, rq, mode, w, p);
-    sw += static_cast<double>(w);
-    sp += static_cast<double>(p);
+  const WeightRow<BF16> wr = make_weight_row<BF16>(a, b, dec);
+  const Partial2* P = a.ws.part2 + static_cast<int64_t>(b) * a.L.nch2;
+  double wv = 0.0, pv = 0.0;
+  if (tid < a.L.nch2) {  // nch2 <= kThreads by construction
+    wv = P[tid].w;
+    pv = P[tid].p;
   }
-  sw = block_sum(sw, shd);
-  sp = block_sum(sp, shd2);
-  if (threadIdx.x == 0) {
-    Partial2 pp;
-    pp.w = sw;
-    pp.p = sp;
-    a.ws.part2[static_cast<int64_t>(b) * a.L.nch2 + c] = pp;
-    __threadfence();
-    const unsigned prev = atomic_add_acq_rel(&a.ws.cnt2[b], 1u);
-    last = (prev == static_cast<unsigned>(a.L.nch2) - 1);
+  if (tid == 0) {
+    sh_tok_min = 0x7fffffff;
+    sh_margin = 0.0f;
+  }
+  csum[tid] = wv;
+  __syncthreads();
+  if (tid == 0) {
+    double total = 0.0;
+    for (int q = 0; q < a.L.nch2; ++q) total += csum[q];
+    // spec_decode.py:48: a residual that sums to zero falls back to p_k
+    sh_use_p = (dec.mode == kModeResidual && !(total > 0.0)) ? 1 : 0;
+    sh_total = total;
   }
   __syncthreads();
-  if (!last) return;
-  __threadfence();
-
-  // ---- last block of sequence b: locate the chunk, then the element ----
-  if (threadIdx.x == 0) {
-    const Partial2* P = a.ws.part2 + static_cast<int64_t>(b) * a.L.nch2;
-    double total = 0.0;
-    for (int q = 0; q < a.L.nch2; ++q) total += load_agent(&P[q].w);
-    int use_p = 0;
-    if (mode == kModeResidual && !(total > 0.0)) {
-      use_p = 1;  // residual sums to zero: fall back to p_k (engine/spec_decode.py:48)
+  const int use_p = sh_use_p;
+  if (use_p) {
+    csum[tid] = pv;
+    __syncthreads();
+  }
+  if (tid == 0) {
+    double total = sh_total;
+    if (use_p) {
       total = 0.0;
-      for (int q = 0; q < a.L.nch2; ++q) total += load_agent(&P[q].p);
+      for (int q = 0; q < a.L.nch2; ++q) total += csum[q];
     }
     const double tau = static_cast<double>(a.u_res[b]) * total;
     double acc = 0.0;
     int chunk = -1, last_nonzero = 0;
     for (int q = 0; q < a.L.nch2; ++q) {
-      const double sq = use_p ? load_agent(&P[q].p) : load_agent(&P[q].w);
+      const double sq = csum[q];
       if (sq > 0.0) last_nonzero = q;
       if (acc + sq > tau) {
         chunk = q;
@@ -509,46 +587,39 @@ __global__ __launch_bounds__(kThreads) void resample_kernel(Args a) {
     if (chunk < 0) {  // tau within rounding of the total: take the last chunk with mass
       chunk = last_nonzero;
       acc = 0.0;
-      for (int q = 0; q < chunk; ++q) acc += use_p ? load_agent(&P[q].p) : load_agent(&P[q].w);
+      for (int q = 0; q < chunk; ++q) acc += csum[q];
     }
     sh_chunk = chunk;
     sh_acc = acc;
     sh_tau = tau;
     sh_total = total;
-    sh_use_p = use_p;
-    sh_tok_min = 0x7fffffff;
-    sh_margin = 0.0f;
   }
   __syncthreads();
   const int chunk = sh_chunk;
   const double acc = sh_acc, tau = sh_tau, total = sh_total;
-  const int use_p = sh_use_p;
   const int clo = chunk * a.L.chunk2;
   const int chi = min(a.V, clo + a.L.chunk2);
-  const int per = (a.L.chunk2 + kThreads - 1) / kThreads;
-  const int tlo = min(chi, clo + static_cast<int>(threadIdx.x) * per);
-  const int thi = min(chi, tlo + per);
+  // each thread owns a contiguous run of 8-element groups of the chunk
+  const int groups = (chi - clo + 7) / 8;
+  const int per = (groups + kThreads - 1) / kThreads;
+  const int tlo = min(chi, clo + tid * per * 8);
+  const int thi = min(chi, tlo + per * 8);
+  const bool vec = a.vec_t && (dec.mode == kModeBonus || a.vec_d);
   double local = 0.0;
-  for (int j = tlo; j < thi; ++j) {
-    float w, p;
-    weight_at<BF16>(a, trow, drow, j, rt, rq, mode, w, p);
-    local += static_cast<double>(use_p ? p : w);
+  for (int j = tlo; j < thi; j += 8) {
+    float w[8], p[8];
+    const int n = min(8, thi - j);
+    wr.at(j, n, vec && n == 8, w, p);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (e < n) local += static_cast<double>(use_p ? p[e] : w[e]);
   }
   const double incl = block_inclusive_scan(local, shd);
-  // Thread t owns [acc + incl_{t-1}, acc + incl_t); incl_{t-1} is read from the neighbour so
-  // that exactly one thread claims tau.
+  // Thread t owns [acc + incl_{t-1}, acc + incl_t); incl_{t-1} comes from the neighbour.
   const double prev_incl = __shfl_up(incl, 1, 64);
-  __shared__ double wave_last[4];
-  if ((threadIdx.x & 63) == 63) wave_last[threadIdx.x >> 6] = incl;
+  if ((tid & 63) == 63) wave_last[tid >> 6] = incl;
   __syncthreads();
-  double start;
-  if (threadIdx.x == 0) {
-    start = 0.0;
-  } else if ((threadIdx.x & 63) == 0) {
-    start = wave_last[(threadIdx.x >> 6) - 1];
-  } else {
-    start = prev_incl;
-  }
+  const double start = tid == 0 ? 0.0 : ((tid & 63) == 0 ? wave_last[(tid >> 6) - 1] : prev_incl);
   const bool claim = (acc + start <= tau) && (tau < acc + incl) && (thi > tlo);
   int tok = -1;
   float mg = 0.0f;
@@ -556,19 +627,22 @@ __global__ __launch_bounds__(kThreads) void resample_kernel(Args a) {
     double run = acc + start;
     int last_pos = -1;
     double lo_edge = run, hi_edge = run;
-    for (int j = tlo; j < thi; ++j) {
-      float w, p;
-      weight_at<BF16>(a, trow, drow, j, rt, rq, mode, w, p);
-      const double wj = static_cast<double>(use_p ? p : w);
-      if (wj > 0.0) last_pos = j;
-      const double nxt = run + wj;
-      if (nxt > tau && wj > 0.0) {
-        tok = j;
-        lo_edge = run;
-        hi_edge = nxt;
-        break;
+    for (int j = tlo; j < thi && tok < 0; j += 8) {
+      float w[8], p[8];
+      const int n = min(8, thi - j);
+      wr.at(j, n, vec && n == 8, w, p);
+      for (int e = 0; e < n; ++e) {
+        const double wj = static_cast<double>(use_p ? p[e] : w[e]);
+        if (wj > 0.0) last_pos = j + e;
+        const double nxt = run + wj;
+        if (nxt > tau && wj > 0.0) {
+          tok = j + e;
+          lo_edge = run;
+          hi_edge = nxt;
+          break;
+        }
+        run = nxt;
       }
-      run = nxt;
     }
     if (tok < 0) {
       tok = last_pos >= 0 ? last_pos : tlo;
@@ -582,24 +656,20 @@ __global__ __launch_bounds__(kThreads) void resample_kernel(Args a) {
   __syncthreads();
   if (claim && tok == sh_tok_min) sh_margin = mg;
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     int pick = sh_tok_min == 0x7fffffff ? -1 : sh_tok_min;
     float pick_margin = sh_margin;
-    if (pick < 0) {  // no thread claimed (rounding at the chunk end): last element with mass
-      for (int j = chi - 1; j >= clo; --j) {
-        float w, p;
-        weight_at<BF16>(a, trow, drow, j, rt, rq, mode, w, p);
-        if ((use_p ? p : w) > 0.0f) {
-          pick = j;
-          break;
-        }
+    if (pick < 0) {  // nobody claimed (rounding at the chunk end): last element with mass
+      for (int j = chi - 1; j >= clo && pick < 0; --j) {
+        float w[8], p[8];
+        wr.at(j, 1, false, w, p);
+        if ((use_p ? p[0] : w[0]) > 0.0f) pick = j;
       }
       if (pick < 0) pick = clo;
       pick_margin = 0.0f;
     }
-    a.out_tok[static_cast<int64_t>(b) * (a.gmax + 1) + k] = pick;
+    a.out_tok[static_cast<int64_t>(b) * (a.gmax + 1) + dec.k] = pick;
     if (a.margin) a.margin[b] = fminf(dec.margin, pick_margin);
-    atomic_store_relaxed(&a.ws.cnt2[b], 0u);
   }
 }
 
@@ -614,14 +684,36 @@ __global__ __launch_bounds__(kThreads) void softmax_kernel(const void* x, int64_
   float m = -INFINITY;
   for (int j = threadIdx.x; j < V; j += kThreads) m = fmaxf(m, ld<BF16>(x, r, in_stride, j) * inv_t);
   m = block_max(m, shf);
+  const float m_l2 = m * kLog2e;
   double s = 0.0;
   for (int j = threadIdx.x; j < V; j += kThreads)
-    s += static_cast<double>(expf(ld<BF16>(x, r, in_stride, j) * inv_t - m));
+    s += static_cast<double>(exp_shift(ld<BF16>(x, r, in_stride, j) * inv_t, m_l2));
   s = block_sum(s, shd);
+  const double inv_s = 1.0 / s;
   for (int j = threadIdx.x; j < V; j += kThreads) {
     const float xs = ld<BF16>(x, r, in_stride, j) * inv_t;
-    out[r * out_stride + j] = static_cast<float>(static_cast<double>(expf(xs - m)) / s);
+    out[r * out_stride + j] = static_cast<float>(static_cast<double>(exp_shift(xs, m_l2)) * inv_s);
   }
+}
+
+template <bool BF16>
+int launch_all(Args& a, bool greedy, hipStream_t s) {
+  const dim3 g1(a.L.nch1, 2 * a.gmax + 1, a.B);
+  if (greedy)
+    hipLaunchKernelGGL((row_stats_kernel<BF16, true>), g1, dim3(kThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL((row_stats_kernel<BF16, false>), g1, dim3(kThreads), 0, s, a);
+  int rc = coopt::check_launch("coopt_accept_sample/row_stats");
+  if (rc != COOPT_OK) return rc;
+  if (greedy) {
+    hipLaunchKernelGGL(greedy_kernel, dim3(a.B), dim3(kThreads), 0, s, a);
+    return coopt::check_launch("coopt_accept_sample/greedy");
+  }
+  hipLaunchKernelGGL((decide_kernel<BF16>), dim3(a.L.nch2, a.B), dim3(kThreads), 0, s, a);
+  rc = coopt::check_launch("coopt_accept_sample/decide");
+  if (rc != COOPT_OK) return rc;
+  hipLaunchKernelGGL((select_kernel<BF16>), dim3(a.B), dim3(kThreads), 0, s, a);
+  return coopt::check_launch("coopt_accept_sample/select");
 }
 
 }  // namespace
@@ -645,7 +737,7 @@ extern "C" int coopt_accept_sample(int logits_dtype, const void* target, int64_t
   COOPT_REQUIRE(logits_dtype == COOPT_DT_F32 || logits_dtype == COOPT_DT_BF16,
                 "logits_dtype must be F32 or BF16");
   COOPT_REQUIRE(B >= 0 && gamma_max >= 0 && gamma_max <= 64 && V > 0, "bad sizes");
-  COOPT_REQUIRE(B <= kMaxCounters / 2, "B must be <= 65536");
+  COOPT_REQUIRE(B <= 65535, "B must be <= 65535");
   if (B == 0) return COOPT_OK;
   const bool greedy = !(temperature > 0.0f);
   COOPT_REQUIRE(target && accepted_len && out_tokens && workspace, "null pointer");
@@ -665,6 +757,7 @@ extern "C" int coopt_accept_sample(int logits_dtype, const void* target, int64_t
     return COOPT_EWORKSPACE;
   }
   coopt::clear_error();
+  const bool bf16 = logits_dtype == COOPT_DT_BF16;
   Args a{};
   a.tgt = target;
   a.tgt_stride = target_row_stride;
@@ -681,28 +774,18 @@ extern "C" int coopt_accept_sample(int logits_dtype, const void* target, int64_t
   a.margin = margin;
   // torch's GPU path evaluates "logits / T" as logits * fp32(1/T).
   a.inv_t = greedy ? 1.0f : 1.0f / temperature;
-  a.greedy = greedy ? 1 : 0;
   a.draft_probs = (draft_kind == 1) ? 1 : 0;
+  // 16-byte loads need 16-byte aligned rows (stride a multiple of 8 bf16 / 4 fp32 elements).
+  a.vec_t = coopt::aligned16(target) && target_row_stride % (bf16 ? 8 : 4) == 0;
+  const int dq = (bf16 && draft_kind == 0) ? 8 : 4;
+  a.vec_d = draft != nullptr && coopt::aligned16(draft) && draft_row_stride % dq == 0;
   a.B = B;
   a.gmax = gamma_max;
   a.V = V;
   a.L = make_layout(B, gamma_max, V);
   carve(&a.ws, reinterpret_cast<uintptr_t>(workspace), B, gamma_max, a.L);
   auto s = static_cast<hipStream_t>(stream);
-  const bool bf16 = logits_dtype == COOPT_DT_BF16;
-  const dim3 g1(a.L.nch1, 2 * gamma_max + 1, B);
-  if (bf16)
-    hipLaunchKernelGGL(row_stats_kernel<true>, g1, dim3(kThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL(row_stats_kernel<false>, g1, dim3(kThreads), 0, s, a);
-  int rc = coopt::check_launch("coopt_accept_sample/row_stats");
-  if (rc != COOPT_OK || greedy) return rc;
-  const dim3 g2(a.L.nch2, B);
-  if (bf16)
-    hipLaunchKernelGGL(resample_kernel<true>, g2, dim3(kThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL(resample_kernel<false>, g2, dim3(kThreads), 0, s, a);
-  return coopt::check_launch("coopt_accept_sample/resample");
+  return bf16 ? launch_all<true>(a, greedy, s) : launch_all<false>(a, greedy, s);
 }
 
 extern "C" int coopt_softmax(int logits_dtype, const void* logits, int64_t in_stride, int64_t rows,

@@ -92,22 +92,3 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
   for (int m = 1; m < COOPT_WAVE; m <<= 1) v += __shfl_xor(v, m, COOPT_WAVE);
   return v;
 }
-
-// Every workspace starts with a fixed 512 KiB region of completion counters (128Ki uint32),
-// whatever the call's shape; kernels leave them at zero.  Scratch data always lives after it,
-// so calls of different shapes can share one workspace without a counter ever landing on
-// another call's scratch bytes.
-constexpr size_t kCounterRegionBytes = 512 * 1024;
-constexpr int kMaxCounters = static_cast<int>(kCounterRegionBytes / sizeof(unsigned));
-
-// Device-scope atomics used by the "last block finishes the reduction" pattern.
-__device__ __forceinline__ unsigned atomic_add_acq_rel(unsigned* p, unsigned v) {
-  return __hip_atomic_fetch_add(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void atomic_store_relaxed(unsigned* p, unsigned v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <typename T>
-__device__ __forceinline__ T load_agent(const T* p) {
-  return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}

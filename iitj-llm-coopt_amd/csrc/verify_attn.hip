@@ -59,7 +59,6 @@ struct AttnArgs {
   uint16_t* out;
   int64_t o_ts, o_hs;
   int split, max_splits, rmax;
-  unsigned* cnt;
   float2* part_ml;
   float* part_o;
 };
@@ -122,7 +121,6 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void verify_attn_kerne
   __shared__ float sm_l[kWaves][kRows];
   __shared__ float sm_M[kRows];
   __shared__ float sm_L[kRows];
-  __shared__ int sm_last;
 
   const int b = blockIdx.z, hkv = blockIdx.y, sidx = blockIdx.x;
   const int q0 = a.cu[b];
@@ -137,7 +135,8 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void verify_attn_kerne
   const int k_begin = sidx * a.split;
   const int k_end = min(L, k_begin + a.split);
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = lane >> 4, l16 = lane & 15;
+  const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, l16 = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int bs_mask = (1 << a.bs_shift) - 1;
   const int32_t* table = a.bt + static_cast<int64_t>(b) * a.bt_stride;
 
@@ -175,32 +174,51 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void verify_attn_kerne
   const int ntiles = (k_end - k_begin + kTileKeys - 1) / kTileKeys;
   const unsigned char* kbase = static_cast<const unsigned char*>(a.kc);
   const unsigned char* vbase = static_cast<const unsigned char*>(a.vc);
+  const int64_t head_off = static_cast<int64_t>(hkv) * a.c_hs;
+  const int64_t shead_off = static_cast<int64_t>(hkv) * a.s_hs;
 
+  // `wave` is uniform, so the tile loop and the two page lookups per tile are scalar.  A
+  // 32-key tile starts on a multiple of 32 and block_size >= 16, so its keys lie in at most
+  // two pages: the one holding key kb and the one holding key kb + 16 (keys past the end are
+  // clamped to L - 1, which stays in the page of its 16-key half).  The page ids of the
+  // wave's next tile are fetched one iteration ahead.
+  auto page_of = [&](int key) {
+    return clamp_page(table[min(key, L - 1) >> a.bs_shift], a.num_blocks);
+  };
+  int64_t nxt0 = 0, nxt1 = 0;
+  if (wave < ntiles) {
+    nxt0 = page_of(k_begin + wave * kTileKeys);
+    nxt1 = page_of(k_begin + wave * kTileKeys + 16);
+  }
   for (int tile = wave; tile < ntiles; tile += kWaves) {
     const int kb = k_begin + tile * kTileKeys;
+    const int64_t pg0 = nxt0, pg1 = nxt1;
+    if (tile + kWaves < ntiles) {
+      nxt0 = page_of(kb + kWaves * kTileKeys);
+      nxt1 = page_of(kb + kWaves * kTileKeys + 16);
+    }
 
-    // K operand: lane's key for each 16-key sub-tile, 8 d values per k-step (INT8: the
-    // codes dequantised to bf16 with that key's scale).
-    u32x4_t kreg[2][TL::kKs];
+    // ---- issue every load of the tile before using any of them ----
+    // K operand: lane's key for each 16-key sub-tile, 8 d values per k-step.
+    u32x4_t kraw[2][TL::kKs];
+    u32x2_t kraw8[2][TL::kKs];
+    float ksc[2] = {0.0f, 0.0f};
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
       const int key = min(kb + kt * 16 + l16, L - 1);
-      const int64_t page = clamp_page(table[key >> a.bs_shift], a.num_blocks);
       const int64_t tok = static_cast<int64_t>(key & bs_mask);
-      const int64_t row = page * a.c_bs + tok * a.c_ts + static_cast<int64_t>(hkv) * a.c_hs;
-      float ksc = 0.0f;
-      if constexpr (INT8) ksc = f16_to_f32(a.ks[page * a.s_bs + tok * a.s_ts + hkv * a.s_hs]);
+      const int64_t pg = kt ? pg1 : pg0;
+      const int64_t row = pg * a.c_bs + tok * a.c_ts + head_off;
 #pragma unroll
       for (int ks = 0; ks < TL::kKs; ++ks) {
         const int64_t e = row + ks * 32 + grp * 8;
         if constexpr (INT8) {
-          const u32x2_t w = *reinterpret_cast<const u32x2_t*>(kbase + e);
-          const u32x2_t lo = dequant4(w[0], ksc), hi = dequant4(w[1], ksc);
-          kreg[kt][ks] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+          kraw8[kt][ks] = *reinterpret_cast<const u32x2_t*>(kbase + e);
         } else {
-          kreg[kt][ks] = *reinterpret_cast<const u32x4_t*>(kbase + 2 * e);
+          kraw[kt][ks] = *reinterpret_cast<const u32x4_t*>(kbase + 2 * e);
         }
       }
+      if constexpr (INT8) ksc[kt] = f16_to_f32(a.ks[pg * a.s_bs + tok * a.s_ts + shead_off]);
     }
     // V tile: coalesced 16-byte chunks, staged through LDS below.
     u32x4_t vreg[TL::kVLoads];
@@ -210,13 +228,29 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void verify_attn_kerne
       const int id = it * 64 + lane;
       const int kk = id / TL::kChunksPerKey, c = id % TL::kChunksPerKey;
       const int key = min(kb + kk, L - 1);
-      const int64_t page = clamp_page(table[key >> a.bs_shift], a.num_blocks);
       const int64_t tok = static_cast<int64_t>(key & bs_mask);
-      const int64_t row = page * a.c_bs + tok * a.c_ts + static_cast<int64_t>(hkv) * a.c_hs;
+      const int64_t pg = kk < 16 ? pg0 : pg1;
+      const int64_t row = pg * a.c_bs + tok * a.c_ts + head_off;
       vreg[it] = *reinterpret_cast<const u32x4_t*>(vbase + TL::kElt * row + c * 16);
       vsc[it] = 0.0f;
-      if constexpr (INT8) vsc[it] = f16_to_f32(a.vs[page * a.s_bs + tok * a.s_ts + hkv * a.s_hs]);
+      if constexpr (INT8) vsc[it] = f16_to_f32(a.vs[pg * a.s_bs + tok * a.s_ts + shead_off]);
     }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // K to bf16 MFMA operands (INT8: dequantised with the lane's key scale).
+    u32x4_t kreg[2][TL::kKs];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int ks = 0; ks < TL::kKs; ++ks) {
+        if constexpr (INT8) {
+          const u32x2_t lo = dequant4(kraw8[kt][ks][0], ksc[kt]);
+          const u32x2_t hi = dequant4(kraw8[kt][ks][1], ksc[kt]);
+          kreg[kt][ks] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+        } else {
+          kreg[kt][ks] = kraw[kt][ks];
+        }
+      }
 
     // ---- scores and online softmax ----
     uint32_t pb[RT][4];
@@ -375,7 +409,7 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void verify_attn_kerne
     return;
   }
 
-  // ---- several splits: publish this split's partial, the last one merges ----
+  // ---- several splits: publish this split's partial; merge_kernel combines them ----
   const int64_t pbase = (item * a.max_splits + sidx) * a.rmax;
   for (int idx = tid; idx < R * kCh; idx += kThreads) {
     const int r = idx / kCh, c = idx % kCh;
@@ -385,46 +419,47 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void verify_attn_kerne
     reinterpret_cast<f32x4_t*>(dst)[1] = f32x4_t{src[4], src[5], src[6], src[7]};
   }
   if (tid < R) a.part_ml[pbase + tid] = make_float2(sm_M[tid], sm_L[tid]);
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned prev = atomic_add_acq_rel(&a.cnt[item], 1u);
-    sm_last = prev == static_cast<unsigned>(nsplit - 1);
-  }
-  __syncthreads();
-  if (!sm_last) return;
-  __threadfence();
-  const int64_t ibase = item * a.max_splits * a.rmax;
-  for (int idx = tid; idx < R * kCh; idx += kThreads) {
+}
+
+// Second launch: combines the split partials of every (sequence, KV head) that needed more
+// than one split.  Stream order makes the first launch's stores visible here; no fences or
+// counters are involved (an agent-scope fence per block writes back and invalidates the L2
+// of this multi-XCD part and costs far more than the extra launch).
+template <int D>
+__global__ __launch_bounds__(kThreads) void merge_kernel(AttnArgs a) {
+  const int b = blockIdx.y, hkv = blockIdx.x;
+  const int q0 = a.cu[b];
+  const int n = a.cu[b + 1] - q0;
+  const int L = min(a.seq_lens[b], a.max_seqlen_k);
+  if (n <= 0) return;
+  const int nsplit = L > 0 ? (L + a.split - 1) / a.split : 1;
+  if (nsplit <= 1) return;
+  const int R = min(a.G * n, a.rmax);
+  constexpr int kCh = D / 8;
+  const int64_t ibase = (static_cast<int64_t>(b) * a.Hkv + hkv) * a.max_splits * a.rmax;
+  for (int idx = threadIdx.x; idx < R * kCh; idx += kThreads) {
     const int r = idx / kCh, c = idx % kCh;
     float M = -INFINITY;
     for (int s = 0; s < nsplit; ++s) M = fmaxf(M, a.part_ml[ibase + s * a.rmax + r].x);
-    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
     float Lsum = 0.0f;
     for (int s = 0; s < nsplit; ++s) {
       const float2 ml = a.part_ml[ibase + s * a.rmax + r];
       if (!(ml.x > -INFINITY)) continue;
       const float w = exp2_fast(ml.x - M);
       Lsum += ml.y * w;
-      const float* src = a.part_o + (ibase + s * a.rmax + r) * D + c * 8;
-      const f32x4_t x0 = reinterpret_cast<const f32x4_t*>(src)[0];
-      const f32x4_t x1 = reinterpret_cast<const f32x4_t*>(src)[1];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        acc[e] += x0[e] * w;
-        acc[4 + e] += x1[e] * w;
-      }
+      const f32x4_t* src = reinterpret_cast<const f32x4_t*>(a.part_o + (ibase + s * a.rmax + r) * D + c * 8);
+      acc0 += src[0] * w;
+      acc1 += src[1] * w;
     }
     const float inv = Lsum > 0.0f ? 1.0f / Lsum : 0.0f;
-    u32x4_t v;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = pack_bf16x2(acc[2 * e] * inv, acc[2 * e + 1] * inv);
+    const u32x4_t v = {pack_bf16x2(acc0[0] * inv, acc0[1] * inv), pack_bf16x2(acc0[2] * inv, acc0[3] * inv),
+                       pack_bf16x2(acc1[0] * inv, acc1[1] * inv), pack_bf16x2(acc1[2] * inv, acc1[3] * inv)};
     const int hl = r / n, j = r - hl * n;
     uint16_t* dst = a.out + static_cast<int64_t>(q0 + j) * a.o_ts +
                     static_cast<int64_t>(hkv * a.G + hl) * a.o_hs + c * 8;
     *reinterpret_cast<u32x4_t*>(dst) = v;
   }
-  if (tid == 0) atomic_store_relaxed(&a.cnt[item], 0u);
 }
 
 // Keys per split: a pure function of the launch shape, so the workspace can be sized without
@@ -439,15 +474,14 @@ int choose_split(int B, int Hkv, int max_seqlen_k) {
 }
 
 struct AttnWs {
-  size_t cnt_off, ml_off, o_off, total;
+  size_t ml_off, o_off, total;
 };
 
 AttnWs attn_ws_layout(int B, int Hkv, int D, int rmax, int max_splits) {
   auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
   AttnWs w;
   const size_t items = static_cast<size_t>(B) * Hkv;
-  w.cnt_off = 0;
-  w.ml_off = kCounterRegionBytes;
+  w.ml_off = 0;
   w.o_off = w.ml_off + al(items * max_splits * rmax * sizeof(float2));
   w.total = w.o_off + al(items * max_splits * rmax * static_cast<size_t>(D) * sizeof(float));
   return w;
@@ -462,7 +496,10 @@ int launch_rt(int RT, const AttnArgs& a, dim3 grid, hipStream_t s) {
     case 4: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 4>), grid, dim3(kThreads), 0, s, a); break;
     default: return COOPT_EINVAL;
   }
-  return coopt::check_launch("coopt_verify_attention");
+  int rc = coopt::check_launch("coopt_verify_attention");
+  if (rc != COOPT_OK || a.max_splits <= 1) return rc;
+  hipLaunchKernelGGL((merge_kernel<D>), dim3(grid.y, grid.z), dim3(kThreads), 0, s, a);
+  return coopt::check_launch("coopt_verify_attention/merge");
 }
 
 }  // namespace
@@ -494,12 +531,11 @@ extern "C" int coopt_verify_attention(int kv_dtype, const void* q, int64_t q_tok
                 "kv_dtype must be COOPT_DT_BF16 or COOPT_DT_I8");
   COOPT_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0, "Hq must be a multiple of Hkv");
   COOPT_REQUIRE(D == 64 || D == 128, "head_dim must be 64 or 128");
-  COOPT_REQUIRE(block_size > 0 && (block_size & (block_size - 1)) == 0,
-                "block_size must be a power of two");
+  COOPT_REQUIRE(block_size >= 16 && (block_size & (block_size - 1)) == 0,
+                "block_size must be a power of two >= 16");
   COOPT_REQUIRE(max_seqlen_q > 0 && max_seqlen_k > 0, "max_seqlen_q/k must be positive");
   const int G = Hq / Hkv;
   COOPT_REQUIRE(G * max_seqlen_q <= 64, "(Hq/Hkv) * max_seqlen_q must be <= 64");
-  COOPT_REQUIRE(static_cast<int64_t>(B) * Hkv <= kMaxCounters, "B * Hkv must be <= 131072");
   COOPT_REQUIRE(bt_stride >= (max_seqlen_k + block_size - 1) / block_size,
                 "block_table narrower than ceil(max_seqlen_k / block_size)");
   if (B == 0) return COOPT_OK;
@@ -561,7 +597,6 @@ extern "C" int coopt_verify_attention(int kv_dtype, const void* q, int64_t q_tok
   a.rmax = G * max_seqlen_q;
   const AttnWs w = attn_ws_layout(B, Hkv, D, a.rmax, a.max_splits);
   char* base = static_cast<char*>(workspace);
-  a.cnt = reinterpret_cast<unsigned*>(base + w.cnt_off);
   a.part_ml = reinterpret_cast<float2*>(base + w.ml_off);
   a.part_o = reinterpret_cast<float*>(base + w.o_off);
 

@@ -11,11 +11,10 @@
  *   - Return value: COOPT_OK (0) or a negative COOPT_E* code; coopt_last_error()
  *     then holds a message for the calling thread.
  *   - Workspaces are caller-owned device buffers of at least the size the matching
- *     *_workspace() function returns.  Their first 512 KiB hold completion counters for
- *     every shape: zero-fill that region once before first use; every call leaves it zero,
- *     and the bytes after it are scratch.  One workspace can therefore serve calls of any
- *     shape and graph replays without a memset, one call at a time: two calls that overlap
- *     in time on the same workspace race.
+ *     *_workspace() function returns.  They need no initialisation and carry nothing from
+ *     one call to the next; kernels exchange partial results through them only across
+ *     launch boundaries (no cross-workgroup fences or counters).  One workspace serves calls
+ *     of any shape, one call at a time: two calls that overlap in time on it race.
  *
  * Reference interfaces replaced (paths under mohsinmubarak/iitj-llm-coopt):
  *   coopt_kv_write          vLLM reshape_and_cache_flash   engine/model.py:242-243
@@ -112,11 +111,11 @@ int coopt_dequantize(int bits, const void* q, const void* scale, int64_t rows, i
  *                           bf16(float(code) * float(scale)), the value dequantize() gives,
  *                           so the result equals the bf16 path on the dequantised cache.
  *   block_table [B, bt_stride] int32; entries past ceil(L/block_size) are never read.
- *   Supported: D in {64, 128}; (Hq/Hkv) * max_seqlen_q <= 64; block_size a power of two;
+ *   Supported: D in {64, 128}; (Hq/Hkv) * max_seqlen_q <= 64; block_size a power of two >= 16;
  *   B * Hkv <= 131072.  Callers must keep seq_lens <= max_seqlen_k, q rows per sequence
  *   <= max_seqlen_q and block ids in [0, num_blocks); the kernel clamps all three so a
  *   malformed call yields wrong rows but never an access outside its buffers.
- *   workspace: coopt_verify_attention_workspace() bytes, zero-filled once (see above).
+ *   workspace: coopt_verify_attention_workspace() bytes (see above).
  */
 size_t coopt_verify_attention_workspace(int B, int Hq, int Hkv, int D, int max_seqlen_q,
                                         int max_seqlen_k);

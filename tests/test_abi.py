@@ -91,6 +91,7 @@ def test_verify_attention_rejects_unsupported_shapes(lib):
     assert "multiple of Hkv" in _err(call(Hq=30))
     assert "<= 64" in _err(call(mq=17))
     assert "power of two" in _err(call(bs=24))
+    assert ">= 16" in _err(call(bs=8))
     assert "narrower" in _err(call(bt=3))
     assert "kv_dtype" in _err(call(kv=7))
     # INT8 without scales
