@@ -25,8 +25,8 @@ _i, _i64, _f, _p, _sz = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_v
 SIGNATURES = {
     "coopt_last_error": (ctypes.c_char_p, []),
     "coopt_hip_runtime_version": (_i, [ctypes.POINTER(_i)]),
-    "coopt_kv_write": (_i, [_i, _p, _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64,
-                            _i64, _p, _i, _i, _i, _i, _i64, _p]),
+    "coopt_kv_write": (_i, [_i, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _p,
+                            _i64, _i64, _i64, _p, _i, _i, _i, _i, _i64, _p]),
     "coopt_quantize": (_i, [_i, _i, _p, _i64, _i, _p, _p, _p]),
     "coopt_dequantize": (_i, [_i, _p, _p, _i64, _i, _i, _p, _p]),
     "coopt_verify_attention_workspace": (_sz, [_i, _i, _i, _i, _i, _i]),
@@ -37,6 +37,9 @@ SIGNATURES = {
     "coopt_accept_sample": (_i, [_i, _p, _i64, _p, _i, _p, _i64, _p, _p, _p, _p, _p, _f, _i, _i,
                                  _i, _p, _p, _p, _p, _sz, _p]),
     "coopt_softmax": (_i, [_i, _p, _i64, _i64, _i, _f, _p, _i64, _p]),
+    "coopt_rms_norm": (_i, [_p, _p, _p, _p, _i64, _i, _f, _p]),
+    "coopt_rope": (_i, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _i, _i, _i, _i, _i, _p]),
+    "coopt_silu_mul": (_i, [_p, _p, _i64, _i, _p]),
 }
 
 _lock = threading.Lock()

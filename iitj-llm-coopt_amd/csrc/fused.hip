@@ -1,0 +1,180 @@
+// Elementwise stages of the Llama forward around the verify path, fused the way the
+// reference's forward fuses them (engine/model.py:234-254, vLLM's rms_norm /
+// fused_add_rms_norm / rotary_embedding / silu_and_mul): one launch per stage instead of the
+// chain of small elementwise kernels plain torch issues.
+#include "common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float block_sum_f32(float v, float* sh) {
+  v = wave_sum_f32(v);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float r = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ uint16_t round_bf16(float f) { return f32_to_bf16(f); }
+
+// One block per row.  With a residual: r = bf16(x + residual), residual := r.  Then
+// out = bf16(w * bf16(r * rsqrt(mean(r^2) + eps))) -- the rounding points of
+// `w * (x.float() * rsqrt(...)).to(bf16)` (engine/model.py:85-89).
+__global__ __launch_bounds__(kThreads) void rms_norm_kernel(const uint16_t* __restrict__ x,
+                                                            uint16_t* __restrict__ residual,
+                                                            const uint16_t* __restrict__ w,
+                                                            uint16_t* __restrict__ out, int H,
+                                                            float eps) {
+  __shared__ float sh[4];
+  const int64_t row = blockIdx.x;
+  const uint16_t* xr = x + row * H;
+  uint16_t* rr = residual ? residual + row * H : nullptr;
+  float ss = 0.0f;
+  for (int i = threadIdx.x * 8; i < H; i += kThreads * 8) {
+    const uint4 xv = *reinterpret_cast<const uint4*>(xr + i);
+    uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+    if (rr) {
+      const uint4 rv = *reinterpret_cast<const uint4*>(rr + i);
+      const uint32_t rw[4] = {rv.x, rv.y, rv.z, rv.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a0 = bf16_to_f32(static_cast<uint16_t>(xw[e])) + bf16_to_f32(static_cast<uint16_t>(rw[e]));
+        const float a1 = bf16_to_f32(static_cast<uint16_t>(xw[e] >> 16)) + bf16_to_f32(static_cast<uint16_t>(rw[e] >> 16));
+        xw[e] = round_bf16(a0) | (static_cast<uint32_t>(round_bf16(a1)) << 16);
+      }
+      *reinterpret_cast<uint4*>(rr + i) = make_uint4(xw[0], xw[1], xw[2], xw[3]);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float a0 = bf16_to_f32(static_cast<uint16_t>(xw[e]));
+      const float a1 = bf16_to_f32(static_cast<uint16_t>(xw[e] >> 16));
+      ss += a0 * a0 + a1 * a1;
+    }
+  }
+  const float rs = rsqrtf(block_sum_f32(ss, sh) / static_cast<float>(H) + eps);
+  const uint16_t* src = rr ? rr : xr;
+  for (int i = threadIdx.x * 8; i < H; i += kThreads * 8) {
+    const uint4 xv = *reinterpret_cast<const uint4*>(src + i);
+    const uint4 wv = *reinterpret_cast<const uint4*>(w + i);
+    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+    uint32_t ow[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float n0 = bf16_to_f32(round_bf16(bf16_to_f32(static_cast<uint16_t>(xw[e])) * rs));
+      const float n1 = bf16_to_f32(round_bf16(bf16_to_f32(static_cast<uint16_t>(xw[e] >> 16)) * rs));
+      const float y0 = bf16_to_f32(static_cast<uint16_t>(ww[e])) * n0;
+      const float y1 = bf16_to_f32(static_cast<uint16_t>(ww[e] >> 16)) * n1;
+      ow[e] = round_bf16(y0) | (static_cast<uint32_t>(round_bf16(y1)) << 16);
+    }
+    *reinterpret_cast<uint4*>(out + row * H + i) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+  }
+}
+
+// In-place neox rotary embedding of q [T, Hq, D] and k [T, Hkv, D]: for i < D/2,
+// (x_i, x_{i+D/2}) -> (x_i c - x_{i+D/2} s, x_{i+D/2} c + x_i s) with c, s = cos/sin[pos][i]
+// from bf16 tables [max_pos, D] (engine/model.py:92-94, 120-124).  One thread per pair.
+__global__ __launch_bounds__(kThreads) void rope_kernel(uint16_t* __restrict__ q, int64_t q_ts,
+                                                        int64_t q_hs, uint16_t* __restrict__ k,
+                                                        int64_t k_ts, int64_t k_hs,
+                                                        const int64_t* __restrict__ pos,
+                                                        const uint16_t* __restrict__ cos,
+                                                        const uint16_t* __restrict__ sin,
+                                                        int64_t tab_stride, int T, int Hq, int Hkv,
+                                                        int D, int max_pos) {
+  const int half = D / 2;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t per_tok = static_cast<int64_t>(Hq + Hkv) * half;
+  if (gid >= per_tok * T) return;
+  const int t = static_cast<int>(gid / per_tok);
+  const int rem = static_cast<int>(gid % per_tok);
+  const int h = rem / half, i = rem % half;
+  uint16_t* base = h < Hq ? q + t * q_ts + h * q_hs : k + t * k_ts + (h - Hq) * k_hs;
+  int64_t p = pos[t];
+  p = p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p);
+  const float c = bf16_to_f32(cos[p * tab_stride + i]);
+  const float s = bf16_to_f32(sin[p * tab_stride + i]);
+  const float x1 = bf16_to_f32(base[i]), x2 = bf16_to_f32(base[i + half]);
+  base[i] = round_bf16(x1 * c - x2 * s);
+  base[i + half] = round_bf16(x2 * c + x1 * s);
+}
+
+// out[t, j] = silu(gu[t, j]) * gu[t, F + j] (engine/model.py:250-253), 8 elements per thread.
+__global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __restrict__ gu,
+                                                            uint16_t* __restrict__ out, int64_t T,
+                                                            int F) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int per_row = F / 8;
+  if (gid >= T * per_row) return;
+  const int64_t t = gid / per_row;
+  const int j = static_cast<int>(gid % per_row) * 8;
+  const uint4 gv = *reinterpret_cast<const uint4*>(gu + t * 2 * F + j);
+  const uint4 uv = *reinterpret_cast<const uint4*>(gu + t * 2 * F + F + j);
+  const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
+  const uint32_t uw[4] = {uv.x, uv.y, uv.z, uv.w};
+  uint32_t ow[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float r[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const float g = bf16_to_f32(static_cast<uint16_t>(gw[e] >> (16 * hh)));
+      const float u = bf16_to_f32(static_cast<uint16_t>(uw[e] >> (16 * hh)));
+      r[hh] = g / (1.0f + __expf(-g)) * u;
+    }
+    ow[e] = round_bf16(r[0]) | (static_cast<uint32_t>(round_bf16(r[1])) << 16);
+  }
+  *reinterpret_cast<uint4*>(out + t * F + j) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+}
+
+}  // namespace
+
+extern "C" int coopt_rms_norm(const void* x, void* residual, const void* weight, void* out,
+                              int64_t rows, int hidden, float eps, coopt_stream_t stream) {
+  COOPT_REQUIRE(rows >= 0 && hidden > 0 && hidden % 8 == 0, "hidden must be a multiple of 8");
+  if (rows == 0) return COOPT_OK;
+  COOPT_REQUIRE(x && weight && out, "null pointer");
+  COOPT_REQUIRE(coopt::aligned16(x) && coopt::aligned16(weight) && coopt::aligned16(out) &&
+                    (residual == nullptr || coopt::aligned16(residual)),
+                "rows must be 16-byte aligned");
+  coopt::clear_error();
+  hipLaunchKernelGGL(rms_norm_kernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x),
+                     static_cast<uint16_t*>(residual), static_cast<const uint16_t*>(weight),
+                     static_cast<uint16_t*>(out), hidden, eps);
+  return coopt::check_launch("coopt_rms_norm");
+}
+
+extern "C" int coopt_rope(void* q, int64_t q_tok_stride, int64_t q_head_stride, void* k,
+                          int64_t k_tok_stride, int64_t k_head_stride, const int64_t* positions,
+                          const void* cos, const void* sin, int64_t table_stride, int max_pos,
+                          int T, int Hq, int Hkv, int D, coopt_stream_t stream) {
+  COOPT_REQUIRE(T >= 0 && Hq > 0 && Hkv >= 0 && D > 0 && D % 2 == 0 && max_pos > 0, "bad sizes");
+  if (T == 0) return COOPT_OK;
+  COOPT_REQUIRE(q && positions && cos && sin && (k || Hkv == 0), "null pointer");
+  coopt::clear_error();
+  const int64_t total = static_cast<int64_t>(T) * (Hq + Hkv) * (D / 2);
+  hipLaunchKernelGGL(rope_kernel, dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                     static_cast<uint16_t*>(q), q_tok_stride, q_head_stride,
+                     static_cast<uint16_t*>(k), k_tok_stride, k_head_stride, positions,
+                     static_cast<const uint16_t*>(cos), static_cast<const uint16_t*>(sin),
+                     table_stride, T, Hq, Hkv, D, max_pos);
+  return coopt::check_launch("coopt_rope");
+}
+
+extern "C" int coopt_silu_mul(const void* gate_up, void* out, int64_t T, int F,
+                              coopt_stream_t stream) {
+  COOPT_REQUIRE(T >= 0 && F > 0 && F % 8 == 0, "F must be a multiple of 8");
+  if (T == 0) return COOPT_OK;
+  COOPT_REQUIRE(gate_up && out && coopt::aligned16(gate_up) && coopt::aligned16(out),
+                "null or misaligned pointer");
+  coopt::clear_error();
+  const int64_t total = T * (F / 8);
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(out), T, F);
+  return coopt::check_launch("coopt_silu_mul");
+}

@@ -33,8 +33,8 @@ __device__ __forceinline__ int quant_code(float x, float s32) {
 // ---------------------------------------------------------------------------------------
 template <int G, bool INT8>
 __global__ __launch_bounds__(256) void kv_write_kernel(
-    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t in_ts, int64_t in_hs,
-    void* __restrict__ kc, void* __restrict__ vc, int64_t c_bs, int64_t c_ts, int64_t c_hs,
+    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t k_ts, int64_t k_hs,
+    int64_t v_ts, int64_t v_hs, void* __restrict__ kc, void* __restrict__ vc, int64_t c_bs, int64_t c_ts, int64_t c_hs,
     uint16_t* __restrict__ ks, uint16_t* __restrict__ vs, int64_t s_bs, int64_t s_ts, int64_t s_hs,
     const int64_t* __restrict__ slot_mapping, int T, int Hkv, int block_size, int64_t num_slots) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -49,9 +49,8 @@ __global__ __launch_bounds__(256) void kv_write_kernel(
   const int64_t blk = slot / block_size;
   const int64_t off = slot % block_size;
 
-  const int64_t in_off = t * in_ts + h * in_hs + c * 8;
-  const uint4 kr = *reinterpret_cast<const uint4*>(k + in_off);
-  const uint4 vr = *reinterpret_cast<const uint4*>(v + in_off);
+  const uint4 kr = *reinterpret_cast<const uint4*>(k + t * k_ts + h * k_hs + c * 8);
+  const uint4 vr = *reinterpret_cast<const uint4*>(v + t * v_ts + h * v_hs + c * 8);
   const int64_t c_off = blk * c_bs + off * c_ts + h * c_hs + c * 8;
 
   if constexpr (!INT8) {
@@ -94,16 +93,16 @@ __global__ __launch_bounds__(256) void kv_write_kernel(
 }
 
 template <bool INT8>
-int launch_kv_write(int G, const uint16_t* k, const uint16_t* v, int64_t in_ts, int64_t in_hs,
-                    void* kc, void* vc, int64_t c_bs, int64_t c_ts, int64_t c_hs, uint16_t* ks,
+int launch_kv_write(int G, const uint16_t* k, const uint16_t* v, int64_t k_ts, int64_t k_hs,
+                    int64_t v_ts, int64_t v_hs, void* kc, void* vc, int64_t c_bs, int64_t c_ts, int64_t c_hs, uint16_t* ks,
                     uint16_t* vs, int64_t s_bs, int64_t s_ts, int64_t s_hs, const int64_t* slot,
                     int T, int Hkv, int block_size, int64_t num_slots, hipStream_t stream) {
   const int64_t threads = static_cast<int64_t>(T) * Hkv * G;
   const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
 #define COOPT_KVW(GV)                                                                         \
   case GV:                                                                                    \
-    hipLaunchKernelGGL((kv_write_kernel<GV, INT8>), grid, dim3(256), 0, stream, k, v, in_ts, \
-                       in_hs, kc, vc, c_bs, c_ts, c_hs, ks, vs, s_bs, s_ts, s_hs, slot, T, Hkv, \
+    hipLaunchKernelGGL((kv_write_kernel<GV, INT8>), grid, dim3(256), 0, stream, k, v, k_ts, k_hs, \
+                       v_ts, v_hs, kc, vc, c_bs, c_ts, c_hs, ks, vs, s_bs, s_ts, s_hs, slot, T, Hkv, \
                        block_size, num_slots);                                                \
     break;
   switch (G) {
@@ -201,8 +200,9 @@ __global__ __launch_bounds__(256) void dequantize_kernel(const uint8_t* __restri
 
 }  // namespace
 
-extern "C" int coopt_kv_write(int cache_dtype, const void* k, const void* v, int64_t in_tok_stride,
-                              int64_t in_head_stride, void* k_cache, void* v_cache,
+extern "C" int coopt_kv_write(int cache_dtype, const void* k, const void* v, int64_t k_tok_stride,
+                              int64_t k_head_stride, int64_t v_tok_stride, int64_t v_head_stride,
+                              void* k_cache, void* v_cache,
                               int64_t c_blk_stride, int64_t c_tok_stride, int64_t c_head_stride,
                               void* k_scale, void* v_scale, int64_t s_blk_stride,
                               int64_t s_tok_stride, int64_t s_head_stride,
@@ -215,8 +215,8 @@ extern "C" int coopt_kv_write(int cache_dtype, const void* k, const void* v, int
                 "D must be 8 * a power of two, at most 512");
   if (T == 0) return COOPT_OK;
   COOPT_REQUIRE(k && v && k_cache && v_cache && slot_mapping, "null pointer");
-  COOPT_REQUIRE(coopt::aligned16(k) && coopt::aligned16(v) && in_tok_stride % 8 == 0 &&
-                    in_head_stride % 8 == 0,
+  COOPT_REQUIRE(coopt::aligned16(k) && coopt::aligned16(v) && k_tok_stride % 8 == 0 &&
+                    k_head_stride % 8 == 0 && v_tok_stride % 8 == 0 && v_head_stride % 8 == 0,
                 "k/v rows must be 16-byte aligned (strides multiples of 8 elements)");
   const bool int8 = cache_dtype == COOPT_DT_I8;
   if (int8) {
@@ -239,12 +239,14 @@ extern "C" int coopt_kv_write(int cache_dtype, const void* k, const void* v, int
   const auto* kp = static_cast<const uint16_t*>(k);
   const auto* vp = static_cast<const uint16_t*>(v);
   if (int8)
-    return launch_kv_write<true>(D / 8, kp, vp, in_tok_stride, in_head_stride, k_cache, v_cache,
+    return launch_kv_write<true>(D / 8, kp, vp, k_tok_stride, k_head_stride, v_tok_stride,
+                                 v_head_stride, k_cache, v_cache,
                                  c_blk_stride, c_tok_stride, c_head_stride,
                                  static_cast<uint16_t*>(k_scale), static_cast<uint16_t*>(v_scale),
                                  s_blk_stride, s_tok_stride, s_head_stride, slot_mapping, T, Hkv,
                                  block_size, num_slots, s);
-  return launch_kv_write<false>(D / 8, kp, vp, in_tok_stride, in_head_stride, k_cache, v_cache,
+  return launch_kv_write<false>(D / 8, kp, vp, k_tok_stride, k_head_stride, v_tok_stride,
+                                v_head_stride, k_cache, v_cache,
                                 c_blk_stride, c_tok_stride, c_head_stride, nullptr, nullptr, 0, 0,
                                 0, slot_mapping, T, Hkv, block_size, num_slots, s);
 }

@@ -98,8 +98,8 @@ def reshape_and_cache_flash(k, v, k_cache, v_cache, slot_mapping, kv_cache_dtype
     """
     _lib.require_cuda(k, v, k_cache, v_cache, slot_mapping)
     _check_cache_pair(k_cache, v_cache)
-    if k.shape != v.shape or k.stride() != v.stride() or k.dim() != 3 or k.stride(-1) != 1:
-        raise ValueError("k and v must be [T, Hkv, D] with equal strides and contiguous D")
+    if k.shape != v.shape or k.dim() != 3 or k.stride(-1) != 1 or v.stride(-1) != 1:
+        raise ValueError("k and v must be [T, Hkv, D] with contiguous D")
     if k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
         raise ValueError("k and v must be bf16")
     T, Hkv, D = k.shape
@@ -128,7 +128,7 @@ def reshape_and_cache_flash(k, v, k_cache, v_cache, slot_mapping, kv_cache_dtype
     lib = _lib.load()
     cs = k_cache.stride()
     _lib.check(lib.coopt_kv_write(code, _lib.ptr(k), _lib.ptr(v), k.stride(0), k.stride(1),
-                                  _lib.ptr(k_cache), _lib.ptr(v_cache), cs[0], cs[1], cs[2],
+                                  v.stride(0), v.stride(1), _lib.ptr(k_cache), _lib.ptr(v_cache), cs[0], cs[1], cs[2],
                                   _lib.ptr(ks), _lib.ptr(vs), sstr[0], sstr[1], sstr[2],
                                   _lib.ptr(slot_mapping), T, Hkv, D, bs, NB,
                                   _lib.stream_handle(k.device)), "coopt_kv_write")

@@ -51,13 +51,15 @@ def _rows(x):
 
 def accept(target_logits, draft, draft_tokens, temperature, u_accept=None, u_resample=None,
            draft_is_probs=False, gamma_per_seq=None, target_row0=None, draft_row0=None,
-           out=None) -> AcceptResult:
+           out=None, workspace=None) -> AcceptResult:
     """Batched acceptance for B sequences with up to gamma_max drafts each.
 
     target_logits [B, gamma_max+1, V] (or [rows, V] with target_row0[b] = first row of b),
     fp32 or bf16; draft [B, gamma_max, V] draft logits (softmax(draft/T) is formed in the
     kernel) or, with draft_is_probs, fp32 draft probabilities; draft_tokens [B, gamma_max].
     temperature <= 0 selects the greedy rule (argmax, accept while equal).
+    out / workspace: optional preallocated AcceptResult and uint8 scratch buffer (neither
+    allocates then, so the call can be recorded into a HIP graph).
     """
     tgt, tstride = _rows(target_logits)
     _lib.require_cuda(tgt, draft_tokens)
@@ -118,13 +120,20 @@ def accept(target_logits, draft, draft_tokens, temperature, u_accept=None, u_res
                            torch.empty(B, dtype=torch.float32, device=dev))
     lib = _lib.load()
     need = int(lib.coopt_accept_sample_workspace(B, gmax, V))
-    ws = _WS.get(need, dev)
+    if workspace is None:
+        ws = _WS.get(need, dev)
+    elif workspace.numel() * workspace.element_size() < need:
+        raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} bytes, "
+                         f"{need} needed")
+    else:
+        ws = workspace
     _lib.check(lib.coopt_accept_sample(
         _lib.dt_code(tgt.dtype), _lib.ptr(tgt), tstride, _lib.ptr(t0),
         1 if draft_is_probs else 0, _lib.ptr(drf), dstride, _lib.ptr(d0),
         _lib.ptr(dtok), _lib.ptr(gam), _lib.ptr(ua), _lib.ptr(ur), float(temperature),
         B, gmax, V, _lib.ptr(out.accepted_len), _lib.ptr(out.tokens), _lib.ptr(out.margin),
-        _lib.ptr(ws), ws.numel(), _lib.stream_handle(dev)), "coopt_accept_sample")
+        _lib.ptr(ws), ws.numel() * ws.element_size(), _lib.stream_handle(dev)),
+        "coopt_accept_sample")
     return out
 
 

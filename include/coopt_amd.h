@@ -25,6 +25,9 @@
  *   coopt_quantize /        kv_tier_manager.quantize /     engine/kv_tier_manager.py:21-41
  *   coopt_dequantize        dequantize
  *   coopt_softmax           torch.softmax(logits / T)       engine/spec_decode.py:16
+ *   coopt_rms_norm          vLLM rms_norm / fused_add_rms_norm  engine/model.py:234, 236, 249, 254
+ *   coopt_rope              vLLM rotary_embedding (neox)    engine/model.py:239
+ *   coopt_silu_mul          vLLM silu_and_mul               engine/model.py:251-252
  */
 #ifndef COOPT_AMD_H
 #define COOPT_AMD_H
@@ -63,7 +66,7 @@ int coopt_hip_runtime_version(int* version);
  * "auto", k_scale, v_scale) at engine/model.py:242-243; the reference defines it as
  *   k_cache[slot // block_size, slot % block_size] = k   (engine/model.py:190, 201-203).
  *
- *   k, v        [T, Hkv, D] bf16, strides (in_tok_stride, in_head_stride, 1), shared by k and v
+ *   k, v        [T, Hkv, D] bf16 with strides (k_tok, k_head, 1) and (v_tok, v_head, 1)
  *   cache_dtype COOPT_DT_BF16: k_cache/v_cache are bf16 [NB, block_size, Hkv, D]
  *               COOPT_DT_I8:   k_cache/v_cache are int8 codes of the same shape and
  *                              k_scale/v_scale are fp16 [NB, block_size, Hkv]; each (token, head)
@@ -75,8 +78,8 @@ int coopt_hip_runtime_version(int* version);
  *   D must be a multiple of 8 with D/8 a power of two <= 64; k/v/cache rows 16-byte aligned.
  */
 int coopt_kv_write(int cache_dtype,
-                   const void* k, const void* v, int64_t in_tok_stride, int64_t in_head_stride,
-                   void* k_cache, void* v_cache,
+                   const void* k, const void* v, int64_t k_tok_stride, int64_t k_head_stride,
+                   int64_t v_tok_stride, int64_t v_head_stride, void* k_cache, void* v_cache,
                    int64_t c_blk_stride, int64_t c_tok_stride, int64_t c_head_stride,
                    void* k_scale, void* v_scale,
                    int64_t s_blk_stride, int64_t s_tok_stride, int64_t s_head_stride,
@@ -169,6 +172,27 @@ int coopt_accept_sample(int logits_dtype,
  */
 int coopt_softmax(int logits_dtype, const void* logits, int64_t in_stride, int64_t rows, int V,
                   float temperature, float* probs, int64_t out_stride, coopt_stream_t stream);
+
+/*
+ * Elementwise stages of the Llama forward around the verify path (the model the step
+ * benchmark runs), fused as the reference's forward fuses them (engine/model.py:234-254).
+ *
+ * coopt_rms_norm: x, residual, weight, out bf16 [rows, hidden] (weight [hidden]).  With a
+ *   residual (vLLM fused_add_rms_norm): residual := bf16(x + residual), then the norm reads it;
+ *   without (vLLM rms_norm) it reads x.  out = bf16(w * bf16(r * rsqrt(mean(r^2) + eps))), the
+ *   rounding points of the reference's rms_norm (engine/model.py:85-89).  out may alias x.
+ * coopt_rope: in place on q [T, Hq, D] and k [T, Hkv, D] (strides as given, D contiguous),
+ *   neox half-split rotation with bf16 cos/sin tables [max_pos, table_stride] indexed by
+ *   positions[t] (engine/model.py:92-94, 120-127); positions are clamped to [0, max_pos).
+ * coopt_silu_mul: out[t, j] = silu(gate_up[t, j]) * gate_up[t, F + j], bf16, F % 8 == 0.
+ */
+int coopt_rms_norm(const void* x, void* residual, const void* weight, void* out, int64_t rows,
+                   int hidden, float eps, coopt_stream_t stream);
+int coopt_rope(void* q, int64_t q_tok_stride, int64_t q_head_stride, void* k,
+               int64_t k_tok_stride, int64_t k_head_stride, const int64_t* positions,
+               const void* cos, const void* sin, int64_t table_stride, int max_pos, int T, int Hq,
+               int Hkv, int D, coopt_stream_t stream);
+int coopt_silu_mul(const void* gate_up, void* out, int64_t T, int F, coopt_stream_t stream);
 
 #ifdef __cplusplus
 }

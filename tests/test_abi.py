@@ -63,19 +63,20 @@ def _err(rc):
 
 
 def test_kv_write_rejects_bad_arguments(lib):
-    msg = _err(lib.coopt_kv_write(99, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 8, 128, 16,
-                                  16, None))
+    msg = _err(lib.coopt_kv_write(99, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 8,
+                                  128, 16, 16, None))
     assert "cache_dtype" in msg
     assert "D must be" in _err(lib.coopt_kv_write(_lib.DT_BF16, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0,
-                                                  0, 0, 0, 0, 1, 8, 96, 16, 16, None))
+                                                  0, 0, 0, 0, 0, 0, 1, 8, 96, 16, 16, None))
     assert "null" in _err(lib.coopt_kv_write(_lib.DT_BF16, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0,
-                                             0, 0, 1, 8, 128, 16, 16, None))
+                                             0, 0, 0, 0, 1, 8, 128, 16, 16, None))
     # misaligned k/v rows (pointer not 16-byte aligned): rejected before launch
-    assert "aligned" in _err(lib.coopt_kv_write(_lib.DT_BF16, 8, 8, 1024, 128, 16, 16, 0, 0, 0,
-                                                0, 0, 0, 0, 0, 16, 1, 8, 128, 16, 16, None))
+    assert "aligned" in _err(lib.coopt_kv_write(_lib.DT_BF16, 8, 8, 1024, 128, 1024, 128, 16, 16,
+                                                0, 0, 0, 0, 0, 0, 0, 0, 16, 1, 8, 128, 16, 16,
+                                                None))
     # T == 0 is a no-op
-    assert lib.coopt_kv_write(_lib.DT_BF16, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 8,
-                              128, 16, 16, None) == 0
+    assert lib.coopt_kv_write(_lib.DT_BF16, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0,
+                              8, 128, 16, 16, None) == 0
 
 
 def test_verify_attention_rejects_unsupported_shapes(lib):

@@ -1,0 +1,68 @@
+"""GPU: fused forward stages (rms_norm / fused add + rms_norm, neox RoPE, silu_and_mul) against
+the plain torch formulas of the reference's forward (engine/model.py:85-94, 199-211), run in
+fp32 on the same inputs.  Bar: within one bf16 rounding of the fp32 result (the fused kernels
+round once where torch's bf16 chain rounds at every op)."""
+import pytest
+import torch
+
+from iitj_llm_coopt_amd import fused
+
+pytestmark = pytest.mark.gpu
+
+
+def bf16_close(a, ref, ulps=2):
+    """|a - ref| <= ulps * bf16-ulp(|ref|) elementwise (ref in fp32)."""
+    tol = ulps * torch.clamp(ref.abs(), min=1e-3) * 2.0 ** -8
+    return bool(((a.float() - ref).abs() <= tol).all())
+
+
+@pytest.mark.parametrize("rows,hidden", [(1, 4096), (160, 4096), (33, 2048), (5, 128)])
+def test_rms_norm_and_fused_add(dev, rows, hidden):
+    g = torch.Generator(device=dev).manual_seed(rows)
+    x = torch.randn(rows, hidden, generator=g, device=dev).to(torch.bfloat16)
+    r = torch.randn(rows, hidden, generator=g, device=dev).to(torch.bfloat16) * 3
+    w = (1 + 0.1 * torch.randn(hidden, generator=g, device=dev)).to(torch.bfloat16)
+    eps = 1e-5
+    out = fused.rms_norm(x, w, eps)
+    xf = x.float()
+    ref = w.float() * (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps))
+    assert bf16_close(out, ref)
+    res = r.clone()
+    out = fused.rms_norm(x, w, eps, residual=res)
+    rsum = (r.float() + x.float()).to(torch.bfloat16)
+    assert torch.equal(res, rsum)  # residual := bf16(x + residual), exactly
+    rf = rsum.float()
+    ref = w.float() * (rf * torch.rsqrt(rf.pow(2).mean(-1, keepdim=True) + eps))
+    assert bf16_close(out, ref)
+
+
+@pytest.mark.parametrize("Hq,Hkv,D", [(32, 8, 128), (32, 8, 64)])
+def test_rope_in_place_on_qkv_views(dev, Hq, Hkv, D):
+    T, theta, max_pos = 37, 500000.0, 4096
+    g = torch.Generator(device=dev).manual_seed(D)
+    qkv = torch.randn(T, (Hq + 2 * Hkv) * D, generator=g, device=dev).to(torch.bfloat16)
+    pos = torch.randint(0, max_pos, (T,), generator=g, device=dev)
+    inv = 1.0 / (theta ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+    emb = torch.outer(torch.arange(max_pos, dtype=torch.float32), inv)
+    emb = torch.cat((emb, emb), -1)
+    cos, sin = emb.cos().to(dev, torch.bfloat16), emb.sin().to(dev, torch.bfloat16)
+    orig = qkv.clone()
+    q = qkv[:, : Hq * D].view(T, Hq, D)
+    k = qkv[:, Hq * D: (Hq + Hkv) * D].view(T, Hkv, D)
+    fused.rope_(q, k, pos, cos, sin)
+    c, s = cos[pos].float().unsqueeze(1), sin[pos].float().unsqueeze(1)
+    for got, x in ((q, orig[:, : Hq * D].view(T, Hq, D)), (k, orig[:, Hq * D: (Hq + Hkv) * D].view(T, Hkv, D))):
+        xf = x.float()
+        x1, x2 = xf.chunk(2, -1)
+        ref = xf * c + torch.cat((-x2, x1), -1) * s
+        assert bf16_close(got, ref, ulps=4)
+    assert torch.equal(qkv[:, (Hq + Hkv) * D:], orig[:, (Hq + Hkv) * D:])  # v untouched
+
+
+def test_silu_and_mul(dev):
+    g = torch.Generator(device=dev).manual_seed(3)
+    gu = (torch.randn(160, 2 * 14336, generator=g, device=dev) * 3).to(torch.bfloat16)
+    out = fused.silu_and_mul(gu)
+    gate, up = gu.float().chunk(2, -1)
+    ref = torch.nn.functional.silu(gate) * up
+    assert bf16_close(out, ref, ulps=2)
