@@ -44,9 +44,17 @@ def parse():
     ap.add_argument("--gamma", type=int, default=4)
     ap.add_argument("--prompt", type=int, default=1024)
     ap.add_argument("--temperature", type=float, default=1.0)
-    ap.add_argument("--cpu-steps", type=int, default=1)
+    ap.add_argument("--cpu-steps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-tune-gemm", action="store_true",
+                    help="skip PyTorch TunableOp selection of the decode-shape GEMMs")
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="run only the per-kernel cases (no model step), for profiling")
+    ap.add_argument("--case", action="append", choices=sorted(KERNEL_CASES),
+                    help="with --kernels-only: the case(s) to run (default: all)")
+    ap.add_argument("--summarize", metavar="DIR", nargs="+",
+                    help="print a text summary of the rocprofv3 CSV output under DIR(s) and exit")
     return ap.parse_args()
 
 
@@ -76,40 +84,58 @@ def time_launches(torch, dev, fn, n=40):
     return sum(d) / n, d[n // 2]
 
 
-def attention_case(torch, M, dev, B, qlen, ctx, kv_dtype, seed):
-    """The north-star verify-attention shape: B sequences, q_len = gamma + 1, `ctx` cached
-    tokens each, block tables a seeded permutation of a shared pool."""
+def rate(res, nbytes, avg, med):
+    res.update({"bytes": nbytes, "avg_us": avg * 1e6, "median_us": med * 1e6,
+                "GB_s": nbytes / avg / 1e9, "frac": nbytes / avg / HBM_PEAK})
+    return res
+
+
+def attention_case(torch, M, dev, ctx, qlen, kv_dtype, seed):
+    """Verify attention over len(ctx) sequences with ctx[b] cached tokens and q_len new rows
+    each (seq_len = ctx + q_len), Hq 32 / Hkv 8, D 128, block size 16, block tables a seeded
+    permutation of a shared pool.  K/V are N(0,1) with 1% x20 outliers, quantised on write for
+    INT8."""
     import numpy as np
 
     Hq, Hkv, D, bs = 32, 8, 128, 16
+    ctx = np.asarray(ctx, np.int64)
+    B = len(ctx)
     seq = ctx + qlen
     W = -(-seq // bs)
-    nblk = B * W + 1
-    perm = np.random.default_rng(seed).permutation(nblk)[: B * W].reshape(B, W).astype(np.int32)
-    table = torch.from_numpy(perm).to(dev)
+    nblk = int(W.sum()) + 1
+    perm = np.random.default_rng(seed).permutation(nblk)
+    table = np.zeros((B, int(W.max())), np.int32)
+    o = 0
+    for b in range(B):
+        table[b, :W[b]] = perm[o:o + W[b]]
+        o += int(W[b])
+    table = torch.from_numpy(table).to(dev)
     kc, vc, ks, vs = M.allocate_kv_cache(nblk, bs, Hkv, D, kv_dtype, device=dev)
     g = torch.Generator(device=dev).manual_seed(seed)
-    k = torch.randn(nblk * bs, Hkv, D, generator=g, device=dev).to(torch.bfloat16)
-    v = torch.randn(nblk * bs, Hkv, D, generator=g, device=dev).to(torch.bfloat16)
     slots = torch.arange(nblk * bs, device=dev)
-    M.reshape_and_cache_flash(k, v, kc, vc, slots, kv_dtype, ks, vs)
-    del k, v
+    for lo in range(0, nblk * bs, 1 << 18):   # fill the pool in chunks
+        hi = min(nblk * bs, lo + (1 << 18))
+        kv = torch.randn(2, hi - lo, Hkv, D, generator=g, device=dev)
+        kv = torch.where(torch.rand(kv.shape, generator=g, device=dev) < 0.01, kv * 20, kv)
+        kv = kv.to(torch.bfloat16)
+        M.reshape_and_cache_flash(kv[0], kv[1], kc, vc, slots[lo:hi], kv_dtype, ks, vs)
+        del kv
     q = torch.randn(B * qlen, Hq, D, generator=g, device=dev).to(torch.bfloat16)
     cu = torch.arange(B + 1, dtype=torch.int32, device=dev) * qlen
-    sl = torch.full((B,), seq, dtype=torch.int32, device=dev)
+    sl = torch.from_numpy(seq.astype(np.int32)).to(dev)
+    max_k = int(seq.max())
     out = torch.empty_like(q)
-    ws = torch.empty(M.attention.workspace_bytes(B, Hq, Hkv, D, qlen, seq), dtype=torch.uint8,
+    ws = torch.empty(M.attention.workspace_bytes(B, Hq, Hkv, D, qlen, max_k), dtype=torch.uint8,
                      device=dev)
-    per_tok = Hkv * D * 2 * 2 if kv_dtype == "auto" else Hkv * (2 * D + 4)
-    nbytes = B * seq * per_tok + 2 * B * qlen * Hq * D * 2
+    per_tok = Hkv * D * 2 * 2 if kv_dtype == "auto" else Hkv * (2 * D + 2 * 2)
+    nbytes = int(seq.sum()) * per_tok + 2 * B * qlen * Hq * D * 2
 
     def fn():
-        M.paged_attention(q, kc, vc, cu, sl, table, qlen, seq, D ** -0.5, ks, vs, out, ws)
+        M.paged_attention(q, kc, vc, cu, sl, table, qlen, max_k, D ** -0.5, ks, vs, out, ws)
 
-    avg, med = time_launches(torch, dev, fn)
-    return {"kv": kv_dtype, "batch": B, "q_len": qlen, "ctx": ctx, "bytes": nbytes,
-            "avg_us": avg * 1e6, "median_us": med * 1e6, "GB_s": nbytes / avg / 1e9,
-            "frac": nbytes / avg / HBM_PEAK}
+    res = {"kv": kv_dtype, "batch": B, "q_len": qlen, "ctx_min": int(ctx.min()),
+           "ctx_max": int(ctx.max()), "ctx_mean": float(ctx.mean())}
+    return rate(res, nbytes, *time_launches(torch, dev, fn))
 
 
 def accept_case(torch, M, dev, B, gamma, V, seed):
@@ -128,14 +154,13 @@ def accept_case(torch, M, dev, B, gamma, V, seed):
     def fn():
         M.accept(tl, dl, dt32, 1.0, ua, ur, out=res, workspace=ws)
 
-    avg, med = time_launches(torch, dev, fn)
     nbytes = B * (2 * gamma + 1) * V * 4 + B * 2 * V * 4
-    return {"batch": B, "gamma": gamma, "vocab": V, "bytes": nbytes, "avg_us": avg * 1e6,
-            "median_us": med * 1e6, "GB_s": nbytes / avg / 1e9, "frac": nbytes / avg / HBM_PEAK}
+    return rate({"batch": B, "gamma": gamma, "vocab": V}, nbytes, *time_launches(torch, dev, fn))
 
 
 def kv_write_case(torch, M, dev, T, seed):
-    """Config 2: 256 sequences x 5 new tokens (T=1280), Hkv 8, D 128, 65,536-block pool."""
+    """Config 2 shape: T new tokens (256 sequences x 5 = 1280), Hkv 8, D 128, INT8 quantise on
+    write into a 65,536-block pool, slots a seeded random subset; N(0,1) with 1% x20 outliers."""
     import numpy as np
 
     NB, bs, Hkv, D = 65536, 16, 8, 128
@@ -143,16 +168,163 @@ def kv_write_case(torch, M, dev, T, seed):
     perm = np.random.default_rng(seed).permutation(NB * bs)[:T]
     slots = torch.from_numpy(perm.astype(np.int64)).to(dev)
     g = torch.Generator(device=dev).manual_seed(seed)
-    k = torch.randn(T, Hkv, D, generator=g, device=dev).to(torch.bfloat16)
-    v = torch.randn(T, Hkv, D, generator=g, device=dev).to(torch.bfloat16)
+    kv = torch.randn(2, T, Hkv, D, generator=g, device=dev)
+    kv = torch.where(torch.rand(kv.shape, generator=g, device=dev) < 0.01, kv * 20, kv)
+    k, v = kv.to(torch.bfloat16).unbind(0)
 
     def fn():
         M.reshape_and_cache_flash(k, v, kc, vc, slots, "int8", ks, vs)
 
-    avg, med = time_launches(torch, dev, fn)
     nbytes = T * Hkv * D * (2 * 2 + 2 * 1) + T * Hkv * 2 * 2 + T * 8
-    return {"tokens": T, "bytes": nbytes, "avg_us": avg * 1e6, "median_us": med * 1e6,
-            "GB_s": nbytes / avg / 1e9, "frac": nbytes / avg / HBM_PEAK}
+    return rate({"tokens": T}, nbytes, *time_launches(torch, dev, fn))
+
+
+def copy_case(torch, M, dev, seed):
+    """A plain streaming kernel of known size (torch.neg over 1 GiB of bf16: 1 GiB read,
+    1 GiB written): the calibration for FETCH_SIZE / WRITE_SIZE and a practical HBM ceiling."""
+    n = 1 << 29
+    a = torch.empty(n, dtype=torch.bfloat16, device=dev).fill_(1.0)
+    b = torch.empty_like(a)
+
+    def fn():
+        torch.neg(a, out=b)
+
+    return rate({"elements": n, "read_bytes": 2 * n, "write_bytes": 2 * n}, 4 * n,
+                *time_launches(torch, dev, fn, n=20))
+
+
+def config_ctx(seed, B, lo, hi):
+    import numpy as np
+
+    return np.random.default_rng(seed).integers(lo, hi + 1, B)
+
+
+KERNEL_CASES = {
+    # the roofline case: the metric's gamma=4, B=32, 8k context, INT8 KV (config 5's target)
+    "attention_int8": lambda t, M, d, s: attention_case(t, M, d, [8192] * 32, 5, "int8", s),
+    "attention_bf16": lambda t, M, d, s: attention_case(t, M, d, [8192] * 32, 5, "auto", s),
+    # config 3: bf16, B=32, ctx U[512, 4096], q_len 5
+    "attention_config3": lambda t, M, d, s: attention_case(t, M, d, config_ctx(s, 32, 512, 4096), 5, "auto", s),
+    # config 4: INT8, B=64, ctx U[4096, 16384], gamma 2 / 4 / 8
+    "attention_config4_g2": lambda t, M, d, s: attention_case(t, M, d, config_ctx(s, 64, 4096, 16384), 3, "int8", s),
+    "attention_config4_g4": lambda t, M, d, s: attention_case(t, M, d, config_ctx(s, 64, 4096, 16384), 5, "int8", s),
+    "attention_config4_g8": lambda t, M, d, s: attention_case(t, M, d, config_ctx(s, 64, 4096, 16384), 9, "int8", s),
+    # config 1 (B=8) and the metric's B=32
+    "accept_b8": lambda t, M, d, s: accept_case(t, M, d, 8, 4, 128256, s),
+    "accept_b32": lambda t, M, d, s: accept_case(t, M, d, 32, 4, 128256, s),
+    # config 2 (T=1280) and a sustained-bandwidth size
+    "kv_write_t1280": lambda t, M, d, s: kv_write_case(t, M, d, 1280, s),
+    "kv_write_t65536": lambda t, M, d, s: kv_write_case(t, M, d, 65536, s),
+    "copy": lambda t, M, d, s: copy_case(t, M, d, s),
+}
+
+
+def run_kernel_cases(torch, M, dev, names, seed):
+    out = {}
+    for name in names:
+        out[name] = KERNEL_CASES[name](torch, M, dev, seed)
+        r = out[name]
+        log(f"{name}: {r['avg_us']:.1f} us/call, {r['GB_s']:.0f} GB/s ({r['frac'] * 100:.1f}% of 8 TB/s)")
+        torch.cuda.empty_cache()
+    return out
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "verify_attention_int8_b32_ctx8192.md")
+
+
+def committed_traffic():
+    """HBM bytes per roofline call from the committed FETCH_SIZE / WRITE_SIZE profile (the
+    `traffic_bytes_per_call:` line), or None."""
+    import re
+
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                m = re.match(r"\s*traffic_bytes_per_call:\s*([0-9.eE+]+)", line)
+                if m:
+                    return float(m.group(1))
+    except OSError:
+        pass
+    return None
+
+
+def _short(name):
+    """Kernel name without `void`, anonymous namespaces and the argument list."""
+    name = name.replace("(anonymous namespace)::", "").replace("void ", "")
+    depth = 0
+    for i, c in enumerate(name):
+        if c == "<":
+            depth += 1
+        elif c == ">":
+            depth -= 1
+        elif c == "(" and depth == 0:
+            return name[:i][:100]
+    return name[:100]
+
+
+# The roofline call's kernels (attention_int8 case: 8 splits x 8 KV heads x 32 sequences of
+# 256 threads, then one merge block per (KV head, sequence)), and the copy calibration kernel.
+ROOFLINE_KERNELS = (("verify_attn_kernel<128, true, 2>", 524288), ("merge_kernel<128>", 65536))
+COPY_KERNEL = ("neg_kernel_cuda", 67108864, 1 << 30, 1 << 30)   # name part, grid, read, write
+
+
+def summarize(paths):
+    """Text summary of rocprofv3 CSV output under `paths`: per-(kernel, grid) durations
+    (*kernel_trace.csv) and mean counter values per dispatch (*counter_collection.csv); with
+    FETCH_SIZE and WRITE_SIZE for the copy calibration kernel and the roofline call's kernels,
+    also the calibrated HBM bytes per roofline call (`traffic_bytes_per_call:`)."""
+    import csv
+
+    def rows(suffix):
+        for path in paths:
+            for dp, _, files in os.walk(path):
+                for f in sorted(files):
+                    if f.endswith(suffix):
+                        with open(os.path.join(dp, f), newline="") as fh:
+                            yield from csv.DictReader(fh)
+
+    trace = {}
+    for r in rows("kernel_trace.csv"):
+        grid = f"{r['Grid_Size_X']}x{r['Grid_Size_Y']}x{r['Grid_Size_Z']}"
+        key = (_short(r["Kernel_Name"]), grid, r["Workgroup_Size_X"])
+        d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        trace.setdefault(key, []).append(d)
+    if trace:
+        print("| kernel | grid (threads) | wg | calls | avg us | min us | max us | total ms |")
+        print("|---|---|---|---|---|---|---|---|")
+        for (k, grid, wg), ds in sorted(trace.items(), key=lambda kv: -sum(kv[1]))[:40]:
+            print(f"| `{k}` | {grid} | {wg} | {len(ds)} | {sum(ds) / len(ds):.1f} | "
+                  f"{min(ds):.1f} | {max(ds):.1f} | {sum(ds) / 1e3:.2f} |")
+    agg = {}
+    for r in rows("counter_collection.csv"):
+        key = (_short(r["Kernel_Name"]), int(r["Grid_Size"]), r["Counter_Name"])
+        n, tot = agg.get(key, (0, 0.0))
+        agg[key] = (n + 1, tot + float(r["Counter_Value"]))
+    if not agg:
+        return
+    mean = {k: tot / n for k, (n, tot) in agg.items()}
+    print("\n| kernel | grid (threads) | counter | dispatches | mean per dispatch (KiB) |")
+    print("|---|---|---|---|---|")
+    for (k, grid, c), (n, tot) in sorted(agg.items()):
+        print(f"| `{k}` | {grid} | {c} | {n} | {tot / n:.1f} |")
+    scale = {}
+    for (k, grid, c), v in mean.items():
+        if COPY_KERNEL[0] in k and grid == COPY_KERNEL[1] and v > 0:
+            known = COPY_KERNEL[2] if c == "FETCH_SIZE" else COPY_KERNEL[3]
+            scale[c] = known / (v * 1024)
+    for c, f in sorted(scale.items()):
+        print(f"\ncalibration {c}: x{f:.4f} (copy kernel moving 1 GiB each way)")
+    if set(scale) == {"FETCH_SIZE", "WRITE_SIZE"}:
+        total = 0.0
+        for name, grid in ROOFLINE_KERNELS:
+            for c in ("FETCH_SIZE", "WRITE_SIZE"):
+                v = [val for (k, g, cc), val in mean.items() if k == name and g == grid and cc == c]
+                if not v:
+                    return
+                b = v[0] * 1024 * scale[c]
+                print(f"{name} {c}: {b / 1e6:.1f} MB per dispatch (calibrated)")
+                total += b
+        print(f"traffic_bytes_per_call: {total:.0f}")
 
 
 def cpu_baseline(torch, dec, steps):
@@ -181,6 +353,9 @@ def cpu_baseline(torch, dec, steps):
 
 def main():
     args = parse()
+    if args.summarize:
+        summarize(args.summarize)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported in this "
               "build (the path runs on a single MI355X; see DESIGN.md for how it would shard)",
@@ -194,6 +369,10 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.manual_seed(args.seed)
+    if args.kernels_only:
+        names = args.case or sorted(KERNEL_CASES)
+        print(json.dumps(run_kernel_cases(torch, M, dev, names, args.seed)), flush=True)
+        return
     B, g, P = args.batch, args.gamma, args.prompt
     t0 = time.perf_counter()
     target = RandomLlama(TARGET_LLAMA31_8B, dev, seed=args.seed + 1)
@@ -207,6 +386,21 @@ def main():
     dec.prefill(prompts, torch.rand(B, generator=gen, device=dev))
     log(f"prefill of {B}x{P} tokens in {time.perf_counter() - t0:.1f}s")
 
+    tuned = False
+    if not args.no_tune_gemm:
+        # Pick the hipBLASLt/rocBLAS solution of each decode-shape GEMM by timing (PyTorch
+        # TunableOp), during the eager warm-up step, i.e. after prefill and before capture.
+        t0 = time.perf_counter()
+        torch.cuda.tunable.enable(True)
+        torch.cuda.tunable.tuning_enable(True)
+        torch.cuda.tunable.set_max_tuning_duration(50)
+        torch.cuda.tunable.set_filename(os.path.join(os.environ.get("TMPDIR", "/tmp"),
+                                                     "coopt_tunableop_%d.csv"))
+        dec.step()
+        torch.cuda.synchronize(dev)
+        torch.cuda.tunable.tuning_enable(False)
+        tuned = True
+        log(f"GEMM tuning step in {time.perf_counter() - t0:.1f}s")
     dec.step()                       # eager warm-up (allocates workspaces)
     dec.capture()                    # then one HIP graph per step
     for _ in range(args.warmup):
@@ -225,14 +419,9 @@ def main():
     acc_rate = (int(dec.accepted) - a0) / max(1, int(dec.drafted) - d0)
     log(f"{args.steps} steps in {secs * 1e3:.1f} ms: {emitted} tokens, acceptance {acc_rate:.3f}")
 
-    # kernel-level measurements (HIP events per launch, torch's current stream)
-    att_i8 = attention_case(torch, M, dev, B, g + 1, 8192, "int8", args.seed)
-    att_bf = attention_case(torch, M, dev, B, g + 1, 8192, "auto", args.seed)
-    acc = accept_case(torch, M, dev, B, g, TARGET_LLAMA31_8B.vocab, args.seed)
-    kvw = kv_write_case(torch, M, dev, 1280, args.seed)
-    log(f"attention int8 {att_i8['avg_us']:.1f}us {att_i8['frac']*100:.1f}% | bf16 "
-        f"{att_bf['avg_us']:.1f}us {att_bf['frac']*100:.1f}% | accept {acc['avg_us']:.1f}us | "
-        f"kv write {kvw['avg_us']:.1f}us")
+    # kernel-level measurements (HIP events per call, torch's current stream)
+    kern = run_kernel_cases(torch, M, dev, sorted(KERNEL_CASES), args.seed)
+    att_i8 = kern["attention_int8"]
 
     cpu = None
     if not args.no_cpu:
@@ -258,17 +447,19 @@ def main():
                                "per step",
                    "global_batch": B, "seq_len": P, "gamma": g,
                    "temperature": args.temperature, "block_size": 16,
+                   "gemm_selection": "PyTorch TunableOp" if tuned else "default",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": att_i8["GB_s"], "peak": HBM_PEAK / 1e9,
-                     "unit": "GB/s", "frac": att_i8["frac"], "traffic": None,
+                     "unit": "GB/s", "frac": att_i8["frac"], "traffic": committed_traffic(),
                      "kernel": "coopt_verify_attention (main + split merge), INT8 KV, B=32, "
                                "q_len 5, 8192 cached tokens",
-                     "bytes_per_launch": att_i8["bytes"], "avg_launch_us": att_i8["avg_us"]},
+                     "bytes_per_launch": att_i8["bytes"], "avg_launch_us": att_i8["avg_us"],
+                     "traffic_source": "profiles/verify_attention_int8_b32_ctx8192.md "
+                                       "(rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)"},
         "cpu_baseline": cpu,
         "acceptance_rate": acc_rate,
         "tokens_per_step": emitted / args.steps,
-        "kernels": {"verify_attention_int8_ctx8192": att_i8, "verify_attention_bf16_ctx8192": att_bf,
-                    "accept_sample_b32_g4": acc, "kv_write_int8_config2": kvw},
+        "kernels": kern,
     }
     print(json.dumps(out), flush=True)
 

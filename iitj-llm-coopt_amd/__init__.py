@@ -9,6 +9,7 @@ surface of mohsinmubarak/iitj-llm-coopt's engine:
   batch         WorkItem / Batch / build_batch varlen layout (engine/batch.py)
 """
 from . import _lib  # noqa: F401  (imports torch first, then binds the library lazily)
+from . import fused  # noqa: F401  (rms_norm / rope_ / silu_and_mul forward stages)
 from .attention import flash_attn_varlen_func, paged_attention
 from .batch import Batch, WorkItem, build_batch, build_padded_batch
 from .block_manager import BlockManager, OutOfBlocks

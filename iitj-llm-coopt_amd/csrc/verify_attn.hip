@@ -5,9 +5,11 @@
 // G = Hq/Hkv query heads of a KV head and all n query rows of the sequence are packed into
 // R = G*n "rows" (row r = head_local * n + j), so each K/V byte is read once per KV head.
 // A block covers `split` keys of one (sequence, KV head); its 4 waves take 32-key tiles in
-// turn and each keeps its own online softmax; the waves merge through LDS, and when a
-// sequence needs several splits the last split block to finish (device-scope counter)
-// merges the split partials from the workspace.
+// turn and each keeps its own online softmax; the waves merge through LDS.  With one split
+// the block writes the bf16 output; otherwise it writes its (max, sum) and unnormalised fp32
+// partial rows to the workspace and a second launch (merge_kernel, one block per (KV head,
+// sequence)) combines the splits -- the kernel boundary orders the two, so no block waits on
+// another and no cross-workgroup fence is needed.
 //
 // MFMA layout (v_mfma_f32_16x16x32_bf16, lane l, g = l/16):
 //   scores  S^T[key][row] = K[key][:] . Q[row][:]   A = K   (key l%16, 8 d values of group g)
