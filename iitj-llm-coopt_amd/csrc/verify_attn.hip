@@ -5,26 +5,32 @@
 // G = Hq/Hkv query heads of a KV head and all n query rows of the sequence are packed into
 // R = G*n "rows" (row r = head_local * n + j), so each K/V byte is read once per KV head.
 // A block covers `split` keys of one (sequence, KV head); its 4 waves take 32-key tiles in
-// turn and each keeps its own online softmax; the waves merge through LDS.  With one split
-// the block writes the bf16 output; otherwise it writes its (max, sum) and unnormalised fp32
-// partial rows to the workspace and a second launch (merge_kernel, one block per (KV head,
-// sequence)) combines the splits -- the kernel boundary orders the two, so no block waits on
-// another and no cross-workgroup fence is needed.
+// turn, each with its own online softmax, and double-buffer them: the loads of a wave's next
+// tile are in flight while it computes the current one.  The waves merge through LDS.  With
+// one split the block writes the bf16 output; otherwise it writes its (max, sum) and
+// unnormalised fp32 rows to the workspace and a second launch (merge_kernel, one block per
+// (KV head, sequence)) combines the splits -- the kernel boundary orders the two, so no block
+// waits on another and no cross-workgroup fence is needed.
 //
-// MFMA layout (v_mfma_f32_16x16x32_bf16, lane l, g = l/16):
-//   scores  S^T[key][row] = K[key][:] . Q[row][:]   A = K   (key l%16, 8 d values of group g)
-//                                                   B = Q^T (row l%16, the same 8 d values)
-//           -> lane l holds row l%16 and keys 4g..4g+3 of each 16-key tile
-//   output  O^T[d][row] += V^T[d][keys] . P^T[keys][row]
-//           B = P^T: lane l supplies row l%16 and keys {4g..4g+3} of tile 0 and of tile 1,
-//           which are exactly the score registers it already holds -- no shuffles.
-//           A = V^T: d = l%16, the same 8 keys, read from the LDS copy of the V tile.
-//   Every lane's accumulators therefore belong to a single query row, so the online-softmax
-//   rescale is a per-lane scalar.
-// INT8 KV: every code is dequantised to bf16(float(code) * scale) -- the values the reference
-// attends over after dequantize(quantize(KV)) (eval/quality.py:48-52) -- K in registers as it
-// is loaded, V before it is staged in LDS, so the MFMA stages are those of the bf16 path and
-// the INT8 result equals the bf16 kernel run on the dequantised cache.
+// MFMA layout (v_mfma_f32_16x16x32_{bf16,f16}; lane l, g = l/16, m = l%16):
+//   scores  S^T[key][row] = sum_d K[key][d] Q[row][d]     A = K, B = Q^T
+//           K is read with 16-byte loads; load c of lane (key m, group g) covers bytes
+//           [64c + 16g, +16) of the key row, so one load instruction reads 64 contiguous bytes
+//           of each of 16 rows.  The contraction index of k-step ks, element e is therefore
+//           d = 32*ks + 8g + e for bf16 and d = 64*(ks/2) + 16g + 8*(ks%2) + e for INT8; the Q
+//           operand (staged in LDS) uses the same map.  The result gives lane l row m and
+//           keys 4g..4g+3 of each 16-key sub-tile.
+//   output  O^T[d][row] += sum_key V[key][d] P[row][key]  A = V^T, B = P^T
+//           B = P^T is exactly the score registers (keys 4g..4g+3 of sub-tiles 0 and 1), so P
+//           never leaves registers.  A's row index m of d-tile dt stands for d = m*(D/16) + dt,
+//           so a lane reads D/16 contiguous elements of each of its 8 keys (whole key rows per
+//           16 lanes: coalesced) and the transpose to "8 keys of one d" is a byte select in
+//           registers (v_perm / v_cvt_f32_ubyte) -- no LDS staging.  Lane l's accumulators
+//           hold row m and d = (4g + i)*(D/16) + dt.
+// INT8 KV: every K and V code is dequantised to bf16(float(code) * scale) -- the value
+// dequantize() returns (engine/kv_tier_manager.py:41), which the reference attends over --
+// as (code + 128) * s - 128 * s in one fma, exact before the single bf16 rounding; the
+// MFMA stages are then those of the bf16 path.
 #include <math.h>
 
 #include "common.h"
@@ -36,8 +42,11 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kThreads = 256;
-constexpr int kWaves = 4;
+constexpr int kThreads = 256;  // merge kernel
+
+// Waves per attention block: 8 (one block per CU at two waves per SIMD) while the
+// accumulators fit 128 VGPRs-per-row-tile budgets (RT <= 2), else 4.
+constexpr int waves_for(int RT) { return RT <= 2 ? 8 : 4; }
 constexpr int kTileKeys = 32;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -78,51 +87,66 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
 }
 
-// Four int8 codes of one word -> bf16(float(code) * scale), as dequantize(q, s, 8, bf16)
-// computes them (engine/kv_tier_manager.py:41): the fp32 product is exact, then one RNE.
-__device__ __forceinline__ u32x2_t dequant4(uint32_t w, float sc) {
-  const float c0 = static_cast<float>(static_cast<int8_t>(w & 0xff));
-  const float c1 = static_cast<float>(static_cast<int8_t>((w >> 8) & 0xff));
-  const float c2 = static_cast<float>(static_cast<int8_t>((w >> 16) & 0xff));
-  const float c3 = static_cast<float>(static_cast<int8_t>(w >> 24));
-  return u32x2_t{pack_bf16x2(c0 * sc, c1 * sc), pack_bf16x2(c2 * sc, c3 * sc)};
-}
-
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ int64_t clamp_page(int32_t page, int64_t num_blocks) {
   return page < 0 ? 0 : (page >= num_blocks ? num_blocks - 1 : page);
 }
 
+// Byte `i` of a dword holding (code + 128) bytes -> float(code) * s, exact: u * s - 128 * s.
+__device__ __forceinline__ float dequant_byte(uint32_t ux, int i, float s, float sb) {
+  return fmaf(static_cast<float>((ux >> (8 * i)) & 0xffu), s, sb);
+}
+
+// Raw data of one wave's 32-key tile (see the layout notes at the top of the file).
 template <int D, bool INT8>
-struct Tile {
-  static constexpr int kKs = D / 32;                   // MFMA k-steps over the head dim
-  static constexpr int kDt = D / 16;                   // 16-wide d tiles of the output
-  static constexpr int kElt = INT8 ? 1 : 2;            // bytes per cached element
-  static constexpr int kChunkElems = 16 / kElt;        // elements per 16-byte chunk
-  static constexpr int kChunksPerKey = D / kChunkElems;
-  static constexpr int kVLoads = kTileKeys * kChunksPerKey / 64;  // 16-byte V loads per lane
-  // LDS pitch of one staged (bf16) V row in bytes: padded so the transposed reads of the
-  // four key groups land in different banks.
-  static constexpr int kPitch = 2 * D + 8;
-  static constexpr int kWaveLds = kTileKeys * kPitch;
+struct RawTile {
+  static constexpr int kElt = INT8 ? 1 : 2;
+  static constexpr int kKVec = (D / 4) * kElt / 16;  // 16-byte K loads per 16-key sub-tile
+  static constexpr int kVWords = (D / 16) * kElt / 4;  // dwords of V per key
+  u32x4_t k[2][kKVec];
+  uint32_t v[8][kVWords];
+  uint32_t ks[2];        // INT8: fp16 scale of the lane's K key (l16) of each sub-tile
+  u32x2_t vs[2];         // INT8: fp16 scales of the lane's V keys 4g..4g+3 of each sub-tile
 };
 
-// Up to 32 query rows the kernel fits 2 waves per SIMD; 48-64 rows need the full register
-// file (accumulators spill into AGPRs) and run at 1 wave per SIMD.
-template <int D, bool INT8, int RT>
-__global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void verify_attn_kernel(AttnArgs a) {
-  using TL = Tile<D, INT8>;
+template <int N>
+__device__ __forceinline__ void load_words(const unsigned char* p, uint32_t* dst) {
+  if constexpr (N == 4) {
+    const u32x4_t x = *reinterpret_cast<const u32x4_t*>(p);
+    dst[0] = x[0]; dst[1] = x[1]; dst[2] = x[2]; dst[3] = x[3];
+  } else if constexpr (N == 2) {
+    const u32x2_t x = *reinterpret_cast<const u32x2_t*>(p);
+    dst[0] = x[0]; dst[1] = x[1];
+  } else {
+    dst[0] = *reinterpret_cast<const uint32_t*>(p);
+  }
+}
+
+// RT row tiles of 16; SC: the scale caches hold consecutive tokens contiguously (token
+// stride 1), so a lane's four scales of a sub-tile are one 8-byte load; DB: double-buffer
+// the wave's tiles in registers (RT <= 2; larger row counts need the registers for
+// accumulators).
+template <int D, bool INT8, int RT, bool SC>
+__global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(AttnArgs a) {
+  using Raw = RawTile<D, INT8>;
+  constexpr int kWaves = waves_for(RT);
+  constexpr int kBlock = 64 * kWaves;
+  constexpr bool DB = RT <= 2;
+  constexpr int kKs = D / 32;   // k-steps of the score MFMA
+  constexpr int kDt = D / 16;   // d-tiles of the output = V elements per lane per key
+  constexpr int kElt = Raw::kElt;
   constexpr int kRows = RT * 16;
-  constexpr int kOPitch = D + 4;  // fp32 row pitch of the merged output in LDS
-  constexpr int kStageBytes = kWaves * TL::kWaveLds;
-  constexpr int kMergeBytes = kRows * kOPitch * 4;
-  constexpr int kLdsBytes = kStageBytes > kMergeBytes ? kStageBytes : kMergeBytes;
-  __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
+  constexpr int kOPitch = D + 4;       // fp32 row pitch of the merged output in LDS
+  constexpr int kQPitch = D * 2 + 16;  // byte pitch of a staged Q row (16 rows -> distinct banks)
+  constexpr int kQBytes = kRows * kQPitch;
+  constexpr int kOBytes = kRows * kOPitch * 4;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kQBytes > kOBytes ? kQBytes : kOBytes];
   __shared__ float sm_m[kWaves][kRows];
   __shared__ float sm_l[kWaves][kRows];
   __shared__ float sm_M[kRows];
   __shared__ float sm_L[kRows];
+  float* osh = reinterpret_cast<float*>(lds);
 
   const int b = blockIdx.z, hkv = blockIdx.y, sidx = blockIdx.x;
   const int q0 = a.cu[b];
@@ -140,144 +164,215 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void verify_attn_kerne
   const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, l16 = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int bs_mask = (1 << a.bs_shift) - 1;
-  const int32_t* table = a.bt + static_cast<int64_t>(b) * a.bt_stride;
+  // The block table is read-only here: reading it through the constant address space lets
+  // the wave-uniform page lookups be scalar loads, which do not wait behind (or drain) the
+  // wave's outstanding K/V vector loads.
+  typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
+  const const_i32_ptr table = (const_i32_ptr)(a.bt + static_cast<int64_t>(b) * a.bt_stride);
 
-  // ---- Q operand (B of the score MFMA) and per-row causal limits ----
-  u32x4_t qreg[RT][TL::kKs];
+  // ---- Q rows into LDS, causal limits ----
+  // Row r of the block is query head hkv*G + r/n at query row j = r % n; rows >= R are 0.
+  constexpr int kQCh = D / 8;  // 16-byte chunks per row
+  constexpr int kQIter = (kRows * kQCh + kBlock - 1) / kBlock;
+#pragma unroll
+  for (int it = 0; it < kQIter; ++it) {
+    const int idx = it * kBlock + tid;
+    const int r = idx / kQCh, c = idx % kQCh;
+    if (r < kRows) {
+      u32x4_t qv = {0, 0, 0, 0};
+      if (r < R) {
+        const int hl = r / n, j = r - hl * n;
+        qv = *reinterpret_cast<const u32x4_t*>(a.q + static_cast<int64_t>(q0 + j) * a.q_ts +
+                                               static_cast<int64_t>(hkv * a.G + hl) * a.q_hs + c * 8);
+      }
+      *reinterpret_cast<u32x4_t*>(lds + r * kQPitch + c * 16) = qv;
+    }
+  }
+  __syncthreads();
+  const float score_scale = a.scale_log2;
   int lim[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const int r = rt * 16 + l16;
-    if (r < R) {
-      const int hl = r / n, j = r - hl * n;
-      const uint16_t* qp = a.q + static_cast<int64_t>(q0 + j) * a.q_ts +
-                           static_cast<int64_t>(hkv * a.G + hl) * a.q_hs + grp * 8;
-#pragma unroll
-      for (int ks = 0; ks < TL::kKs; ++ks) qreg[rt][ks] = *reinterpret_cast<const u32x4_t*>(qp + ks * 32);
-      lim[rt] = L - n + j;  // bottom-right aligned causal mask
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < TL::kKs; ++ks) qreg[rt][ks] = u32x4_t{0, 0, 0, 0};
-      lim[rt] = -1;
-    }
+    lim[rt] = r < R ? L - n + (r % n) : -1;  // bottom-right aligned causal mask
   }
+  // the lane's Q operand of (rt, ks): row rt*16 + l16, the 8 elements from d_of(ks) (the
+  // contraction map of the K loads)
+  const unsigned char* qlds = lds + l16 * kQPitch;
+  auto q_byte = [&](int ks) {
+    return INT8 ? 2 * (64 * (ks >> 1) + 16 * grp + 8 * (ks & 1)) : 2 * (32 * ks + 8 * grp);
+  };
 
-  f32x4_t o[RT][TL::kDt];
+  f32x4_t o[RT][kDt];
   float m_run[RT], l_run[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     m_run[rt] = -INFINITY;
     l_run[rt] = 0.0f;
 #pragma unroll
-    for (int dt = 0; dt < TL::kDt; ++dt) o[rt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int dt = 0; dt < kDt; ++dt) o[rt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 
-  unsigned char* stage = lds + wave * TL::kWaveLds;
   const int ntiles = (k_end - k_begin + kTileKeys - 1) / kTileKeys;
   const unsigned char* kbase = static_cast<const unsigned char*>(a.kc);
   const unsigned char* vbase = static_cast<const unsigned char*>(a.vc);
   const int64_t head_off = static_cast<int64_t>(hkv) * a.c_hs;
   const int64_t shead_off = static_cast<int64_t>(hkv) * a.s_hs;
+  const int min_lim = L - n;  // causal limit of the first query row
 
-  // `wave` is uniform, so the tile loop and the two page lookups per tile are scalar.  A
-  // 32-key tile starts on a multiple of 32 and block_size >= 16, so its keys lie in at most
-  // two pages: the one holding key kb and the one holding key kb + 16 (keys past the end are
-  // clamped to L - 1, which stays in the page of its 16-key half).  The page ids of the
-  // wave's next tile are fetched one iteration ahead.
+  // `wave` is uniform, so tile bookkeeping and page lookups are scalar.  A 32-key tile starts
+  // on a multiple of 32 and block_size >= 16, so its keys lie in at most two pages: the page
+  // of key kb (sub-tile 0) and of key kb + 16 (sub-tile 1); keys past the end are clamped to
+  // L - 1, which stays in the page of its 16-key sub-tile.
   auto page_of = [&](int key) {
     return clamp_page(table[min(key, L - 1) >> a.bs_shift], a.num_blocks);
   };
-  int64_t nxt0 = 0, nxt1 = 0;
-  if (wave < ntiles) {
-    nxt0 = page_of(k_begin + wave * kTileKeys);
-    nxt1 = page_of(k_begin + wave * kTileKeys + 16);
-  }
-  for (int tile = wave; tile < ntiles; tile += kWaves) {
-    const int kb = k_begin + tile * kTileKeys;
-    const int64_t pg0 = nxt0, pg1 = nxt1;
-    if (tile + kWaves < ntiles) {
-      nxt0 = page_of(kb + kWaves * kTileKeys);
-      nxt1 = page_of(kb + kWaves * kTileKeys + 16);
-    }
 
-    // ---- issue every load of the tile before using any of them ----
-    // K operand: lane's key for each 16-key sub-tile, 8 d values per k-step.
-    u32x4_t kraw[2][TL::kKs];
-    u32x2_t kraw8[2][TL::kKs];
-    float ksc[2] = {0.0f, 0.0f};
+  // Issue every load of tile `t` (pages pg0/pg1).  Page bases are wave-uniform (scalar);
+  // lanes add 32-bit byte offsets.  Full tiles (every key < L) use offsets fixed for the
+  // whole loop; the last, partial tile clamps each key to L - 1, so no row past the
+  // sequence is read.
+  const int c_ts = static_cast<int>(a.c_ts), s_ts = static_cast<int>(a.s_ts);
+  const uint32_t k_lane = kElt * l16 * c_ts + 16 * grp;
+  uint32_t v_lane[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v_lane[i] = kElt * ((grp * 4 + i) * c_ts + l16 * kDt);
+  // The empty asm keeps each offset a 32-bit register at its use, so the loads take the
+  // scalar-base + 32-bit-offset form instead of a per-lane 64-bit address.
+  auto issue = [&](Raw& raw, int kt, const unsigned char* kp, const unsigned char* vp,
+                   uint32_t ko, const uint32_t (&vo)[4]) {
+#pragma unroll
+    for (int c = 0; c < Raw::kKVec; ++c) {
+      uint32_t off = ko + 64u * c;
+      asm volatile("" : "+v"(off));
+      raw.k[kt][c] = *reinterpret_cast<const u32x4_t*>(kp + off);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t off = vo[i];
+      asm volatile("" : "+v"(off));
+      load_words<Raw::kVWords>(vp + off, raw.v[kt * 4 + i]);
+    }
+  };
+  // a full tile: every key < L
+  auto load_full = [&](Raw& raw, int t, int64_t pg0, int64_t pg1) {
+    const int kb = k_begin + t * kTileKeys;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
-      const int key = min(kb + kt * 16 + l16, L - 1);
-      const int64_t tok = static_cast<int64_t>(key & bs_mask);
       const int64_t pg = kt ? pg1 : pg0;
-      const int64_t row = pg * a.c_bs + tok * a.c_ts + head_off;
-#pragma unroll
-      for (int ks = 0; ks < TL::kKs; ++ks) {
-        const int64_t e = row + ks * 32 + grp * 8;
-        if constexpr (INT8) {
-          kraw8[kt][ks] = *reinterpret_cast<const u32x2_t*>(kbase + e);
+      const int tok0 = (kb + kt * 16) & bs_mask;
+      const int64_t r = pg * a.c_bs + head_off + static_cast<int64_t>(tok0) * c_ts;
+      issue(raw, kt, kbase + kElt * r, vbase + kElt * r, k_lane, v_lane);
+      if constexpr (INT8) {
+        const uint16_t* ksp = a.ks + pg * a.s_bs + shead_off;
+        const uint16_t* vsp = a.vs + pg * a.s_bs + shead_off;
+        if constexpr (SC) {
+          uint32_t ko2 = l16 * 2, vo2 = grp * 8;
+          asm volatile("" : "+v"(ko2), "+v"(vo2));
+          raw.ks[kt] = *reinterpret_cast<const uint16_t*>(reinterpret_cast<const unsigned char*>(ksp + tok0) + ko2);
+          raw.vs[kt] = *reinterpret_cast<const u32x2_t*>(reinterpret_cast<const unsigned char*>(vsp + tok0) + vo2);
         } else {
-          kraw[kt][ks] = *reinterpret_cast<const u32x4_t*>(kbase + 2 * e);
+          raw.ks[kt] = ksp[(tok0 + l16) * s_ts];
+          uint32_t vh[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) vh[i] = vsp[(tok0 + grp * 4 + i) * s_ts];
+          raw.vs[kt] = u32x2_t{vh[0] | (vh[1] << 16), vh[2] | (vh[3] << 16)};
         }
       }
-      if constexpr (INT8) ksc[kt] = f16_to_f32(a.ks[pg * a.s_bs + tok * a.s_ts + shead_off]);
     }
-    // V tile: coalesced 16-byte chunks, staged through LDS below.
-    u32x4_t vreg[TL::kVLoads];
-    float vsc[TL::kVLoads];
+  };
+  // the split's last tile when it ends inside a tile: keys clamped to L - 1
+  auto load_partial = [&](Raw& raw, int t, int64_t pg0, int64_t pg1) {
+    const int kb = k_begin + t * kTileKeys;
 #pragma unroll
-    for (int it = 0; it < TL::kVLoads; ++it) {
-      const int id = it * 64 + lane;
-      const int kk = id / TL::kChunksPerKey, c = id % TL::kChunksPerKey;
-      const int key = min(kb + kk, L - 1);
-      const int64_t tok = static_cast<int64_t>(key & bs_mask);
-      const int64_t pg = kk < 16 ? pg0 : pg1;
-      const int64_t row = pg * a.c_bs + tok * a.c_ts + head_off;
-      vreg[it] = *reinterpret_cast<const u32x4_t*>(vbase + TL::kElt * row + c * 16);
-      vsc[it] = 0.0f;
-      if constexpr (INT8) vsc[it] = f16_to_f32(a.vs[pg * a.s_bs + tok * a.s_ts + shead_off]);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    // K to bf16 MFMA operands (INT8: dequantised with the lane's key scale).
-    u32x4_t kreg[2][TL::kKs];
+    for (int kt = 0; kt < 2; ++kt) {
+      const int64_t pg = kt ? pg1 : pg0;
+      const int sub = kb + kt * 16;
+      const int64_t row0 = pg * a.c_bs + head_off;
+      const int ktk = min(sub + l16, L - 1) & bs_mask;
+      const uint32_t ko = kElt * ktk * c_ts + 16 * grp;
+      uint32_t vo[4], tk[4];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int ks = 0; ks < TL::kKs; ++ks) {
-        if constexpr (INT8) {
-          const u32x2_t lo = dequant4(kraw8[kt][ks][0], ksc[kt]);
-          const u32x2_t hi = dequant4(kraw8[kt][ks][1], ksc[kt]);
-          kreg[kt][ks] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
-        } else {
-          kreg[kt][ks] = kraw[kt][ks];
-        }
+      for (int i = 0; i < 4; ++i) {
+        tk[i] = min(sub + grp * 4 + i, L - 1) & bs_mask;
+        vo[i] = kElt * (tk[i] * c_ts + l16 * kDt);
       }
+      issue(raw, kt, kbase + kElt * row0, vbase + kElt * row0, ko, vo);
+      if constexpr (INT8) {
+        const uint16_t* ksp = a.ks + pg * a.s_bs + shead_off;
+        const uint16_t* vsp = a.vs + pg * a.s_bs + shead_off;
+        raw.ks[kt] = ksp[ktk * s_ts];
+        uint32_t vh[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vh[i] = vsp[tk[i] * s_ts];
+        raw.vs[kt] = u32x2_t{vh[0] | (vh[1] << 16), vh[2] | (vh[3] << 16)};
+      }
+    }
+  };
 
-    // ---- scores and online softmax ----
+  auto compute_tile = [&](const Raw& raw, int t) {
+    const int kb = k_begin + t * kTileKeys;
+    // every key of the tile inside the split and visible to every row: no masking
+    const bool open = kb + kTileKeys <= k_end && kb + kTileKeys - 1 <= min_lim;
+    auto scale_of = [&](const u32x2_t& w, int i) {
+      return f16_to_f32(static_cast<uint16_t>(w[i >> 1] >> (16 * (i & 1))));
+    };
+
+    // ---- scores: S^T = K . Q^T, K operands built per k-step ----
+    f32x4_t acc[RT][2];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) acc[rt][0] = acc[rt][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < kKs; ++ks) {
+      u32x4_t qop[RT];
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+        qop[rt] = *reinterpret_cast<const u32x4_t*>(qlds + rt * 16 * kQPitch + q_byte(ks));
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        u32x4_t kop;
+        if constexpr (INT8) {
+          // the lane's key l16 of sub-tile kt: codes 8*(ks%2) .. +8 of its load ks/2
+          const u32x4_t& c4 = raw.k[kt][ks >> 1];
+          const float sk = f16_to_f32(static_cast<uint16_t>(raw.ks[kt]));
+          const float skb = -128.0f * sk;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const uint32_t ux = c4[(ks & 1) * 2 + h] ^ 0x80808080u;
+            kop[2 * h] = pack_bf16x2(dequant_byte(ux, 0, sk, skb), dequant_byte(ux, 1, sk, skb));
+            kop[2 * h + 1] = pack_bf16x2(dequant_byte(ux, 2, sk, skb), dequant_byte(ux, 3, sk, skb));
+          }
+        } else {
+          kop = raw.k[kt][ks];
+        }
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) acc[rt][kt] = mfma_bf16(kop, qop[rt], acc[rt][kt]);
+      }
+    }
+
+    // ---- online softmax ----
     uint32_t pb[RT][4];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       float sv[2][4];
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < TL::kKs; ++ks) acc = mfma_bf16(kreg[kt][ks], qreg[rt][ks], acc);
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int key = kb + kt * 16 + grp * 4 + i;
-          const float s = acc[i] * a.scale_log2;
-          sv[kt][i] = (key > lim[rt] || key >= k_end) ? -INFINITY : s;
+          const float s = acc[rt][kt][i] * score_scale;
+          if (open) {
+            sv[kt][i] = s;
+          } else {
+            const int key = kb + kt * 16 + grp * 4 + i;
+            sv[kt][i] = (key > lim[rt] || key >= k_end) ? -INFINITY : s;
+          }
         }
-      }
       float tmax = fmaxf(fmaxf(fmaxf(sv[0][0], sv[0][1]), fmaxf(sv[0][2], sv[0][3])),
                          fmaxf(fmaxf(sv[1][0], sv[1][1]), fmaxf(sv[1][2], sv[1][3])));
       tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
       tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
       const float m_new = fmaxf(m_run[rt], tmax);
       const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-      const float alpha = exp2_fast(m_run[rt] - m_use);
       float p[2][4], psum = 0.0f;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
@@ -286,51 +381,43 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void verify_attn_kerne
           p[kt][i] = exp2_fast(sv[kt][i] - m_use);
           psum += p[kt][i];
         }
-      l_run[rt] = l_run[rt] * alpha + psum;
-      m_run[rt] = m_new;
+      // rescale only when some row's running max moved (alpha != 1 somewhere in the wave)
+      if (__builtin_amdgcn_ballot_w64(m_new != m_run[rt])) {
+        const float alpha = exp2_fast(m_run[rt] - m_use);
+        l_run[rt] *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < TL::kDt; ++dt) o[rt][dt] *= alpha;
+        for (int dt = 0; dt < kDt; ++dt) o[rt][dt] *= alpha;
+      }
+      l_run[rt] += psum;
+      m_run[rt] = m_new;
       pb[rt][0] = pack_bf16x2(p[0][0], p[0][1]);
       pb[rt][1] = pack_bf16x2(p[0][2], p[0][3]);
       pb[rt][2] = pack_bf16x2(p[1][0], p[1][1]);
       pb[rt][3] = pack_bf16x2(p[1][2], p[1][3]);
     }
 
-    // ---- stage V in LDS (this wave's region; only this wave reads it) ----
+    // ---- O^T += V^T . P^T, the V^T operand built in registers ----
+    uint32_t vx[8][Raw::kVWords];
 #pragma unroll
-    for (int it = 0; it < TL::kVLoads; ++it) {
-      const int id = it * 64 + lane;
-      const int kk = id / TL::kChunksPerKey, c = id % TL::kChunksPerKey;
-      unsigned char* dst = stage + kk * TL::kPitch + c * 2 * TL::kChunkElems;
-      if constexpr (INT8) {
-        u32x2_t* d64 = reinterpret_cast<u32x2_t*>(dst);
+    for (int j = 0; j < 8; ++j)
 #pragma unroll
-        for (int w = 0; w < 4; ++w) d64[w] = dequant4(vreg[it][w], vsc[it]);
-      } else {
-        u32x2_t* d64 = reinterpret_cast<u32x2_t*>(dst);
-        d64[0] = u32x2_t{vreg[it][0], vreg[it][1]};
-        d64[1] = u32x2_t{vreg[it][2], vreg[it][3]};
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    // ---- O^T += V^T . P^T ----
+      for (int w = 0; w < Raw::kVWords; ++w) vx[j][w] = INT8 ? (raw.v[j][w] ^ 0x80808080u) : raw.v[j][w];
 #pragma unroll
-    for (int dt = 0; dt < TL::kDt; ++dt) {
-      const int d = dt * 16 + l16;
+    for (int dt = 0; dt < kDt; ++dt) {
       u32x4_t va;
 #pragma unroll
       for (int e2 = 0; e2 < 4; ++e2) {
-        uint32_t half[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int e = e2 * 2 + h;
-          const int kk = e < 4 ? grp * 4 + e : 16 + grp * 4 + (e - 4);
-          half[h] = *reinterpret_cast<const uint16_t*>(stage + kk * TL::kPitch + 2 * d);
+        const int j0 = 2 * e2, j1 = 2 * e2 + 1;  // keys of k-elements 2*e2, 2*e2+1
+        if constexpr (INT8) {
+          const int w = dt >> 2, byte = dt & 3;
+          const float s0 = scale_of(raw.vs[j0 >> 2], j0 & 3), s1 = scale_of(raw.vs[j1 >> 2], j1 & 3);
+          const float x0 = dequant_byte(vx[j0][w], byte, s0, -128.0f * s0);
+          const float x1 = dequant_byte(vx[j1][w], byte, s1, -128.0f * s1);
+          va[e2] = pack_bf16x2(x0, x1);
+        } else {
+          const int w = dt >> 1;
+          va[e2] = __builtin_amdgcn_perm(vx[j1][w], vx[j0][w], (dt & 1) ? 0x07060302u : 0x05040100u);
         }
-        va[e2] = half[0] | (half[1] << 16);
       }
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
@@ -338,9 +425,58 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void verify_attn_kerne
         o[rt][dt] = mfma_bf16(va, pbv, o[rt][dt]);
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
+  };
+
+  // ---- the wave's tiles: double-buffered (the next tile's loads in flight while the current
+  // one is computed) or, for large row counts, one at a time; then the partial tile ----
+  const int nfull = (k_end - k_begin) / kTileKeys;
+  auto pages = [&](int t, int64_t& p0, int64_t& p1) {
+    const int kb = k_begin + t * kTileKeys;
+    p0 = page_of(kb);
+    p1 = page_of(kb + 16);
+  };
+  if constexpr (DB) {
+    // Loads inside the loop are unconditional (an index past the last full tile repeats it,
+    // already cached, and is never computed), so each compute waits only for its own
+    // buffer's loads and the other buffer's stay in flight.
+    Raw bufA, bufB;
+    const int tlast = nfull - 1;
+    int t = wave;
+    int64_t nx0 = 0, nx1 = 0;  // pages of the wave's next tile to load
+    if (t < nfull) {
+      int64_t p0, p1;
+      pages(t, p0, p1);
+      load_full(bufA, t, p0, p1);
+      pages(min(t + kWaves, tlast), nx0, nx1);
+    }
+    for (; t < nfull; t += 2 * kWaves) {
+      const int t1 = t + kWaves, t2 = t1 + kWaves;
+      load_full(bufB, min(t1, tlast), nx0, nx1);
+      pages(min(t2, tlast), nx0, nx1);
+      compute_tile(bufA, t);
+      if (t1 >= nfull) break;
+      load_full(bufA, min(t2, tlast), nx0, nx1);
+      pages(min(t2 + kWaves, tlast), nx0, nx1);
+      compute_tile(bufB, t1);
+    }
+  } else {
+    Raw buf;
+    int64_t nx0 = 0, nx1 = 0;
+    if (wave < nfull) pages(wave, nx0, nx1);
+    for (int t = wave; t < nfull; t += kWaves) {
+      load_full(buf, t, nx0, nx1);
+      if (t + kWaves < nfull) pages(t + kWaves, nx0, nx1);
+      compute_tile(buf, t);
+    }
   }
+  if (nfull < ntiles && wave == nfull % kWaves) {
+    Raw buf;
+    int64_t p0, p1;
+    pages(nfull, p0, p1);
+    load_partial(buf, nfull, p0, p1);
+    compute_tile(buf, nfull);
+  }
+  __syncthreads();  // Q in LDS is dead; the merge below reuses the space
 
   // ---- merge the 4 waves ----
 #pragma unroll
@@ -365,13 +501,14 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void verify_attn_kerne
       if (sm_m[w][r] > -INFINITY) Lsum += sm_l[w][r] * exp2_fast(sm_m[w][r] - M);
     const float f = m_run[rt] > -INFINITY ? exp2_fast(m_run[rt] - M) : 0.0f;
 #pragma unroll
-    for (int dt = 0; dt < TL::kDt; ++dt) o[rt][dt] *= f;
+    for (int dt = 0; dt < kDt; ++dt) o[rt][dt] *= f;
     if (wave == 0 && grp == 0) {
       sm_M[r] = M;
       sm_L[r] = Lsum;
     }
   }
-  float* osh = reinterpret_cast<float*>(lds);
+  // lane's accumulators: row rt*16 + l16, d = (4g + i) * kDt + dt -- kDt contiguous floats
+  // for each (rt, i)
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
     if (wave == w) {
@@ -379,12 +516,15 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void verify_attn_kerne
       for (int rt = 0; rt < RT; ++rt) {
         const int r = rt * 16 + l16;
 #pragma unroll
-        for (int dt = 0; dt < TL::kDt; ++dt) {
-          f32x4_t* dst = reinterpret_cast<f32x4_t*>(osh + r * kOPitch + dt * 16 + grp * 4);
-          if (w == 0) {
-            *dst = o[rt][dt];
-          } else {
-            *dst = *dst + o[rt][dt];
+        for (int i = 0; i < 4; ++i) {
+          float* dst = osh + r * kOPitch + (grp * 4 + i) * kDt;
+#pragma unroll
+          for (int d4 = 0; d4 < kDt / 4; ++d4) {
+            const f32x4_t x = {o[rt][d4 * 4 + 0][i], o[rt][d4 * 4 + 1][i], o[rt][d4 * 4 + 2][i],
+                               o[rt][d4 * 4 + 3][i]};
+            f32x4_t* dp = reinterpret_cast<f32x4_t*>(dst + 4 * d4);
+            if (w == 0) *dp = x;
+            else *dp = *dp + x;
           }
         }
       }
@@ -395,7 +535,7 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void verify_attn_kerne
   constexpr int kCh = D / 8;  // 8-element chunks per row
   const int64_t item = static_cast<int64_t>(b) * a.Hkv + hkv;
   if (nsplit == 1) {
-    for (int idx = tid; idx < R * kCh; idx += kThreads) {
+    for (int idx = tid; idx < R * kCh; idx += kBlock) {
       const int r = idx / kCh, c = idx % kCh;
       const float Lr = sm_L[r];
       const float inv = Lr > 0.0f ? 1.0f / Lr : 0.0f;
@@ -413,7 +553,7 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void verify_attn_kerne
 
   // ---- several splits: publish this split's partial; merge_kernel combines them ----
   const int64_t pbase = (item * a.max_splits + sidx) * a.rmax;
-  for (int idx = tid; idx < R * kCh; idx += kThreads) {
+  for (int idx = tid; idx < R * kCh; idx += kBlock) {
     const int r = idx / kCh, c = idx % kCh;
     const float* src = osh + r * kOPitch + c * 8;
     float* dst = a.part_o + (pbase + r) * D + c * 8;
@@ -465,13 +605,17 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(AttnArgs a) {
 }
 
 // Keys per split: a pure function of the launch shape, so the workspace can be sized without
-// reading seq_lens.  Aims at ~2048 blocks (8 per CU) for the longest context.
-int choose_split(int B, int Hkv, int max_seqlen_k) {
+// reading seq_lens.  Aims at one block per CU (8-wave blocks) or two (4-wave blocks) for the
+// longest context, in whole rounds of 32-key tiles over the block's waves; a sequence longer
+// than one split is split, so shorter ones run whole.
+int choose_split(int B, int Hkv, int max_seqlen_k, int waves) {
   const int64_t items = static_cast<int64_t>(B) * Hkv;
-  int64_t per = (static_cast<int64_t>(max_seqlen_k) * items + 2047) / 2048;
-  per = ((per + 127) / 128) * 128;
-  if (per < 256) per = 256;
-  if (per > 8192) per = 8192;
+  const int64_t target = waves == 8 ? 256 : 512;
+  const int64_t gran = 32 * waves;
+  int64_t per = (static_cast<int64_t>(max_seqlen_k) * items + target - 1) / target;
+  per = ((per + gran - 1) / gran) * gran;
+  if (per < 2 * gran) per = 2 * gran;
+  if (per > 65536) per = 65536;
   return static_cast<int>(per);
 }
 
@@ -489,13 +633,13 @@ AttnWs attn_ws_layout(int B, int Hkv, int D, int rmax, int max_splits) {
   return w;
 }
 
-template <int D, bool INT8>
+template <int D, bool INT8, bool SC>
 int launch_rt(int RT, const AttnArgs& a, dim3 grid, hipStream_t s) {
   switch (RT) {
-    case 1: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 1>), grid, dim3(kThreads), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 2>), grid, dim3(kThreads), 0, s, a); break;
-    case 3: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 3>), grid, dim3(kThreads), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 4>), grid, dim3(kThreads), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 1, SC>), grid, dim3(64 * waves_for(1)), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 2, SC>), grid, dim3(64 * waves_for(2)), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 3, SC>), grid, dim3(64 * waves_for(3)), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 4, SC>), grid, dim3(64 * waves_for(4)), 0, s, a); break;
     default: return COOPT_EINVAL;
   }
   int rc = coopt::check_launch("coopt_verify_attention");
@@ -504,13 +648,19 @@ int launch_rt(int RT, const AttnArgs& a, dim3 grid, hipStream_t s) {
   return coopt::check_launch("coopt_verify_attention/merge");
 }
 
+template <int D>
+int launch_d(bool int8, bool sc, int RT, const AttnArgs& a, dim3 grid, hipStream_t s) {
+  if (!int8) return launch_rt<D, false, false>(RT, a, grid, s);
+  return sc ? launch_rt<D, true, true>(RT, a, grid, s) : launch_rt<D, true, false>(RT, a, grid, s);
+}
+
 }  // namespace
 
 extern "C" size_t coopt_verify_attention_workspace(int B, int Hq, int Hkv, int D, int max_seqlen_q,
                                                    int max_seqlen_k) {
   if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv || max_seqlen_q <= 0 || max_seqlen_k <= 0) return 0;
   const int rmax = (Hq / Hkv) * max_seqlen_q;
-  const int split = choose_split(B, Hkv, max_seqlen_k);
+  const int split = choose_split(B, Hkv, max_seqlen_k, waves_for((rmax + 15) / 16));
   const int max_splits = (max_seqlen_k + split - 1) / split;
   return attn_ws_layout(B, Hkv, D, rmax, max_splits).total;
 }
@@ -563,6 +713,10 @@ extern "C" int coopt_verify_attention(int kv_dtype, const void* q, int64_t q_tok
     return COOPT_EWORKSPACE;
   }
   COOPT_REQUIRE(num_blocks > 0, "num_blocks must be positive");
+  // lanes address a page's rows with 32-bit byte offsets
+  COOPT_REQUIRE(c_tok_stride > 0 && (block_size * c_tok_stride + D) * (int8 ? 1 : 2) < (int64_t{1} << 31) &&
+                    (!int8 || (s_tok_stride >= 0 && block_size * s_tok_stride * 2 < (int64_t{1} << 31))),
+                "cache token stride too large for one page");
   coopt::clear_error();
 
   AttnArgs a{};
@@ -594,9 +748,9 @@ extern "C" int coopt_verify_attention(int kv_dtype, const void* q, int64_t q_tok
   a.out = static_cast<uint16_t*>(out);
   a.o_ts = o_tok_stride;
   a.o_hs = o_head_stride;
-  a.split = choose_split(B, Hkv, max_seqlen_k);
-  a.max_splits = (max_seqlen_k + a.split - 1) / a.split;
   a.rmax = G * max_seqlen_q;
+  a.split = choose_split(B, Hkv, max_seqlen_k, waves_for((a.rmax + 15) / 16));
+  a.max_splits = (max_seqlen_k + a.split - 1) / a.split;
   const AttnWs w = attn_ws_layout(B, Hkv, D, a.rmax, a.max_splits);
   char* base = static_cast<char*>(workspace);
   a.part_ml = reinterpret_cast<float2*>(base + w.ml_off);
@@ -605,6 +759,9 @@ extern "C" int coopt_verify_attention(int kv_dtype, const void* q, int64_t q_tok
   const int RT = (a.rmax + 15) / 16;
   const dim3 grid(a.max_splits, Hkv, B);
   auto s = static_cast<hipStream_t>(stream);
-  if (D == 128) return int8 ? launch_rt<128, true>(RT, a, grid, s) : launch_rt<128, false>(RT, a, grid, s);
-  return int8 ? launch_rt<64, true>(RT, a, grid, s) : launch_rt<64, false>(RT, a, grid, s);
+  // scale caches with consecutive tokens adjacent and 8-byte aligned groups of four
+  const bool sc = int8 && s_tok_stride == 1 && s_blk_stride % 4 == 0 && s_head_stride % 4 == 0 &&
+                  (reinterpret_cast<uintptr_t>(k_scale) & 7u) == 0 &&
+                  (reinterpret_cast<uintptr_t>(v_scale) & 7u) == 0;
+  return D == 128 ? launch_d<128>(int8, sc, RT, a, grid, s) : launch_d<64>(int8, sc, RT, a, grid, s);
 }

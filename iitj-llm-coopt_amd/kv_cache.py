@@ -72,11 +72,14 @@ def allocate_kv_cache(num_blocks: int, block_size: int, num_kv_heads: int, head_
         return (torch.zeros(shape, dtype=dtype, device=device),
                 torch.zeros(shape, dtype=dtype, device=device), None, None)
     if kv_cache_dtype == "int8":
-        sshape = shape[:-1]
+        # scales are [num_blocks, block_size, Hkv] views of head-major storage
+        # [num_blocks, Hkv, block_size]: a head's consecutive tokens are adjacent, so the
+        # attention kernel reads a lane's four scales with one load
+        sstore = (num_blocks, num_kv_heads, block_size)
         return (torch.zeros(shape, dtype=torch.int8, device=device),
                 torch.zeros(shape, dtype=torch.int8, device=device),
-                torch.zeros(sshape, dtype=torch.float16, device=device),
-                torch.zeros(sshape, dtype=torch.float16, device=device))
+                torch.zeros(sstore, dtype=torch.float16, device=device).transpose(1, 2),
+                torch.zeros(sstore, dtype=torch.float16, device=device).transpose(1, 2))
     raise ValueError(f"kv_cache_dtype must be 'auto' or 'int8', got {kv_cache_dtype!r}")
 
 
