@@ -318,6 +318,33 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
       return f16_to_f32(static_cast<uint16_t>(w[i >> 1] >> (16 * (i & 1))));
     };
 
+    // ---- V^T operands, built first: they do not depend on the scores, so their VALU work
+    // is scheduled alongside the score MFMAs in one basic block ----
+    u32x4_t va[kDt];
+    {
+      uint32_t vx[8][Raw::kVWords];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int w = 0; w < Raw::kVWords; ++w) vx[j][w] = INT8 ? (raw.v[j][w] ^ 0x80808080u) : raw.v[j][w];
+#pragma unroll
+      for (int dt = 0; dt < kDt; ++dt)
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const int j0 = 2 * e2, j1 = 2 * e2 + 1;  // keys of k-elements 2*e2, 2*e2+1
+          if constexpr (INT8) {
+            const int w = dt >> 2, byte = dt & 3;
+            const float s0 = scale_of(raw.vs[j0 >> 2], j0 & 3), s1 = scale_of(raw.vs[j1 >> 2], j1 & 3);
+            const float x0 = dequant_byte(vx[j0][w], byte, s0, -128.0f * s0);
+            const float x1 = dequant_byte(vx[j1][w], byte, s1, -128.0f * s1);
+            va[dt][e2] = pack_bf16x2(x0, x1);
+          } else {
+            const int w = dt >> 1;
+            va[dt][e2] = __builtin_amdgcn_perm(vx[j1][w], vx[j0][w], (dt & 1) ? 0x07060302u : 0x05040100u);
+          }
+        }
+    }
+
     // ---- scores: S^T = K . Q^T, K operands built per k-step ----
     f32x4_t acc[RT][2];
 #pragma unroll
@@ -350,81 +377,81 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
       }
     }
 
-    // ---- online softmax ----
+    // ---- online softmax (log2 domain) ----
+    // m_run is a per-row reference max that is raised only when a score exceeds it by more
+    // than kSlack: exponents are then at most 2^kSlack (exact range for bf16 P and the fp32
+    // sums), and the accumulators are rescaled only on those rare raises (one branch per
+    // tile, taken by the whole wave).
+    constexpr float kSlack = 8.0f;
+    float sv[RT][2][4];  // raw scores (the scale is applied in the exponent); masked -inf
+    if (open) {  // one uniform branch for the whole tile
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sv[rt][kt][i] = acc[rt][kt][i];
+    } else {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = kb + kt * 16 + grp * 4 + i;
+            sv[rt][kt][i] = (key > lim[rt] || key >= k_end) ? -INFINITY : acc[rt][kt][i];
+          }
+    }
+    float m_tile[RT];
+    bool raise_any = false;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      float tmax = fmaxf(fmaxf(fmaxf(sv[rt][0][0], sv[rt][0][1]), fmaxf(sv[rt][0][2], sv[rt][0][3])),
+                         fmaxf(fmaxf(sv[rt][1][0], sv[rt][1][1]), fmaxf(sv[rt][1][2], sv[rt][1][3])));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      m_tile[rt] = tmax * score_scale;
+      raise_any |= m_tile[rt] > m_run[rt] + kSlack;
+    }
+    if (__builtin_amdgcn_ballot_w64(raise_any)) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        const bool raise = m_tile[rt] > m_run[rt] + kSlack;
+        const float m_new = raise ? m_tile[rt] : m_run[rt];
+        const float alpha = raise ? exp2_fast(m_run[rt] - m_new) : 1.0f;  // 0 when raised from -inf
+        l_run[rt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < kDt; ++dt) o[rt][dt] *= alpha;
+        m_run[rt] = m_new;
+      }
+    }
     uint32_t pb[RT][4];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      float sv[2][4];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float s = acc[rt][kt][i] * score_scale;
-          if (open) {
-            sv[kt][i] = s;
-          } else {
-            const int key = kb + kt * 16 + grp * 4 + i;
-            sv[kt][i] = (key > lim[rt] || key >= k_end) ? -INFINITY : s;
-          }
-        }
-      float tmax = fmaxf(fmaxf(fmaxf(sv[0][0], sv[0][1]), fmaxf(sv[0][2], sv[0][3])),
-                         fmaxf(fmaxf(sv[1][0], sv[1][1]), fmaxf(sv[1][2], sv[1][3])));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const float m_new = fmaxf(m_run[rt], tmax);
-      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+      const float m_use = m_run[rt] == -INFINITY ? 0.0f : m_run[rt];
       float p[2][4], psum = 0.0f;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          p[kt][i] = exp2_fast(sv[kt][i] - m_use);
+          p[kt][i] = exp2_fast(fmaf(sv[rt][kt][i], score_scale, -m_use));
           psum += p[kt][i];
         }
-      // rescale only when some row's running max moved (alpha != 1 somewhere in the wave)
-      if (__builtin_amdgcn_ballot_w64(m_new != m_run[rt])) {
-        const float alpha = exp2_fast(m_run[rt] - m_use);
-        l_run[rt] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < kDt; ++dt) o[rt][dt] *= alpha;
-      }
       l_run[rt] += psum;
-      m_run[rt] = m_new;
       pb[rt][0] = pack_bf16x2(p[0][0], p[0][1]);
       pb[rt][1] = pack_bf16x2(p[0][2], p[0][3]);
       pb[rt][2] = pack_bf16x2(p[1][0], p[1][1]);
       pb[rt][3] = pack_bf16x2(p[1][2], p[1][3]);
     }
 
-    // ---- O^T += V^T . P^T, the V^T operand built in registers ----
-    uint32_t vx[8][Raw::kVWords];
+    // ---- O^T += V^T . P^T ----
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int w = 0; w < Raw::kVWords; ++w) vx[j][w] = INT8 ? (raw.v[j][w] ^ 0x80808080u) : raw.v[j][w];
-#pragma unroll
-    for (int dt = 0; dt < kDt; ++dt) {
-      u32x4_t va;
-#pragma unroll
-      for (int e2 = 0; e2 < 4; ++e2) {
-        const int j0 = 2 * e2, j1 = 2 * e2 + 1;  // keys of k-elements 2*e2, 2*e2+1
-        if constexpr (INT8) {
-          const int w = dt >> 2, byte = dt & 3;
-          const float s0 = scale_of(raw.vs[j0 >> 2], j0 & 3), s1 = scale_of(raw.vs[j1 >> 2], j1 & 3);
-          const float x0 = dequant_byte(vx[j0][w], byte, s0, -128.0f * s0);
-          const float x1 = dequant_byte(vx[j1][w], byte, s1, -128.0f * s1);
-          va[e2] = pack_bf16x2(x0, x1);
-        } else {
-          const int w = dt >> 1;
-          va[e2] = __builtin_amdgcn_perm(vx[j1][w], vx[j0][w], (dt & 1) ? 0x07060302u : 0x05040100u);
-        }
-      }
+    for (int dt = 0; dt < kDt; ++dt)
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
         const u32x4_t pbv = {pb[rt][0], pb[rt][1], pb[rt][2], pb[rt][3]};
-        o[rt][dt] = mfma_bf16(va, pbv, o[rt][dt]);
+        o[rt][dt] = mfma_bf16(va[dt], pbv, o[rt][dt]);
       }
-    }
   };
 
   // ---- the wave's tiles: double-buffered (the next tile's loads in flight while the current

@@ -66,18 +66,23 @@ def dequantize(q: torch.Tensor, scale, bits: int, dtype=torch.bfloat16):
 
 def allocate_kv_cache(num_blocks: int, block_size: int, num_kv_heads: int, head_dim: int,
                       kv_cache_dtype: str = "auto", device="cuda", dtype=torch.bfloat16):
-    """One layer's (k_cache, v_cache, k_scale, v_scale); the scales are None for "auto"."""
-    shape = (num_blocks, block_size, num_kv_heads, head_dim)
+    """One layer's (k_cache, v_cache, k_scale, v_scale); the scales are None for "auto".
+
+    Every tensor has the reference's logical shape -- caches [num_blocks, block_size, Hkv, D]
+    (engine/model.py:148-155), INT8 scales [num_blocks, block_size, Hkv] -- as a view of
+    head-major storage [num_blocks, Hkv, block_size, ...]: one head's tokens of a block are
+    adjacent in HBM, so the verify-attention kernel reads each (block, head) as one contiguous
+    run (16 tokens x D codes) instead of D-sized pieces strided by Hkv * D.  The kernels take
+    any strides, so caches in the reference's token-major layout work too.
+    """
+    store = (num_blocks, num_kv_heads, block_size, head_dim)
     if kv_cache_dtype == "auto":
-        return (torch.zeros(shape, dtype=dtype, device=device),
-                torch.zeros(shape, dtype=dtype, device=device), None, None)
+        return (torch.zeros(store, dtype=dtype, device=device).transpose(1, 2),
+                torch.zeros(store, dtype=dtype, device=device).transpose(1, 2), None, None)
     if kv_cache_dtype == "int8":
-        # scales are [num_blocks, block_size, Hkv] views of head-major storage
-        # [num_blocks, Hkv, block_size]: a head's consecutive tokens are adjacent, so the
-        # attention kernel reads a lane's four scales with one load
         sstore = (num_blocks, num_kv_heads, block_size)
-        return (torch.zeros(shape, dtype=torch.int8, device=device),
-                torch.zeros(shape, dtype=torch.int8, device=device),
+        return (torch.zeros(store, dtype=torch.int8, device=device).transpose(1, 2),
+                torch.zeros(store, dtype=torch.int8, device=device).transpose(1, 2),
                 torch.zeros(sstore, dtype=torch.float16, device=device).transpose(1, 2),
                 torch.zeros(sstore, dtype=torch.float16, device=device).transpose(1, 2))
     raise ValueError(f"kv_cache_dtype must be 'auto' or 'int8', got {kv_cache_dtype!r}")

@@ -81,7 +81,7 @@ def test_kv_write_skips_padding_and_out_of_pool_slots(dev):
     for mode in ("auto", "int8"):
         kc, vc, ks, vs = M.allocate_kv_cache(NB, BS, H, D, mode, device=dev)
         M.reshape_and_cache_flash(k, k, kc, vc, slots, mode, ks, vs)
-        written = kc.view(NB * BS, H * D).ne(0).any(1).nonzero().flatten().tolist()
+        written = kc.reshape(NB * BS, H * D).ne(0).any(1).nonzero().flatten().tolist()
         assert written == [5, 7], (mode, written)
 
 
