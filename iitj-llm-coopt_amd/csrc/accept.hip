@@ -324,6 +324,33 @@ __device__ __forceinline__ RowStat combine_row(const Args& a, int b, int slot, b
   return rs;
 }
 
+// Sampling statistics of every row slot of sequence b, one wave per row: lanes read the chunk
+// partials in parallel, then (max, sum * exp(m_c - max)) reduce across the wave.  The sum
+// follows the chunk order of combine_row's serial loop only up to fp64 rounding.
+__device__ __forceinline__ void combine_rows_waves(const Args& a, int b, int nrow_t, int nrow_d,
+                                                   RowStat* rows) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nrows = nrow_t + nrow_d;
+  for (int r = wave; r < nrows; r += kThreads / 64) {
+    const int slot = r < nrow_t ? r : (a.gmax + 1) + (r - nrow_t);
+    const Partial1* p = a.ws.part1 + (static_cast<int64_t>(b) * (2 * a.gmax + 1) + slot) * a.L.nch1;
+    float m = -INFINITY;
+    for (int c = lane; c < a.L.nch1; c += 64) m = fmaxf(m, p[c].m);
+    m = wave_max_f32(m);
+    double s = 0.0;
+    for (int c = lane; c < a.L.nch1; c += 64) {
+      const Partial1 q = p[c];
+      if (q.s > 0.0) s += q.s * exp(static_cast<double>(q.m) - static_cast<double>(m));
+    }
+    s = wave_sum_f64(s);
+    if (lane == 0) {
+      rows[slot].m = m;
+      rows[slot].argmax = -1;
+      rows[slot].s = s;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // Launch 2 (greedy): argmax prefix rule, one block per sequence.
 // ---------------------------------------------------------------------------------------
@@ -426,36 +453,45 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(Args a) {
   __shared__ RowStat rows[kMaxSlots];
   __shared__ Decision sdec;
   __shared__ double shd[4], shd2[4];
+  __shared__ float sh_p[64], sh_q[64];  // p_i[d_i], q_i[d_i]
   const int c = blockIdx.x, b = blockIdx.y;
   const int g = gamma_of(a, b);
   const int tid = threadIdx.x;
   const int nrow_t = g + 1, nrow_d = a.draft_probs ? 0 : g;
-  if (tid < nrow_t + nrow_d) {
-    const int slot = tid < nrow_t ? tid : (a.gmax + 1) + (tid - nrow_t);
-    rows[slot] = combine_row(a, b, slot, false);
+  const int32_t* d = a.dtok + static_cast<int64_t>(b) * a.gmax;
+  // The logits at the draft tokens do not depend on the row statistics: one lane per
+  // (row, draft) issues its load before the combination below.
+  const bool want_t = tid < g, want_d = tid >= 64 && tid < 64 + g;
+  const int di = want_t ? tid : tid - 64;
+  int tok = -1;
+  float x = 0.0f;
+  if (want_t || want_d) {
+    tok = d[di];
+    if (tok >= 0 && tok < a.V) {
+      if (want_t) x = ld<BF16>(a.tgt, tgt_row(a, b, di), a.tgt_stride, tok) * a.inv_t;
+      else if (a.draft_probs) x = static_cast<const float*>(a.drf)[drf_row(a, b, di) * a.drf_stride + tok];
+      else x = ld<BF16>(a.drf, drf_row(a, b, di), a.drf_stride, tok) * a.inv_t;
+    }
+  }
+  combine_rows_waves(a, b, nrow_t, nrow_d, rows);
+  __syncthreads();
+  if (want_t || want_d) {
+    const bool valid = tok >= 0 && tok < a.V;
+    if (want_t) {
+      sh_p[di] = valid ? prob_at(x, rows[di].m, rows[di].s) : 0.0f;
+    } else {
+      const RowStat& rq = rows[a.gmax + 1 + di];
+      sh_q[di] = !valid ? 1.0f : (a.draft_probs ? x : prob_at(x, rq.m, rq.s));
+    }
   }
   __syncthreads();
   if (tid == 0) {
-    const int32_t* d = a.dtok + static_cast<int64_t>(b) * a.gmax;
     const float* u = a.u_acc + static_cast<int64_t>(b) * a.gmax;
     int k = g, mode = kModeBonus;
     float margin = INFINITY;
     for (int i = 0; i < g; ++i) {
-      const int tok = d[i];
-      float ratio = 0.0f;
-      if (tok >= 0 && tok < a.V) {
-        const float xt = ld<BF16>(a.tgt, tgt_row(a, b, i), a.tgt_stride, tok) * a.inv_t;
-        const float p = prob_at(xt, rows[i].m, rows[i].s);
-        float q;
-        if (a.draft_probs) {
-          q = static_cast<const float*>(a.drf)[drf_row(a, b, i) * a.drf_stride + tok];
-        } else {
-          const float xq = ld<BF16>(a.drf, drf_row(a, b, i), a.drf_stride, tok) * a.inv_t;
-          const RowStat& rq = rows[a.gmax + 1 + i];
-          q = prob_at(xq, rq.m, rq.s);
-        }
-        ratio = fminf(p / fmaxf(q, 1e-20f), 1.0f);
-      }
+      // an out-of-vocabulary draft token has ratio 0 and is rejected (p = 0 above)
+      const float ratio = fminf(sh_p[i] / fmaxf(sh_q[i], 1e-20f), 1.0f);
       margin = fminf(margin, fabsf(u[i] - ratio));
       if (u[i] >= ratio) {
         k = i;
@@ -605,8 +641,27 @@ __global__ __launch_bounds__(kThreads) void select_kernel(Args a) {
   const int tlo = min(chi, clo + tid * per * 8);
   const int thi = min(chi, tlo + per * 8);
   const bool vec = a.vec_t && (dec.mode == kModeBonus || a.vec_d);
+  // The first kKeep groups of the thread's run stay in registers for the claim pass below.
+  constexpr int kKeep = 4;
+  float keep[kKeep][8];
   double local = 0.0;
-  for (int j = tlo; j < thi; j += 8) {
+#pragma unroll
+  for (int gi = 0; gi < kKeep; ++gi) {
+    const int j = tlo + gi * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) keep[gi][e] = 0.0f;
+    if (j < thi) {
+      float w[8], p[8];
+      const int n = min(8, thi - j);
+      wr.at(j, n, vec && n == 8, w, p);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        keep[gi][e] = e < n ? (use_p ? p[e] : w[e]) : 0.0f;
+        local += static_cast<double>(keep[gi][e]);
+      }
+    }
+  }
+  for (int j = tlo + kKeep * 8; j < thi; j += 8) {
     float w[8], p[8];
     const int n = min(8, thi - j);
     wr.at(j, n, vec && n == 8, w, p);
@@ -627,12 +682,20 @@ __global__ __launch_bounds__(kThreads) void select_kernel(Args a) {
     double run = acc + start;
     int last_pos = -1;
     double lo_edge = run, hi_edge = run;
-    for (int j = tlo; j < thi && tok < 0; j += 8) {
-      float w[8], p[8];
+    for (int j = tlo, gi = 0; j < thi && tok < 0; j += 8, ++gi) {
+      float v[8];
       const int n = min(8, thi - j);
-      wr.at(j, n, vec && n == 8, w, p);
+      if (gi < kKeep) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = keep[gi < kKeep ? gi : 0][e];
+      } else {
+        float w[8], p[8];
+        wr.at(j, n, vec && n == 8, w, p);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = use_p ? p[e] : w[e];
+      }
       for (int e = 0; e < n; ++e) {
-        const double wj = static_cast<double>(use_p ? p[e] : w[e]);
+        const double wj = static_cast<double>(v[e]);
         if (wj > 0.0) last_pos = j + e;
         const double nxt = run + wj;
         if (nxt > tau && wj > 0.0) {

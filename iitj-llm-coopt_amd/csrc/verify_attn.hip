@@ -44,9 +44,9 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;  // merge kernel
 
-// Waves per attention block: 8 (one block per CU at two waves per SIMD) while the
-// accumulators fit 128 VGPRs-per-row-tile budgets (RT <= 2), else 4.
-constexpr int waves_for(int RT) { return RT <= 2 ? 8 : 4; }
+// Waves per attention block: 8 (one block per CU at two waves per SIMD, i.e. at most 256
+// registers per lane) while the accumulators and two tile buffers fit that (RT <= 3), else 4.
+constexpr int waves_for(int RT) { return RT <= 3 ? 8 : 4; }
 constexpr int kTileKeys = 32;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -125,14 +125,14 @@ __device__ __forceinline__ void load_words(const unsigned char* p, uint32_t* dst
 
 // RT row tiles of 16; SC: the scale caches hold consecutive tokens contiguously (token
 // stride 1), so a lane's four scales of a sub-tile are one 8-byte load; DB: double-buffer
-// the wave's tiles in registers (RT <= 2; larger row counts need the registers for
-// accumulators).
+// the wave's tiles in registers (RT <= 2, and RT 3 with the smaller INT8 tiles; the other
+// shapes need the registers for accumulators).
 template <int D, bool INT8, int RT, bool SC>
 __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(AttnArgs a) {
   using Raw = RawTile<D, INT8>;
   constexpr int kWaves = waves_for(RT);
   constexpr int kBlock = 64 * kWaves;
-  constexpr bool DB = RT <= 2;
+  constexpr bool DB = RT <= 2 || (INT8 && RT == 3);
   constexpr int kKs = D / 32;   // k-steps of the score MFMA
   constexpr int kDt = D / 16;   // d-tiles of the output = V elements per lane per key
   constexpr int kElt = Raw::kElt;
