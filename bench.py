@@ -181,6 +181,71 @@ def kv_write_case(torch, M, dev, T, seed):
     return rate({"tokens": T}, nbytes, *time_launches(torch, dev, fn))
 
 
+def kv_swap_case(torch, M, dev, seed, tokens=4096, bits=8):
+    """Swap codec, one launch: gather + INT8-quantise one layer's K blocks of a `tokens`-token
+    sequence (bf16 cache, head-major storage, blocks a seeded permutation of a 4096-block
+    pool) into the contiguous swap format."""
+    import numpy as np
+
+    NB, bs, Hkv, D = 4096, 16, 8, 128
+    cache, _, _, _ = M.allocate_kv_cache(NB, bs, Hkv, D, "auto", device=dev)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    cache.copy_(torch.randn(cache.shape, generator=g, device=dev).to(torch.bfloat16))
+    nb = tokens // bs
+    blocks = torch.from_numpy(np.random.default_rng(seed).permutation(NB)[:nb].astype(np.int64)).to(dev)
+    q, sc = M.swap_out_blocks(cache, blocks, bits)
+
+    def fn():
+        M.swap_out_blocks(cache, blocks, bits, out=q, out_scale=sc)
+
+    nbytes = nb * bs * Hkv * (D * 2 + D * bits // 8 + 2) + nb * 8
+    return rate({"tokens": tokens, "bits": bits}, nbytes, *time_launches(torch, dev, fn))
+
+
+def kv_tier_case(torch, M, dev, seed, tokens=4096, layers=32):
+    """KVTierManager swap_out + swap_in of one `tokens`-token sequence of a Llama-3.1-8B-shaped
+    target (32 layers, bf16 caches, INT8 tier): codec launches plus the PCIe copies to and from
+    pinned host memory, host-timed around synchronisation (PCIe-inclusive)."""
+    import types
+
+    import numpy as np
+
+    NB, bs, Hkv, D = 2 * tokens // 16, 16, 8, 128
+    kc, vc = [], []
+    g = torch.Generator(device=dev).manual_seed(seed)
+    for _ in range(layers):
+        a, b, _, _ = M.allocate_kv_cache(NB, bs, Hkv, D, "auto", device=dev)
+        a.copy_(torch.randn(a.shape, generator=g, device=dev).to(torch.bfloat16))
+        b.copy_(torch.randn(b.shape, generator=g, device=dev).to(torch.bfloat16))
+        kc.append(a)
+        vc.append(b)
+    cfg = types.SimpleNamespace(num_hidden_layers=layers, num_key_value_heads=Hkv, head_dim=D)
+    eng = types.SimpleNamespace(target=types.SimpleNamespace(k_cache=kc, v_cache=vc, cfg=cfg),
+                                bm=M.BlockManager(NB, bs, free_order=np.random.default_rng(seed).permutation(NB)),
+                                counters={})
+    tm = M.KVTierManager(eng, cpu_gb=64.0, bits=8)
+    seq = types.SimpleNamespace(seq_id=0, num_computed=tokens)
+    times = []
+    for it in range(4):
+        eng.bm.ensure(0, tokens)
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        tm.swap_out(seq)
+        eng.bm.free(0)
+        tm.swap_in(seq)
+        torch.cuda.synchronize(dev)
+        if it:
+            times.append(time.perf_counter() - t0)
+        eng.bm.free(0)
+    avg = sum(times) / len(times)
+    host_bytes = 2 * tm.estimate_bytes(tokens, 8)   # out and back over PCIe
+    return {"tokens": tokens, "layers": layers, "bits": 8, "host_bytes": host_bytes,
+            "avg_us": avg * 1e6, "median_us": sorted(times)[len(times) // 2] * 1e6,
+            "GB_s": host_bytes / avg / 1e9, "frac": None,
+            "note": "PCIe-inclusive: swap_out (64 codec launches, one D2H copy) + swap_in "
+                    "(one H2D copy, 64 codec launches), host-timed"}
+
+
 def copy_case(torch, M, dev, seed):
     """A plain streaming kernel of known size (torch.neg over 1 GiB of bf16: 1 GiB read,
     1 GiB written): the calibration for FETCH_SIZE / WRITE_SIZE and a practical HBM ceiling."""
@@ -217,6 +282,8 @@ KERNEL_CASES = {
     # config 2 (T=1280) and a sustained-bandwidth size
     "kv_write_t1280": lambda t, M, d, s: kv_write_case(t, M, d, 1280, s),
     "kv_write_t65536": lambda t, M, d, s: kv_write_case(t, M, d, 65536, s),
+    "kv_swap_out_4096tok": lambda t, M, d, s: kv_swap_case(t, M, d, s),
+    "kv_tier_roundtrip": lambda t, M, d, s: kv_tier_case(t, M, d, s),
     "copy": lambda t, M, d, s: copy_case(t, M, d, s),
 }
 
@@ -226,7 +293,8 @@ def run_kernel_cases(torch, M, dev, names, seed):
     for name in names:
         out[name] = KERNEL_CASES[name](torch, M, dev, seed)
         r = out[name]
-        log(f"{name}: {r['avg_us']:.1f} us/call, {r['GB_s']:.0f} GB/s ({r['frac'] * 100:.1f}% of 8 TB/s)")
+        frac = "" if r["frac"] is None else f" ({r['frac'] * 100:.1f}% of 8 TB/s)"
+        log(f"{name}: {r['avg_us']:.1f} us/call, {r['GB_s']:.0f} GB/s{frac}")
         torch.cuda.empty_cache()
     return out
 

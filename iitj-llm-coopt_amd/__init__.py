@@ -4,6 +4,7 @@ gfx950 HIP kernels (libcoopt_amd.so, C ABI in include/coopt_amd.h) behind the Py
 surface of mohsinmubarak/iitj-llm-coopt's engine:
   spec_decode   sample / verify / batched accept      (engine/spec_decode.py)
   kv_cache      quantize / dequantize / paged write   (engine/kv_tier_manager.py, model.py:242)
+  kv_tier       KVTierManager swap_out / swap_in      (engine/kv_tier_manager.py:44-131)
   attention     flash_attn_varlen_func-compatible paged verification attention (model.py:244)
   block_manager BlockManager slot / block-table contract (engine/block_manager.py)
   batch         WorkItem / Batch / build_batch varlen layout (engine/batch.py)
@@ -14,11 +15,12 @@ from .attention import flash_attn_varlen_func, paged_attention
 from .batch import Batch, WorkItem, build_batch, build_padded_batch
 from .block_manager import BlockManager, OutOfBlocks
 from .kv_cache import allocate_kv_cache, dequantize, quantize, reshape_and_cache_flash
+from .kv_tier import KVTierManager, SwappedKV, swap_in_blocks, swap_out_blocks
 from .spec_decode import AcceptResult, accept, sample, softmax, verify
 
 __all__ = [
     "flash_attn_varlen_func", "paged_attention", "Batch", "WorkItem", "build_batch",
     "build_padded_batch", "BlockManager", "OutOfBlocks", "allocate_kv_cache", "dequantize",
     "quantize", "reshape_and_cache_flash", "AcceptResult", "accept", "sample", "softmax",
-    "verify",
+    "verify", "KVTierManager", "SwappedKV", "swap_in_blocks", "swap_out_blocks",
 ]

@@ -198,6 +198,211 @@ __global__ __launch_bounds__(256) void dequantize_kernel(const uint8_t* __restri
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Swap codec (engine/kv_tier_manager.py:93-101 and :113-119).  swap_out gathers whole cache
+// blocks by id and quantises them into a contiguous [n_ids, block_size, Hkv, D(/2)] buffer --
+// quantize(cache[blocks], bits) in one launch; swap_in dequantises such a buffer and scatters
+// it into blocks -- cache[blocks] = dequantize(q, s, bits, cache.dtype).  G = D/8 lanes per
+// (token, head) vector, 8 elements each.  An INT8 cache already holds codes and scales: its
+// blocks are copied as they are (bits 8 only).  Ids outside [0, num_blocks) read as zeros
+// (swap_out) or are skipped (swap_in).
+// ---------------------------------------------------------------------------------------
+template <int BITS>
+struct SwapElt {  // bytes of 8 elements in the swapped format
+  static constexpr int kBytes = BITS == 16 ? 16 : (BITS == 8 ? 8 : 4);
+};
+
+template <int G, int BITS, bool SRC8>
+__global__ __launch_bounds__(256) void swap_out_kernel(
+    const void* __restrict__ cache, int64_t c_bs, int64_t c_ts, int64_t c_hs,
+    const uint16_t* __restrict__ cscale, int64_t s_bs, int64_t s_ts, int64_t s_hs,
+    const int64_t* __restrict__ ids, int nid, int bs, int Hkv, int64_t num_blocks,
+    unsigned char* __restrict__ q, uint16_t* __restrict__ scale) {
+  constexpr int D = G * 8;
+  constexpr int kOut = SwapElt<BITS>::kBytes;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int c = static_cast<int>(gid % G);
+  const int64_t vec = gid / G;
+  if (vec >= static_cast<int64_t>(nid) * bs * Hkv) return;  // whole groups leave together
+  const int per_blk = bs * Hkv;
+  const int i = static_cast<int>(vec / per_blk);
+  const int rem = static_cast<int>(vec % per_blk);
+  const int t = rem / Hkv, h = rem % Hkv;
+  const int64_t blk = ids[i];
+  unsigned char* qo = q + vec * (D / 8) * kOut + c * kOut;
+  if (blk < 0 || blk >= num_blocks) {
+    if constexpr (kOut == 16) *reinterpret_cast<uint4*>(qo) = make_uint4(0, 0, 0, 0);
+    else if constexpr (kOut == 8) *reinterpret_cast<uint2*>(qo) = make_uint2(0, 0);
+    else *reinterpret_cast<uint32_t*>(qo) = 0;
+    if (BITS != 16 && c == 0) scale[vec] = 0;
+    return;
+  }
+  const int64_t off = blk * c_bs + t * c_ts + h * c_hs + c * 8;
+  if constexpr (SRC8) {
+    *reinterpret_cast<uint2*>(qo) = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(cache) + off);
+    if (c == 0) scale[vec] = cscale[blk * s_bs + t * s_ts + h * s_hs];
+  } else {
+    const uint4 x = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(cache) + off);
+    if constexpr (BITS == 16) {
+      *reinterpret_cast<uint4*>(qo) = x;
+    } else {
+      constexpr int QMAX = BITS == 8 ? 127 : 7;
+      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+      uint32_t amax = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) amax = max(amax, max(w[e] & 0x7fffu, (w[e] >> 16) & 0x7fffu));
+      amax = group_max_u32<G>(amax);
+      const float s32 = quant_scale<QMAX>(bf16_to_f32(static_cast<uint16_t>(amax)));
+      int code[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        code[e] = quant_code<QMAX>(bf16_to_f32(static_cast<uint16_t>(w[e / 2] >> (16 * (e & 1)))), s32);
+      if constexpr (BITS == 8) {
+        uint32_t b[2] = {0, 0};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) b[e / 4] |= (static_cast<uint32_t>(code[e]) & 0xffu) << (8 * (e & 3));
+        *reinterpret_cast<uint2*>(qo) = make_uint2(b[0], b[1]);
+      } else {  // even element in the low nibble, odd in the high one, both offset by +8
+        uint32_t b = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          b |= ((static_cast<uint32_t>(code[2 * j] + 8) | (static_cast<uint32_t>(code[2 * j + 1] + 8) << 4)) & 0xffu) << (8 * j);
+        *reinterpret_cast<uint32_t*>(qo) = b;
+      }
+      if (c == 0) scale[vec] = f32_to_f16(s32);
+    }
+  }
+}
+
+template <int G, int BITS, bool DST8>
+__global__ __launch_bounds__(256) void swap_in_kernel(
+    const unsigned char* __restrict__ q, const uint16_t* __restrict__ scale,
+    const int64_t* __restrict__ ids, int nid, int bs, int Hkv, int64_t num_blocks,
+    void* __restrict__ cache, int64_t c_bs, int64_t c_ts, int64_t c_hs,
+    uint16_t* __restrict__ cscale, int64_t s_bs, int64_t s_ts, int64_t s_hs) {
+  constexpr int D = G * 8;
+  constexpr int kIn = SwapElt<BITS>::kBytes;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int c = static_cast<int>(gid % G);
+  const int64_t vec = gid / G;
+  if (vec >= static_cast<int64_t>(nid) * bs * Hkv) return;
+  const int per_blk = bs * Hkv;
+  const int i = static_cast<int>(vec / per_blk);
+  const int rem = static_cast<int>(vec % per_blk);
+  const int t = rem / Hkv, h = rem % Hkv;
+  const int64_t blk = ids[i];
+  if (blk < 0 || blk >= num_blocks) return;
+  const unsigned char* qi = q + vec * (D / 8) * kIn + c * kIn;
+  const int64_t off = blk * c_bs + t * c_ts + h * c_hs + c * 8;
+  if constexpr (DST8) {
+    *reinterpret_cast<uint2*>(static_cast<int8_t*>(cache) + off) = *reinterpret_cast<const uint2*>(qi);
+    if (c == 0) cscale[blk * s_bs + t * s_ts + h * s_hs] = scale[vec];
+  } else if constexpr (BITS == 16) {
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(cache) + off) = *reinterpret_cast<const uint4*>(qi);
+  } else {
+    const float s = f16_to_f32(scale[vec]);
+    int code[8];
+    if constexpr (BITS == 8) {
+      const uint2 r = *reinterpret_cast<const uint2*>(qi);
+      const uint32_t b[2] = {r.x, r.y};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) code[e] = static_cast<int8_t>((b[e / 4] >> (8 * (e & 3))) & 0xffu);
+    } else {
+      const uint32_t b = *reinterpret_cast<const uint32_t*>(qi);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t byte = (b >> (8 * j)) & 0xffu;
+        code[2 * j] = static_cast<int>(byte & 0x0fu) - 8;
+        code[2 * j + 1] = static_cast<int>(byte >> 4) - 8;
+      }
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)  // dtype(float(code) * float(scale)); the product is exact
+      o[e] = f32_to_bf16(static_cast<float>(code[2 * e]) * s) |
+             (static_cast<uint32_t>(f32_to_bf16(static_cast<float>(code[2 * e + 1]) * s)) << 16);
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(cache) + off) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+template <int BITS, bool I8>
+int launch_swap(bool out, int G, const void* cache, int64_t c_bs, int64_t c_ts, int64_t c_hs,
+                void* cscale, int64_t s_bs, int64_t s_ts, int64_t s_hs, const int64_t* ids, int nid,
+                int bs, int Hkv, int64_t num_blocks, void* q, void* scale, hipStream_t stream) {
+  const int64_t threads = static_cast<int64_t>(nid) * bs * Hkv * G;
+  const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+#define COOPT_SW(GV)                                                                              \
+  case GV:                                                                                        \
+    if (out)                                                                                      \
+      hipLaunchKernelGGL((swap_out_kernel<GV, BITS, I8>), grid, dim3(256), 0, stream, cache, c_bs, \
+                         c_ts, c_hs, static_cast<const uint16_t*>(cscale), s_bs, s_ts, s_hs, ids, nid, \
+                         bs, Hkv, num_blocks, static_cast<unsigned char*>(q),                    \
+                         static_cast<uint16_t*>(scale));                                         \
+    else                                                                                          \
+      hipLaunchKernelGGL((swap_in_kernel<GV, BITS, I8>), grid, dim3(256), 0, stream,             \
+                         static_cast<const unsigned char*>(q), static_cast<const uint16_t*>(scale), \
+                         ids, nid, bs, Hkv, num_blocks, const_cast<void*>(cache), c_bs, c_ts, c_hs, \
+                         static_cast<uint16_t*>(cscale), s_bs, s_ts, s_hs);                      \
+    break;
+  switch (G) {
+    COOPT_SW(1)
+    COOPT_SW(2)
+    COOPT_SW(4)
+    COOPT_SW(8)
+    COOPT_SW(16)
+    COOPT_SW(32)
+    COOPT_SW(64)
+    default:
+      return COOPT_EINVAL;
+  }
+#undef COOPT_SW
+  return coopt::check_launch(out ? "coopt_kv_swap_out" : "coopt_kv_swap_in");
+}
+
+// Argument checks shared by swap_out / swap_in; returns COOPT_OK or an error code.
+int check_swap(int bits, int cache_dtype, const void* cache, int64_t c_bs, int64_t c_ts,
+               int64_t c_hs, const void* cscale, const int64_t* ids, int nid, int bs, int Hkv,
+               int D, int64_t num_blocks, const void* q, const void* scale) {
+  COOPT_REQUIRE(bits == 16 || bits == 8 || bits == 4, "bits must be 16, 8 or 4");
+  COOPT_REQUIRE(cache_dtype == COOPT_DT_BF16 || cache_dtype == COOPT_DT_I8,
+                "cache_dtype must be COOPT_DT_BF16 or COOPT_DT_I8");
+  COOPT_REQUIRE(cache_dtype == COOPT_DT_BF16 || bits == 8, "an INT8 cache swaps at 8 bits");
+  COOPT_REQUIRE(nid >= 0 && bs > 0 && Hkv > 0 && num_blocks > 0, "bad sizes");
+  COOPT_REQUIRE(D % 8 == 0 && D >= 8 && D <= 512 && ((D / 8) & (D / 8 - 1)) == 0,
+                "D must be 8 * a power of two, at most 512");
+  if (nid == 0) return COOPT_OK;
+  COOPT_REQUIRE(cache && ids && q && (bits == 16 || scale), "null pointer");
+  const int qalign = bits == 16 ? 16 : (bits == 8 ? 8 : 4);
+  COOPT_REQUIRE((reinterpret_cast<uintptr_t>(q) % qalign) == 0, "swap buffer misaligned");
+  if (cache_dtype == COOPT_DT_I8) {
+    COOPT_REQUIRE(cscale != nullptr, "INT8 cache needs its scale cache");
+    COOPT_REQUIRE((reinterpret_cast<uintptr_t>(cache) & 7u) == 0 && c_bs % 8 == 0 && c_ts % 8 == 0 &&
+                      c_hs % 8 == 0, "INT8 cache rows must be 8-byte aligned");
+  } else {
+    COOPT_REQUIRE(coopt::aligned16(cache) && c_bs % 8 == 0 && c_ts % 8 == 0 && c_hs % 8 == 0,
+                  "bf16 cache rows must be 16-byte aligned");
+  }
+  return COOPT_OK;
+}
+
+int dispatch_swap(bool out, int bits, int cache_dtype, const void* cache, int64_t c_bs, int64_t c_ts,
+                  int64_t c_hs, void* cscale, int64_t s_bs, int64_t s_ts, int64_t s_hs,
+                  const int64_t* ids, int nid, int bs, int Hkv, int D, int64_t num_blocks, void* q,
+                  void* scale, hipStream_t s) {
+  const int G = D / 8;
+  if (cache_dtype == COOPT_DT_I8)
+    return launch_swap<8, true>(out, G, cache, c_bs, c_ts, c_hs, cscale, s_bs, s_ts, s_hs, ids, nid, bs,
+                                Hkv, num_blocks, q, scale, s);
+  if (bits == 16)
+    return launch_swap<16, false>(out, G, cache, c_bs, c_ts, c_hs, cscale, s_bs, s_ts, s_hs, ids, nid,
+                                  bs, Hkv, num_blocks, q, scale, s);
+  if (bits == 8)
+    return launch_swap<8, false>(out, G, cache, c_bs, c_ts, c_hs, cscale, s_bs, s_ts, s_hs, ids, nid, bs,
+                                 Hkv, num_blocks, q, scale, s);
+  return launch_swap<4, false>(out, G, cache, c_bs, c_ts, c_hs, cscale, s_bs, s_ts, s_hs, ids, nid, bs,
+                               Hkv, num_blocks, q, scale, s);
+}
+
 }  // namespace
 
 extern "C" int coopt_kv_write(int cache_dtype, const void* k, const void* v, int64_t k_tok_stride,
@@ -312,4 +517,37 @@ extern "C" int coopt_dequantize(int bits, const void* q, const void* scale, int6
   }
 #undef COOPT_DQ
   return coopt::check_launch("coopt_dequantize");
+}
+
+extern "C" int coopt_kv_swap_out(int bits, int cache_dtype, const void* cache,
+                                 int64_t c_blk_stride, int64_t c_tok_stride, int64_t c_head_stride,
+                                 const void* cache_scale, int64_t s_blk_stride,
+                                 int64_t s_tok_stride, int64_t s_head_stride,
+                                 const int64_t* block_ids, int num_ids, int block_size, int Hkv,
+                                 int D, int64_t num_blocks, void* q, void* scale,
+                                 coopt_stream_t stream) {
+  const int rc = check_swap(bits, cache_dtype, cache, c_blk_stride, c_tok_stride, c_head_stride,
+                            cache_scale, block_ids, num_ids, block_size, Hkv, D, num_blocks, q, scale);
+  if (rc != COOPT_OK || num_ids == 0) return rc;
+  coopt::clear_error();
+  return dispatch_swap(true, bits, cache_dtype, cache, c_blk_stride, c_tok_stride, c_head_stride,
+                       const_cast<void*>(cache_scale), s_blk_stride, s_tok_stride, s_head_stride,
+                       block_ids, num_ids, block_size, Hkv, D, num_blocks, q, scale,
+                       static_cast<hipStream_t>(stream));
+}
+
+extern "C" int coopt_kv_swap_in(int bits, int cache_dtype, const void* q, const void* scale,
+                                const int64_t* block_ids, int num_ids, int block_size, int Hkv,
+                                int D, int64_t num_blocks, void* cache, int64_t c_blk_stride,
+                                int64_t c_tok_stride, int64_t c_head_stride, void* cache_scale,
+                                int64_t s_blk_stride, int64_t s_tok_stride, int64_t s_head_stride,
+                                coopt_stream_t stream) {
+  const int rc = check_swap(bits, cache_dtype, cache, c_blk_stride, c_tok_stride, c_head_stride,
+                            cache_scale, block_ids, num_ids, block_size, Hkv, D, num_blocks, q, scale);
+  if (rc != COOPT_OK || num_ids == 0) return rc;
+  coopt::clear_error();
+  return dispatch_swap(false, bits, cache_dtype, cache, c_blk_stride, c_tok_stride, c_head_stride,
+                       cache_scale, s_blk_stride, s_tok_stride, s_head_stride, block_ids, num_ids,
+                       block_size, Hkv, D, num_blocks, const_cast<void*>(q), const_cast<void*>(scale),
+                       static_cast<hipStream_t>(stream));
 }

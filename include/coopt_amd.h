@@ -24,6 +24,8 @@
  *                           batched as at engine/engine.py:421-446
  *   coopt_quantize /        kv_tier_manager.quantize /     engine/kv_tier_manager.py:21-41
  *   coopt_dequantize        dequantize
+ *   coopt_kv_swap_out /     quantize(cache[blocks], bits) / engine/kv_tier_manager.py:93-101
+ *   coopt_kv_swap_in        cache[blocks] = dequantize(..)  engine/kv_tier_manager.py:113-119
  *   coopt_softmax           torch.softmax(logits / T)       engine/spec_decode.py:16
  *   coopt_rms_norm          vLLM rms_norm / fused_add_rms_norm  engine/model.py:234, 236, 249, 254
  *   coopt_rope              vLLM rotary_embedding (neox)    engine/model.py:239
@@ -99,6 +101,35 @@ int coopt_quantize(int bits, int in_dtype, const void* x, int64_t rows, int D,
                    void* q, void* scale, coopt_stream_t stream);
 int coopt_dequantize(int bits, const void* q, const void* scale, int64_t rows, int D,
                      int out_dtype, void* out, coopt_stream_t stream);
+
+/*
+ * KV tier swap codec, one launch per (layer, K or V) cache.  Replaces the per-layer
+ *   q, s = quantize(cache[blocks], bits)            (swap_out, engine/kv_tier_manager.py:99)
+ *   cache[blocks] = dequantize(q, s, bits, dtype)   (swap_in, engine/kv_tier_manager.py:119)
+ * with the gather / scatter fused into the codec.
+ *   cache        [num_blocks, block_size, Hkv, D] with strides (c_blk, c_tok, c_head, 1):
+ *                COOPT_DT_BF16 values, or COOPT_DT_I8 codes with fp16 cache_scale
+ *                [num_blocks, block_size, Hkv] (strides s_blk, s_tok, s_head).
+ *   block_ids    [num_ids] int64 device array; q / scale are contiguous
+ *                [num_ids, block_size, Hkv, D'] and [num_ids, block_size, Hkv] (fp16):
+ *                bits 16: q holds bf16 copies (D' = D, no scale); bits 8: int8 codes (D' = D);
+ *                bits 4: two codes per byte (D' = D/2), even element in the low nibble, +8.
+ *   Codes and scales are those of kv_tier_manager.quantize on the GPU (bit-exact); swap_in
+ *   writes bf16(float(code) * float(scale)).  An INT8 cache (bits must be 8) is copied code for
+ *   code with its scales, both ways (lossless).  Ids outside [0, num_blocks) are read as zero
+ *   vectors by swap_out and skipped by swap_in.  D must be 8 * a power of two, <= 512.
+ */
+int coopt_kv_swap_out(int bits, int cache_dtype, const void* cache,
+                      int64_t c_blk_stride, int64_t c_tok_stride, int64_t c_head_stride,
+                      const void* cache_scale, int64_t s_blk_stride, int64_t s_tok_stride,
+                      int64_t s_head_stride, const int64_t* block_ids, int num_ids,
+                      int block_size, int Hkv, int D, int64_t num_blocks, void* q, void* scale,
+                      coopt_stream_t stream);
+int coopt_kv_swap_in(int bits, int cache_dtype, const void* q, const void* scale,
+                     const int64_t* block_ids, int num_ids, int block_size, int Hkv, int D,
+                     int64_t num_blocks, void* cache, int64_t c_blk_stride, int64_t c_tok_stride,
+                     int64_t c_head_stride, void* cache_scale, int64_t s_blk_stride,
+                     int64_t s_tok_stride, int64_t s_head_stride, coopt_stream_t stream);
 
 /*
  * Paged GQA verification attention.  Replaces flash_attn_varlen_func(q, k_cache, v_cache,

@@ -3,6 +3,7 @@
 slot_mapping   engine/block_manager.py:216-220   slot = table[p // bs] * bs + p % bs
 block_table    engine/block_manager.py:222-229   [B, W] int32, rows zero-padded
 kv_write       engine/model.py:190, 201-203      k_cache[slot // bs, slot % bs] = k
+swap_out/in    engine/kv_tier_manager.py:99, 119  quantize(cache[blocks]) / cache[blocks] = dequantize
                (the semantics tests/kv_write_check.py:26-30 pins for the fused vLLM op);
                INT8 caches store quantize(k, 8) (engine/kv_tier_manager.py:21-31) per vector
 attention      engine/model.py:204-207, 244-247 (flash_attn_varlen_func, causal, paged):
@@ -111,3 +112,24 @@ def attention(q, k_cache, v_cache, cu_seqlens_q, seq_lens, block_tables, block_s
 def dequantized_cache(codes, scales):
     """INT8 cache -> the bf16 values dequantize(q, scale, 8, bf16) gives, as float32."""
     return codec.bf16_round(codec.dequantize(codes, scales, 8))
+
+
+def swap_out(cache, blocks, bits: int, mode: str = "device"):
+    """quantize(cache[blocks], bits) (engine/kv_tier_manager.py:99) on cache values [NB, bs,
+    H, D]: -> (codes, fp16 scales), or (cache[blocks] copy, None) at 16 bits.  Ids outside the
+    pool give zero vectors (the kernel's documented behaviour for them)."""
+    cache = np.asarray(cache, dtype=np.float32)
+    blocks = np.asarray(blocks, dtype=np.int64)
+    ok = (blocks >= 0) & (blocks < cache.shape[0])
+    x = np.zeros((len(blocks),) + cache.shape[1:], dtype=np.float32)
+    x[ok] = cache[blocks[ok]]
+    if bits == 16:
+        return x, None
+    return codec.quantize(x, bits, mode)
+
+
+def swap_in(q, scale, bits: int):
+    """dequantize(q, scale, bits, bf16) (engine/kv_tier_manager.py:119) as float32 values."""
+    if bits == 16:
+        return np.asarray(q, dtype=np.float32)
+    return codec.bf16_round(codec.dequantize(q, scale, bits))

@@ -174,3 +174,48 @@ def test_kv_write_index_put_and_no_leak_into_other_layers():
     assert np.array_equal(vc[slots // bs, slots % bs], v)
     others = np.concatenate([buf[:, l] for l in range(Lyr) if l != 2])
     assert (others == 0).all()
+
+
+def test_tier_manager_accounting_matches_reference_formula():
+    """engine/kv_tier_manager.py:67-82 without a GPU: estimate_bytes for the Llama-3.1-8B
+    geometry (32 layers, 8 KV heads, head_dim 128), capacity, hit rate, and the early
+    refusals of swap_out (nothing computed; does not fit)."""
+    import types
+
+    torch = pytest.importorskip("torch")
+    from iitj_llm_coopt_amd.kv_tier import KVTierManager
+
+    cfg = types.SimpleNamespace(num_hidden_layers=32, num_key_value_heads=8, head_dim=128)
+    e = types.SimpleNamespace(target=types.SimpleNamespace(cfg=cfg, k_cache=[], v_cache=[]), bm=None)
+    tm = KVTierManager(e, cpu_gb=1.0, bits=8)
+    assert e.kv_tiers is tm
+    per_tok8 = 2 * 32 * 8 * 128          # bytes of codes per token at 8 bits
+    assert tm.estimate_bytes(1000, 8) == int(per_tok8 * 1000 * (1 + 2 / 128))
+    assert tm.estimate_bytes(1000, 16) == 2 * per_tok8 * 1000
+    assert tm.estimate_bytes(1000, 4) == int(per_tok8 / 2 * 1000 * (1 + 2 / 128))
+    assert tm.cpu_usage == 0.0 and tm.hit_rate == 0.0
+    tm.note_recompute()
+    assert tm.hit_rate == 0.0 and tm.recomputes == 1
+    seq = types.SimpleNamespace(seq_id=1, num_computed=0)
+    assert tm.swap_out(seq) is False      # nothing computed
+    tm.capacity = 10
+    seq.num_computed = 5
+    assert tm.swap_out(seq) is False      # does not fit (checked before touching the GPU)
+    tm.drop(99)                           # unknown ids are ignored
+    with pytest.raises(ValueError):
+        KVTierManager(e, bits=3)
+
+
+def test_swap_oracle_is_gather_then_codec():
+    rng = np.random.default_rng(4)
+    cache = rng.standard_normal((6, 16, 2, 32)).astype(np.float32)
+    blocks = np.array([4, -1, 0])
+    q, s = paged.swap_out(cache, blocks, 8)
+    from oracle import codec as OC
+    q0, s0 = OC.quantize(cache[4], 8)
+    assert np.array_equal(q[0], q0) and np.array_equal(s[0], s0)
+    assert np.all(q[1] == 0) and np.all(s[1] == 0)
+    x, none = paged.swap_out(cache, blocks, 16)
+    assert none is None and np.array_equal(x[2], cache[0])
+    back = paged.swap_in(q, s, 8)
+    assert np.allclose(back[0], cache[4], atol=np.abs(cache[4]).max() / 127)
