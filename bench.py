@@ -246,6 +246,38 @@ def kv_tier_case(torch, M, dev, seed, tokens=4096, layers=32):
                     "(one H2D copy, 64 codec launches), host-timed"}
 
 
+def migrate_case(torch, M, dev, seed, pairs=256):
+    """Block migration copy: `pairs` blocks of the block-major elastic buffer of a
+    Llama-3.1-8B-shaped target (32 layers x K/V x 16 tokens x 8 heads x 128, bf16: 2 MiB a
+    block) move to free blocks, one coopt_kv_copy_blocks launch.  Also timed: the same pairs
+    as one torch copy per block, the reference's copy_fn (engine/elastic.py:131)."""
+    import numpy as np
+
+    nb = 4 * pairs
+    buf, _, _ = M.allocate_block_major_kv(nb, 32, 16, 8, 128, device=dev)
+    buf.view(torch.int16).random_(generator=torch.Generator(device=dev).manual_seed(seed))
+    perm = np.random.default_rng(seed).permutation(nb)
+    src, dst = perm[:pairs], perm[pairs:2 * pairs]
+    s_t = torch.from_numpy(src.astype(np.int64)).to(dev)
+    d_t = torch.from_numpy(dst.astype(np.int64)).to(dev)
+    M.copy_blocks(buf, src, dst)             # host checks once; the timed calls pass device ids
+
+    def fn():
+        M.copy_blocks(buf, s_t, d_t)
+
+    res = rate({"pairs": pairs, "block_bytes": buf[0].numel() * 2},
+               2 * pairs * buf[0].numel() * 2, *time_launches(torch, dev, fn, n=20))
+    sl, dl = src.tolist(), dst.tolist()
+
+    def per_block():
+        for a, b in zip(sl, dl):
+            buf[b].copy_(buf[a])
+
+    avg, _ = time_launches(torch, dev, per_block, n=5)
+    res["per_block_torch_copy_us"] = avg * 1e6
+    return res
+
+
 def copy_case(torch, M, dev, seed):
     """A plain streaming kernel of known size (torch.neg over 1 GiB of bf16: 1 GiB read,
     1 GiB written): the calibration for FETCH_SIZE / WRITE_SIZE and a practical HBM ceiling."""
@@ -284,6 +316,7 @@ KERNEL_CASES = {
     "kv_write_t65536": lambda t, M, d, s: kv_write_case(t, M, d, 65536, s),
     "kv_swap_out_4096tok": lambda t, M, d, s: kv_swap_case(t, M, d, s),
     "kv_tier_roundtrip": lambda t, M, d, s: kv_tier_case(t, M, d, s),
+    "kv_migrate_256x2MiB": lambda t, M, d, s: migrate_case(t, M, d, s),
     "copy": lambda t, M, d, s: copy_case(t, M, d, s),
 }
 

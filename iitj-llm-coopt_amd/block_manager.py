@@ -3,9 +3,11 @@
 Call surface of engine/block_manager.py (mohsinmubarak/iitj-llm-coopt): BlockManager(num_blocks,
 block_size), ensure (:86-93), truncate (:95-103), free (:105-110), blocks_for (:48-49),
 can_fit (:54-55), num_free / usage (:40-46), slot_mapping (:216-220), block_table_tensor
-(:222-229) and OutOfBlocks (:22-23).  Token p of a sequence lives in slot
-table[p // block_size] * block_size + p % block_size.  Prefix caching and the elastic
-grow/shrink/migrate methods of the reference are control-plane features outside this path.
+(:222-229), OutOfBlocks (:22-23), and the elastic pool's add_blocks / migrate_out_of /
+withdraw_free / take_free_excluding (:159-213).  Token p of a sequence lives in slot
+table[p // block_size] * block_size + p % block_size.  Prefix caching (hashes, reference counts,
+the evictable LRU) is a control-plane feature outside this path: every block here belongs to
+one table, and evictable blocks do not exist.
 
 `free_order` lets a caller fix the order in which blocks are handed out (e.g. a seeded
 permutation, so that block tables are scattered over the pool as in a long-running server).
@@ -78,6 +80,56 @@ class BlockManager:
         table = self.tables.pop(seq_id, [])
         self._free.extend(table)
         return len(table)
+
+    # ---- pool growth, shrinkage and migration (the elastic buffer's park / unpark) ----------
+    def add_blocks(self, ids) -> None:
+        """Grows the pool with blocks whose memory was just handed over (engine/block_manager.py
+        :159-163); they join the end of the free list in the given order."""
+        ids = [int(b) for b in ids]
+        self._free.extend(ids)
+        self.num_blocks += len(ids)
+
+    def take_free_excluding(self, excluded) -> int:
+        """Takes the first free block not in `excluded` (engine/block_manager.py:202-213)."""
+        for i, b in enumerate(self._free):
+            if b not in excluded:
+                del self._free[i]
+                return b
+        raise OutOfBlocks("no free block outside the excluded range")
+
+    def migrate_out_of(self, ids, copy_fn) -> int:
+        """Moves every in-use block in `ids` to a free block outside `ids`, in ascending id
+        order, calling copy_fn(src, dst) for each and rewriting every table that holds it; the
+        source joins the end of the free list (engine/block_manager.py:165-187).  Returns the
+        number moved, or -1 (nothing changed) when too few free blocks lie outside `ids`.
+        Sources are all in `ids` and destinations all outside, so the copies may run in any
+        order, e.g. batched into one kv_blocks.copy_blocks launch."""
+        ids = set(int(b) for b in ids)
+        used = sorted({b for t in self.tables.values() for b in t if b in ids})
+        if sum(1 for b in self._free if b not in ids) < len(used):
+            return -1
+        where = {}
+        for sid, t in self.tables.items():
+            for i, b in enumerate(t):
+                if b in ids:
+                    where.setdefault(b, []).append((sid, i))
+        for src in used:
+            dst = self.take_free_excluding(ids)
+            copy_fn(src, dst)
+            for sid, i in where[src]:
+                self.tables[sid][i] = dst
+            self._free.append(src)
+        return len(used)
+
+    def withdraw_free(self, ids) -> None:
+        """Shrinks the pool by the blocks `ids`, which must all be free
+        (engine/block_manager.py:189-199); raises OutOfBlocks otherwise, changing nothing."""
+        ids = set(int(b) for b in ids)
+        remaining = deque(b for b in self._free if b not in ids)
+        if len(self._free) - len(remaining) != len(ids):
+            raise OutOfBlocks("withdraw_free: some blocks are still in use")
+        self._free = remaining
+        self.num_blocks -= len(ids)
 
     # ---- tensors for the kernels -------------------------------------------------------------
     def slot_mapping(self, seq_id: int, start: int, end: int) -> torch.Tensor:

@@ -26,6 +26,8 @@
  *   coopt_dequantize        dequantize
  *   coopt_kv_swap_out /     quantize(cache[blocks], bits) / engine/kv_tier_manager.py:93-101
  *   coopt_kv_swap_in        cache[blocks] = dequantize(..)  engine/kv_tier_manager.py:113-119
+ *   coopt_kv_copy_blocks    buf[dst].copy_(buf[src]) per    engine/elastic.py:131 via
+ *                           migrated block                  engine/block_manager.py:165-187
  *   coopt_softmax           torch.softmax(logits / T)       engine/spec_decode.py:16
  *   coopt_rms_norm          vLLM rms_norm / fused_add_rms_norm  engine/model.py:234, 236, 249, 254
  *   coopt_rope              vLLM rotary_embedding (neox)    engine/model.py:239
@@ -130,6 +132,26 @@ int coopt_kv_swap_in(int bits, int cache_dtype, const void* q, const void* scale
                      int64_t num_blocks, void* cache, int64_t c_blk_stride, int64_t c_tok_stride,
                      int64_t c_head_stride, void* cache_scale, int64_t s_blk_stride,
                      int64_t s_tok_stride, int64_t s_head_stride, coopt_stream_t stream);
+
+/*
+ * Block migration copy: for every pair i, block dst_ids[i] <- block src_ids[i] in every
+ * region, in one launch per 32 regions.  Replaces the per-block copy_fn(src, dst) =
+ * buf[dst].copy_(buf[src]) that BlockManager.migrate_out_of calls (engine/elastic.py:131,
+ * engine/block_manager.py:165-187).
+ *   regions   host array [num_regions][3] of int64 {device base address, bytes between
+ *             consecutive block ids, bytes per block}: block b of a region is the byte range
+ *             [base + b * stride, base + b * stride + bytes).  One region may be the whole
+ *             block-major buffer [NB, L, 2, bs, Hkv, D] (engine/elastic.py:74-77), or one
+ *             per-layer K/V cache or INT8 scale cache whose blocks are dense.  Base, stride
+ *             and bytes must be multiples of 16, and 0 < bytes <= stride.
+ *   src_ids, dst_ids  [num_pairs] int64 device arrays.  A pair with either id outside
+ *             [0, num_blocks) is skipped.  Pairs are copied in no particular order, so no dst
+ *             may be the src of another pair, and no two pairs may share a dst (a migration
+ *             out of a set of blocks into free blocks outside it satisfies both).
+ */
+int coopt_kv_copy_blocks(const int64_t* regions, int num_regions, const int64_t* src_ids,
+                         const int64_t* dst_ids, int num_pairs, int64_t num_blocks,
+                         coopt_stream_t stream);
 
 /*
  * Paged GQA verification attention.  Replaces flash_attn_varlen_func(q, k_cache, v_cache,

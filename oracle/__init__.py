@@ -8,7 +8,9 @@ Each function restates the reference algorithm (mohsinmubarak/iitj-llm-coopt, ci
 file:line) in numpy / torch-CPU:
   oracle.codec     quantize / dequantize          engine/kv_tier_manager.py:21-41
   oracle.paged     slot mapping, KV write,        engine/block_manager.py:216-229,
-                   paged causal GQA attention     engine/model.py:186-207, :242-247
+                   paged causal GQA attention,    engine/model.py:186-207, :242-247,
+                   tier swap, block migration     engine/kv_tier_manager.py:99, 119,
+                                                  engine/block_manager.py:165-187
   oracle.accept    softmax, sample, verify         engine/spec_decode.py:12-49,
                    (explicit uniforms), batched    engine/engine.py:421-446
                    greedy accept

@@ -3,9 +3,11 @@
 slot_mapping   engine/block_manager.py:216-220   slot = table[p // bs] * bs + p % bs
 block_table    engine/block_manager.py:222-229   [B, W] int32, rows zero-padded
 kv_write       engine/model.py:190, 201-203      k_cache[slot // bs, slot % bs] = k
-swap_out/in    engine/kv_tier_manager.py:99, 119  quantize(cache[blocks]) / cache[blocks] = dequantize
                (the semantics tests/kv_write_check.py:26-30 pins for the fused vLLM op);
                INT8 caches store quantize(k, 8) (engine/kv_tier_manager.py:21-31) per vector
+swap_out/in    engine/kv_tier_manager.py:99, 119  quantize(cache[blocks]) / cache[blocks] = dequantize
+migrate        engine/block_manager.py:165-187   move in-use blocks out of a set, FIFO destinations
+copy_blocks    engine/elastic.py:131              buf[dst] = buf[src] per migrated block
 attention      engine/model.py:204-207, 244-247 (flash_attn_varlen_func, causal, paged):
                query j of a sequence with n new tokens and L keys sees keys [0, L - n + j]
                (causal mask aligned bottom-right, engine/model.py:8-10); head h reads KV head
@@ -133,3 +135,39 @@ def swap_in(q, scale, bits: int):
     if bits == 16:
         return np.asarray(q, dtype=np.float32)
     return codec.bf16_round(codec.dequantize(q, scale, bits))
+
+
+def migrate(tables, free, ids):
+    """BlockManager.migrate_out_of (engine/block_manager.py:165-187) over plain lists, without
+    prefix-cache state: -> (pairs [(src, dst)], tables, free) after the move, or None when
+    fewer free blocks than in-use blocks of `ids` lie outside `ids` (nothing changes).  Sources
+    are the in-use ids in ascending order; each takes the first free block outside `ids`
+    (:202-208), every table entry holding it is rewritten, and it joins the end of the free
+    list."""
+    ids = set(ids)
+    tables = {k: list(v) for k, v in tables.items()}
+    free = list(free)
+    used = sorted({b for t in tables.values() for b in t if b in ids})
+    if sum(1 for b in free if b not in ids) < len(used):
+        return None
+    pairs = []
+    for src in used:
+        j = next(i for i, b in enumerate(free) if b not in ids)
+        dst = free.pop(j)
+        pairs.append((src, dst))
+        for t in tables.values():
+            for i, b in enumerate(t):
+                if b == src:
+                    t[i] = dst
+        free.append(src)
+    return pairs, tables, free
+
+
+def copy_blocks(caches, pairs):
+    """buf[dst] = buf[src] for each pair in order (engine/elastic.py:131), on numpy arrays
+    whose dim 0 is the block id; returns new arrays."""
+    out = [np.array(c, copy=True) for c in caches]
+    for s, d in pairs:
+        for c in out:
+            c[d] = c[s]
+    return out

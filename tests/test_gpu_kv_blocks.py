@@ -1,0 +1,135 @@
+"""GPU: block migration copy (coopt_kv_copy_blocks) and the elastic unpark migration.
+
+Bar: bit-exact.  Every copied block equals oracle.paged.copy_blocks (the reference's per-block
+buf[dst].copy_(buf[src]), engine/elastic.py:131), blocks outside the pairs are untouched, and
+attention over migrated caches equals attention before the migration bit for bit.
+"""
+import numpy as np
+import pytest
+import torch
+
+import iitj_llm_coopt_amd as M
+from iitj_llm_coopt_amd import _lib
+from oracle import paged
+
+pytestmark = pytest.mark.gpu
+
+
+def _fill(t, seed):
+    g = torch.Generator(device=t.device).manual_seed(seed)
+    if t.dtype == torch.int8:
+        t.copy_(torch.randint(-128, 128, t.shape, generator=g, device=t.device, dtype=torch.int8))
+    else:
+        t.copy_(torch.randn(t.shape, generator=g, device=t.device).to(t.dtype))
+
+
+def _pairs(rng, nb, n):
+    perm = rng.permutation(nb)
+    return perm[:n], perm[n:2 * n]
+
+
+def _bits(t):
+    x = t.cpu()
+    return x.view(torch.int16).numpy() if x.element_size() == 2 else x.numpy()
+
+
+def test_copy_blocks_block_major_buffer(dev):
+    rng = np.random.default_rng(0)
+    buf, kc, vc = M.allocate_block_major_kv(96, 4, 16, 8, 128, device=dev)   # 256 KiB blocks
+    _fill(buf, 1)
+    src, dst = _pairs(rng, 96, 30)
+    want = paged.copy_blocks([_bits(buf)], list(zip(src, dst)))[0]
+    print(f"[copy_blocks] block-major, {len(src)} pairs of {buf[0].numel() * 2} B", flush=True)
+    M.copy_blocks(buf, src, dst)
+    assert np.array_equal(_bits(buf), want)
+
+
+def test_copy_blocks_per_layer_caches_many_regions(dev):
+    """72 regions in one call (three launches of up to 32): INT8 codes, their head-major fp16
+    scales and bf16 caches, blocks of 16 KiB, 256 B and 32 KiB."""
+    rng = np.random.default_rng(1)
+    NB = 64
+    caches = []
+    for layer in range(12):
+        kq, vq, ks, vs = M.allocate_kv_cache(NB, 16, 8, 128, "int8", device=dev)
+        kb, vb, _, _ = M.allocate_kv_cache(NB, 16, 8, 128, "auto", device=dev)
+        caches += [kq, vq, ks, vs, kb, vb]
+    for i, c in enumerate(caches):
+        _fill(c, 10 + i)
+    src, dst = _pairs(rng, NB, 20)
+    before = [_bits(c) for c in caches]
+    want = paged.copy_blocks(before, list(zip(src, dst)))
+    print(f"[copy_blocks] {len(caches)} regions, {len(src)} pairs", flush=True)
+    M.copy_blocks(caches, src, dst)
+    for c, w in zip(caches, want):
+        assert np.array_equal(_bits(c), w)
+
+
+def test_copy_blocks_device_ids_skip_out_of_pool_pairs(dev):
+    buf, _, _ = M.allocate_block_major_kv(32, 2, 16, 8, 64, device=dev)
+    _fill(buf, 3)
+    before = _bits(buf)
+    src = torch.tensor([1, 2, 40, -1, 5], device=dev)
+    dst = torch.tensor([10, 11, 12, 13, 99], device=dev)
+    M.copy_blocks(buf, src, dst)
+    want = paged.copy_blocks([before], [(1, 10), (2, 11)])[0]
+    assert np.array_equal(_bits(buf), want)
+
+
+def test_copy_blocks_argument_errors(dev):
+    buf, kc, _ = M.allocate_block_major_kv(16, 2, 16, 8, 64, device=dev)
+    with pytest.raises(ValueError):
+        M.copy_blocks(buf, [1, 2], [3, 3])             # repeated dst
+    with pytest.raises(ValueError):
+        M.copy_blocks(buf, [1, 2], [2, 4])             # dst that is also a src
+    with pytest.raises(ValueError):
+        M.copy_blocks(buf, [1], [16])                  # out of range
+    ids = torch.tensor([0, 1], device=dev)
+    bad = np.array([[buf.data_ptr() + 8, buf.stride(0) * 2, 256]], dtype=np.int64)
+    rc = _lib.load().coopt_kv_copy_blocks(bad.ctypes.data, 1, _lib.ptr(ids), _lib.ptr(ids), 1, 16,
+                                          _lib.stream_handle(buf.device))
+    assert rc != 0 and "multiples of 16" in _lib.last_error()
+    bad = np.array([[buf.data_ptr(), 256, 512]], dtype=np.int64)
+    rc = _lib.load().coopt_kv_copy_blocks(bad.ctypes.data, 1, _lib.ptr(ids), _lib.ptr(ids), 1, 16,
+                                          _lib.stream_handle(buf.device))
+    assert rc != 0 and "block stride" in _lib.last_error()
+
+
+def test_unpark_migration_keeps_attention_bit_identical(dev):
+    """The elastic unpark: sequences spill into the tail blocks, migrate_out_of moves them out
+    in one launch, and verify attention over the new tables equals the old output exactly."""
+    L, bs, H, Hq, D = 2, 16, 8, 32, 128
+    base, tail = 48, 40
+    buf, kc, vc = M.allocate_block_major_kv(base + tail, L, bs, H, D, device=dev)
+    _fill(buf, 7)
+    rng = np.random.default_rng(2)
+    bm = M.BlockManager(base, bs, free_order=rng.permutation(base))
+    bm.add_blocks(range(base, base + tail))
+    lens = [300, 200, 90, 150]          # 19 + 13 + 6 + 10 = 48 blocks: the base pool
+    for sid, n in enumerate(lens):
+        bm.ensure(sid, n)
+    bm.free(0)                          # 19 base blocks return behind the tail
+    bm.ensure(4, 220)                   # 14 blocks, all from the tail
+    sids = [1, 2, 3, 4]
+    in_tail = sum(b >= base for s in sids for b in bm.tables[s])
+    assert in_tail == 14
+    q_len = 5
+    q = torch.randn(len(sids) * q_len, Hq, D, device=dev).to(torch.bfloat16)
+    cu = torch.arange(0, len(sids) * q_len + 1, q_len, device=dev, dtype=torch.int32)
+    sl = torch.tensor([200, 90, 150, 220], device=dev, dtype=torch.int32)
+
+    def attend():
+        tab = bm.block_table_tensor(sids).to(dev)
+        return [M.flash_attn_varlen_func(q=q, k=kc[i], v=vc[i], cu_seqlens_q=cu, max_seqlen_q=q_len,
+                                         seqused_k=sl, max_seqlen_k=220, softmax_scale=D ** -0.5,
+                                         causal=True, block_table=tab) for i in range(L)]
+
+    before = [o.clone() for o in attend()]
+    moved = M.migrate_out_of(bm, range(base, base + tail), buf)
+    print(f"[unpark] {in_tail} tail blocks in use, {moved} moved", flush=True)
+    assert moved == in_tail
+    assert not any(b >= base for s in sids for b in bm.tables[s])
+    bm.withdraw_free(range(base, base + tail))
+    after = attend()
+    for x, y in zip(before, after):
+        assert torch.equal(x, y)

@@ -219,3 +219,110 @@ def test_swap_oracle_is_gather_then_codec():
     assert none is None and np.array_equal(x[2], cache[0])
     back = paged.swap_in(q, s, 8)
     assert np.allclose(back[0], cache[4], atol=np.abs(cache[4]).max() / 127)
+
+
+# ---- elastic pool: add / migrate / withdraw (engine/block_manager.py:159-213) ---------------
+def _tail_scenario():
+    bm = BlockManager(num_blocks=4, block_size=16)
+    bm.add_blocks([4, 5])
+    bm.ensure(1, 48)
+    bm.ensure(2, 32)
+    bm.free(1)
+    return bm
+
+
+def test_migrate_known_answer():
+    # free [5, 0, 1, 2], tables {2: [3, 4]}: block 4 moves to the first free block outside
+    # {4, 5}, i.e. 0; the source joins the end of the free list; 5 and 4 are then withdrawn.
+    bm = _tail_scenario()
+    assert bm.num_blocks == 6 and list(bm.free_blocks) == [5, 0, 1, 2] and bm.tables == {2: [3, 4]}
+    pairs = []
+    assert bm.migrate_out_of({4, 5}, lambda s, d: pairs.append((s, d))) == 1
+    assert pairs == [(4, 0)] and bm.tables == {2: [3, 0]} and list(bm.free_blocks) == [5, 1, 2, 4]
+    bm.withdraw_free({4, 5})
+    assert bm.num_blocks == 4 and list(bm.free_blocks) == [1, 2]
+    got = paged.migrate({2: [3, 4]}, [5, 0, 1, 2], {4, 5})
+    assert got == ([(4, 0)], {2: [3, 0]}, [5, 1, 2, 4])
+
+
+def test_migrate_without_room_changes_nothing():
+    bm = BlockManager(num_blocks=4, block_size=16)
+    bm.add_blocks([4, 5])
+    bm.ensure(1, 96)                       # all six blocks, two of them in {4, 5}
+    before = (dict((k, list(v)) for k, v in bm.tables.items()), list(bm.free_blocks))
+    assert bm.migrate_out_of({4, 5}, lambda s, d: pytest.fail("no copy expected")) == -1
+    assert (bm.tables, list(bm.free_blocks)) == before
+    assert paged.migrate(bm.tables, bm.free_blocks, {4, 5}) is None
+    with pytest.raises(OutOfBlocks):
+        bm.withdraw_free({4, 5})
+    assert (bm.tables, list(bm.free_blocks), bm.num_blocks) == (before[0], before[1], 6)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2, 3])
+def test_migrate_invariants_and_oracle_agree(seed):
+    """Random pools: the product and the restatement agree, and both keep every table reading
+    the same KV (content[dst] = content[src]) with no table left in the migrated set."""
+    rng = np.random.default_rng(seed)
+    base, tail = 64, 24
+    bm = BlockManager(base, 16, free_order=rng.permutation(base))
+    bm.add_blocks(rng.permutation(np.arange(base, base + tail)).tolist())
+    for sid in range(12):
+        bm.ensure(sid, int(rng.integers(1, 7 * 16)))
+    for sid in rng.choice(12, 5, replace=False):
+        bm.free(int(sid))
+    ids = set(range(base, base + tail))
+    tables0 = {k: list(v) for k, v in bm.tables.items()}
+    free0 = list(bm.free_blocks)
+    content = np.arange(base + tail) * 7 + 3          # a distinct payload per block
+    pairs = []
+
+    def copy(s, d):
+        pairs.append((s, d))
+        content[d] = content[s]
+
+    moved = bm.migrate_out_of(ids, copy)
+    want = paged.migrate(tables0, free0, ids)
+    if want is None:
+        assert moved == -1
+        return
+    assert moved == len(want[0]) and pairs == want[0]
+    assert bm.tables == want[1] and list(bm.free_blocks) == want[2]
+    assert all(s in ids and d not in ids for s, d in pairs)
+    assert len({d for _, d in pairs}) == len(pairs)
+    assert not any(b in ids for t in bm.tables.values() for b in t)
+    for sid, t in bm.tables.items():
+        assert [content[b] for b in t] == [(b * 7 + 3) for b in tables0[sid]]
+    n_before = bm.num_blocks
+    bm.withdraw_free(ids)
+    assert bm.num_blocks == n_before - tail and bm.num_free + sum(map(len, bm.tables.values())) == base
+
+
+def test_copy_blocks_oracle_is_fancy_indexing_for_disjoint_pairs():
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal((40, 3, 4)).astype(np.float32)
+    b = rng.integers(-128, 127, size=(40, 6)).astype(np.int8)
+    src = rng.choice(20, 9, replace=False)
+    dst = 20 + rng.choice(20, 9, replace=False)
+    got = paged.copy_blocks([a, b], list(zip(src, dst)))
+    for x, y in zip([a, b], got):
+        want = x.copy()
+        want[dst] = x[src]
+        assert np.array_equal(y, want)
+
+
+def test_block_region_of_cache_layouts():
+    from iitj_llm_coopt_amd.kv_blocks import block_region
+
+    NB, L, bs, H, D = 6, 3, 16, 8, 128
+    buf = torch.empty((NB, L, 2, bs, H, D), dtype=torch.bfloat16)
+    base, stride, per = block_region(buf)
+    assert (stride, per) == (L * 2 * bs * H * D * 2,) * 2
+    base, stride, per = block_region(buf[:, 1, 0])
+    assert base == buf.data_ptr() + (2 * bs * H * D) * 2 and stride == L * 2 * bs * H * D * 2
+    assert per == bs * H * D * 2
+    hm = torch.empty((NB, H, bs, D), dtype=torch.int8).permute(0, 2, 1, 3)   # head-major view
+    assert block_region(hm)[1:] == (H * bs * D, H * bs * D)
+    sc = torch.empty((NB, H, bs), dtype=torch.float16).permute(0, 2, 1)
+    assert block_region(sc)[1:] == (H * bs * 2, H * bs * 2)
+    with pytest.raises(ValueError):
+        block_region(buf[:, :, 0, :8])                # half the tokens of each block
