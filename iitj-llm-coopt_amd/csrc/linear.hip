@@ -1,0 +1,297 @@
+// Weight-streaming linear layer for decode / verify row counts: Y[M, N] = X[M, K] W[N, K]^T
+// in bf16 with fp32 accumulation, for M <= 256 (the 32-160 rows of a speculative step).
+// Replaces torch.nn.functional.linear at the reference's projections (engine/model.py:236-254:
+// qkv_proj, o_proj, gate_up_proj, down_proj, lm_head).
+//
+// At these row counts the layer is a stream over W (2 bytes per weight, read once) with
+// intensity 2M flop/byte, under the bf16 MFMA ridge (~310 flop/byte) up to M = 155; the
+// library GEMMs pick square macro tiles and leave most CUs idle on N = 4096 outputs.
+//
+// Decomposition.  A workgroup of WAVES waves owns WAVES * NW 16-column tiles of the output
+// and a K range of `kt` elements; gridDim.y workgroups split K, and when it exceeds one they
+// write fp32 partials that reduce_kernel sums in a fixed order (deterministic, no atomics).
+//   * W streams from HBM straight into MFMA B operands: per 128-wide K step a lane reads 64
+//     contiguous bytes of its output row as 4 x 16 B (MFMA j covers k0 + 32j + [8g, 8g+8),
+//     g = lane / 16), PF steps ahead of the MFMAs.
+//   * X is shared: each K step's [M, 128] slice is staged once per workgroup in LDS (double
+//     buffered, rows padded to 272 bytes) and read by all waves as MFMA A operands.
+//   * v_mfma_f32_16x16x32_bf16 with A = X rows, B = W rows: lane l holds
+//     C[4(l/16) + i][l % 16] of each 16x16 tile.
+#include "common.h"
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kKB = 128;                  // K elements per step
+constexpr int kPitch = kKB * 2 + 16;      // LDS bytes per staged X row
+
+struct LinArgs {
+  const uint16_t* x;
+  int64_t ldx;
+  const uint16_t* w;
+  int64_t ldw;
+  int M, N, K;
+  int kt;            // K elements per workgroup (multiple of kKB)
+  uint16_t* y;
+  int64_t ldy;
+  float* part;       // [gridDim.y, 16 * MT, N] fp32 when gridDim.y > 1
+};
+
+__device__ __forceinline__ f32x4_t mfma_bf16(u32x4_t a, u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ u32x4_t ldg16(const uint16_t* p) {
+  return *reinterpret_cast<const u32x4_t*>(p);
+}
+
+// MT: 16-row tiles of M; NW: 16-column tiles per wave; WAVES: waves per workgroup;
+// PF: K steps of W in flight per wave (even).
+template <int MT, int NW, int WAVES, int PF>
+__global__ __launch_bounds__(64 * WAVES) void linear_kernel(LinArgs a) {
+  static_assert(PF % 2 == 0, "the step loop is unrolled by PF and alternates X buffers");
+  constexpr int kThreads = 64 * WAVES;
+  constexpr int kRowsPerRound = kThreads / 16;                     // X rows staged per round
+  constexpr int kRounds = (MT * 16 + kRowsPerRound - 1) / kRowsPerRound;
+  __shared__ __attribute__((aligned(16))) unsigned char xs[2][MT * 16 * kPitch];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int n0 = (blockIdx.x * WAVES + wave) * NW * 16;
+  const int kbeg = blockIdx.y * a.kt;
+  const int nsteps = (a.K - kbeg < a.kt ? a.K - kbeg : a.kt) / kKB;
+  const int last = nsteps - 1;
+
+  // W rows of this lane (clamped into [0, N): columns past N are computed and dropped)
+  const uint16_t* wrow[NW];
+#pragma unroll
+  for (int nt = 0; nt < NW; ++nt) {
+    int n = n0 + nt * 16 + l16;
+    n = n < a.N ? n : a.N - 1;
+    wrow[nt] = a.w + static_cast<int64_t>(n) * a.ldw + kbeg + 8 * g;
+  }
+  // X staging: in round r, thread t loads 16 B of row r * kRowsPerRound + t / 16 at byte
+  // 16 (t % 16) of the step; rows >= M are zeros, rows >= 16 MT are not staged.
+  const int xr_row = threadIdx.x >> 4, xr_col = (threadIdx.x & 15) * 8;
+  const uint16_t* xrow[kRounds];
+  bool xok[kRounds], xin[kRounds];
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int m = r * kRowsPerRound + xr_row;
+    xin[r] = m < MT * 16;
+    xok[r] = m < a.M;
+    xrow[r] = a.x + static_cast<int64_t>(xok[r] ? m : 0) * a.ldx + kbeg + xr_col;
+  }
+
+  auto load_x = [&](int s, u32x4_t (&xr)[kRounds]) {
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r)
+      xr[r] = xok[r] ? ldg16(xrow[r] + s * kKB) : u32x4_t{0, 0, 0, 0};
+  };
+  auto load_w = [&](int s, u32x4_t (&wr)[NW][4]) {
+#pragma unroll
+    for (int nt = 0; nt < NW; ++nt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wr[nt][j] = ldg16(wrow[nt] + s * kKB + 32 * j);
+  };
+  auto store_x = [&](int buf, const u32x4_t (&xr)[kRounds]) {
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r)
+      if (xin[r])
+        *reinterpret_cast<u32x4_t*>(
+            &xs[buf][(r * kRowsPerRound + xr_row) * kPitch + xr_col * 2]) = xr[r];
+  };
+
+  f32x4_t acc[MT][NW];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NW; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int buf, const u32x4_t (&wr)[NW][4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const u32x4_t xa = *reinterpret_cast<const u32x4_t*>(
+            &xs[buf][(mt * 16 + l16) * kPitch + 64 * j + 16 * g]);
+#pragma unroll
+        for (int nt = 0; nt < NW; ++nt) acc[mt][nt] = mfma_bf16(xa, wr[nt][j], acc[mt][nt]);
+      }
+  };
+
+  // Pipeline.  W: a ring of PF register buffers, step s + PF loaded right after step s's
+  // MFMAs.  X: two register buffers, step s + 2 loaded at the start of step s and stored to
+  // LDS at the end of step s + 1, so the wait for it never covers the W loads issued after
+  // it.  Step indices past the last are clamped: those reloads hit L2, not HBM, and keep
+  // every load unconditional.
+  u32x4_t xq[2][kRounds];
+  u32x4_t wbuf[PF][NW][4];
+  load_x(0, xq[0]);
+  load_x(last < 1 ? last : 1, xq[1]);
+#pragma unroll
+  for (int p = 0; p < PF; ++p) load_w(p < last ? p : last, wbuf[p]);
+  store_x(0, xq[0]);
+  for (int s0 = 0; s0 < nsteps; s0 += PF) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      const int s = s0 + u;
+      if (s < nsteps) {
+        load_x(s + 2 < last ? s + 2 : last, xq[u & 1]);
+        __syncthreads();
+        compute(u & 1, wbuf[u]);
+        load_w(s + PF < last ? s + PF : last, wbuf[u]);
+        store_x((u + 1) & 1, xq[(u + 1) & 1]);
+      }
+    }
+  }
+
+  // Epilogue: lane holds rows 16 mt + 4 g + i of column n0 + 16 nt + l16.
+  if (gridDim.y == 1) {
+#pragma unroll
+    for (int nt = 0; nt < NW; ++nt) {
+      const int n = n0 + nt * 16 + l16;
+      if (n >= a.N) continue;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = mt * 16 + 4 * g + i;
+          if (m < a.M) a.y[static_cast<int64_t>(m) * a.ldy + n] = f32_to_bf16(acc[mt][nt][i]);
+        }
+    }
+  } else {
+    float* p = a.part + static_cast<int64_t>(blockIdx.y) * (MT * 16) * a.N;
+#pragma unroll
+    for (int nt = 0; nt < NW; ++nt) {
+      const int n = n0 + nt * 16 + l16;
+      if (n >= a.N) continue;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          p[static_cast<int64_t>(mt * 16 + 4 * g + i) * a.N + n] = acc[mt][nt][i];
+    }
+  }
+}
+
+// y[m, n] = bf16(sum over slices s = 0..ks-1, in order, of part[s, m, n]); 4 columns a thread.
+__global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ part, int ks,
+                                                     int64_t slice, int M, int N,
+                                                     uint16_t* __restrict__ y, int64_t ldy) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int nq = N / 4;
+  if (gid >= static_cast<int64_t>(M) * nq) return;
+  const int m = static_cast<int>(gid / nq), n = static_cast<int>(gid % nq) * 4;
+  const float* p = part + static_cast<int64_t>(m) * N + n;
+  float4 s = *reinterpret_cast<const float4*>(p);
+  for (int k = 1; k < ks; ++k) {
+    const float4 v = *reinterpret_cast<const float4*>(p + k * slice);
+    s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+  }
+  uint16_t* o = y + static_cast<int64_t>(m) * ldy + n;
+  const uint32_t lo = f32_to_bf16(s.x) | (static_cast<uint32_t>(f32_to_bf16(s.y)) << 16);
+  const uint32_t hi = f32_to_bf16(s.z) | (static_cast<uint32_t>(f32_to_bf16(s.w)) << 16);
+  *reinterpret_cast<uint2*>(o) = make_uint2(lo, hi);
+}
+
+struct Plan {
+  int mt, nw, waves, ks, kt;
+};
+
+// 16-row tiles of M, rounded up to an instantiated count.
+int m_tiles(int M) {
+  const int t = (M + 15) / 16;
+  static const int kTiles[] = {1, 2, 4, 6, 8, 10, 12, 16};
+  for (int v : kTiles)
+    if (t <= v) return v;
+  return -1;
+}
+
+// Launch shape (measured on MI355X over the decode / verify projections of an 8B / 1B Llama
+// pair): 8 waves of one 16-column tile each, or 4 waves for N <= 4096 at M <= 64, or 4
+// column tiles per wave for very wide N (lm_head).  K is split in powers of two while the
+// grid stays within 256 workgroups and each keeps at least 4 K steps; every split adds
+// 4 * 16 * MT bytes of fp32 partials per column against 2 * kt bytes of weights.
+Plan plan_for(int M, int N, int K) {
+  Plan p{m_tiles(M), 1, 8, 1, K};
+  if (p.mt <= 4 && N <= 4096) p.waves = 4;
+  if (p.mt <= 4 && N >= 65536) p.nw = 4;
+  const int cols = p.waves * p.nw * 16;
+  const int nb = (N + cols - 1) / cols;
+  const int steps = K / kKB;
+  int ks = 1;
+  while (nb * ks * 2 <= 256 && steps / (ks * 2) >= 4) ks *= 2;
+  p.kt = ((steps + ks - 1) / ks) * kKB;
+  p.ks = (K + p.kt - 1) / p.kt;
+  return p;
+}
+
+template <int MT, int NW, int WAVES, int PF>
+void launch_cfg(const Plan& p, const LinArgs& a, hipStream_t s) {
+  const int cols = WAVES * NW * 16;
+  hipLaunchKernelGGL((linear_kernel<MT, NW, WAVES, PF>), dim3((a.N + cols - 1) / cols, p.ks),
+                     dim3(64 * WAVES), 0, s, a);
+}
+
+template <int MT>
+void launch_mt(const Plan& p, const LinArgs& a, hipStream_t s) {
+  if constexpr (MT <= 4) {
+    if (p.nw == 4) return launch_cfg<MT, 4, 8, 2>(p, a, s);
+    if (p.waves == 4) return launch_cfg<MT, 1, 4, 2>(p, a, s);
+  }
+  launch_cfg<MT, 1, 8, 2>(p, a, s);
+}
+
+}  // namespace
+
+extern "C" size_t coopt_linear_workspace(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % kKB != 0 || m_tiles(M) < 0) return 0;
+  const Plan p = plan_for(M, N, K);
+  return p.ks > 1 ? static_cast<size_t>(p.ks) * p.mt * 16 * N * sizeof(float) : 0;
+}
+
+extern "C" int coopt_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, int N,
+                            int K, void* y, int64_t ldy, void* workspace, size_t workspace_bytes,
+                            coopt_stream_t stream) {
+  coopt::clear_error();
+  COOPT_REQUIRE(M >= 0 && N >= 0 && K >= 0, "negative size");
+  if (M == 0 || N == 0) return COOPT_OK;
+  COOPT_REQUIRE(M <= 256, "M must be <= 256 (decode / verify row counts)");
+  COOPT_REQUIRE(K > 0 && K % kKB == 0, "K must be a positive multiple of 128");
+  COOPT_REQUIRE(N % 4 == 0, "N must be a multiple of 4");
+  COOPT_REQUIRE(x && w && y, "null pointer");
+  COOPT_REQUIRE(coopt::aligned16(x) && coopt::aligned16(w), "x and w must be 16-byte aligned");
+  COOPT_REQUIRE(ldx >= K && ldw >= K && ldx % 8 == 0 && ldw % 8 == 0,
+                "row strides of x and w must be >= K and multiples of 8");
+  COOPT_REQUIRE(ldy >= N && ldy % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0,
+                "y rows must be 8-byte aligned with stride >= N, a multiple of 4");
+  COOPT_REQUIRE(static_cast<int64_t>(N) * ldw < (int64_t(1) << 62), "w too large");
+  const Plan p = plan_for(M, N, K);
+  const size_t need = coopt_linear_workspace(M, N, K);
+  COOPT_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+                "workspace smaller than coopt_linear_workspace()");
+  LinArgs a{static_cast<const uint16_t*>(x), ldx, static_cast<const uint16_t*>(w), ldw, M, N, K,
+            p.kt, static_cast<uint16_t*>(y), ldy, static_cast<float*>(workspace)};
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (p.mt) {
+    case 1: launch_mt<1>(p, a, s); break;
+    case 2: launch_mt<2>(p, a, s); break;
+    case 4: launch_mt<4>(p, a, s); break;
+    case 6: launch_mt<6>(p, a, s); break;
+    case 8: launch_mt<8>(p, a, s); break;
+    case 10: launch_mt<10>(p, a, s); break;
+    case 12: launch_mt<12>(p, a, s); break;
+    default: launch_mt<16>(p, a, s); break;
+  }
+  int rc = coopt::check_launch("coopt_linear");
+  if (rc != COOPT_OK || p.ks == 1) return rc;
+  const int64_t n4 = static_cast<int64_t>(M) * (N / 4);
+  hipLaunchKernelGGL(reduce_kernel, dim3(static_cast<unsigned>((n4 + 255) / 256)), dim3(256), 0,
+                     s, static_cast<const float*>(workspace), p.ks,
+                     static_cast<int64_t>(p.mt) * 16 * N, M, N, static_cast<uint16_t*>(y), ldy);
+  return coopt::check_launch("coopt_linear");
+}

@@ -4,12 +4,17 @@ Counterparts of the vLLM ops the reference's forward calls (engine/model.py:234-
   rms_norm(x, weight, eps, residual=None, out=None)   _ops.rms_norm / _ops.fused_add_rms_norm
   rope_(q, k, positions, cos, sin)                     _ops.rotary_embedding (neox, in place)
   silu_and_mul(gate_up, out=None)                      torch.ops._C.silu_and_mul
+  linear(x, weight, out=None)                          the projections (nn.Linear, no bias)
 """
 import torch
+import torch.nn.functional as F
 
 from . import _lib
 
-__all__ = ["rms_norm", "rope_", "silu_and_mul"]
+__all__ = ["rms_norm", "rope_", "silu_and_mul", "linear", "LINEAR_MAX_ROWS"]
+
+LINEAR_MAX_ROWS = 256
+_WS = _lib.WorkspaceCache()
 
 
 def _bf16_rows(t, name):
@@ -64,4 +69,37 @@ def silu_and_mul(gate_up, out=None):
         out = torch.empty((T, F2 // 2), dtype=gate_up.dtype, device=gate_up.device)
     _lib.check(_lib.load().coopt_silu_mul(_lib.ptr(gate_up), _lib.ptr(out), T, F2 // 2,
                                           _lib.stream_handle(gate_up.device)), "coopt_silu_mul")
+    return out
+
+
+def linear(x, weight, out=None):
+    """x [..., K] @ weight[N, K]^T -> [..., N], bf16 with fp32 accumulation (no bias), as the
+    reference's projections (engine/model.py:236-254).
+
+    The weight-streaming kernel coopt_linear takes bf16 operands with K a multiple of 128 at
+    up to LINEAR_MAX_ROWS rows, and runs where it measured faster than torch's GEMM on MI355X:
+    up to 64 rows (draft steps), or N <= 8192 outputs at any supported row count (the verify
+    step's qkv / o / down projections).  Other shapes -- prefill-sized row counts, and the
+    wide gate_up / lm_head outputs at verify row counts -- go to torch (hipBLASLt)."""
+    _lib.require_cuda(x, weight, out)
+    K = x.shape[-1]
+    N = weight.shape[0]
+    x2 = x.reshape(-1, K)
+    M = x2.shape[0]
+    if (M > LINEAR_MAX_ROWS or K % 128 or N % 4 or x.dtype != torch.bfloat16
+            or weight.dtype != torch.bfloat16 or weight.dim() != 2 or weight.shape[1] != K
+            or (M > 64 and N > 8192)):
+        return F.linear(x, weight, out=out) if out is not None else F.linear(x, weight)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or weight.stride(-1) != 1 or weight.stride(0) % 8:
+        x2 = x2.contiguous()
+        weight = weight.contiguous()
+    if out is None:
+        out = torch.empty(x.shape[:-1] + (N,), dtype=torch.bfloat16, device=x.device)
+    y2 = out.view(-1, N)
+    need = int(_lib.load().coopt_linear_workspace(M, N, K))
+    ws = _WS.get(need, x.device) if need else None
+    _lib.check(_lib.load().coopt_linear(
+        _lib.ptr(x2), x2.stride(0), _lib.ptr(weight), weight.stride(0), M, N, K, _lib.ptr(y2),
+        y2.stride(0), _lib.ptr(ws), 0 if ws is None else ws.numel(),
+        _lib.stream_handle(x.device)), "coopt_linear")
     return out

@@ -27,7 +27,7 @@ import torch.nn.functional as F
 
 from . import _lib
 from .attention import paged_attention, workspace_bytes
-from .fused import rms_norm, rope_, silu_and_mul
+from .fused import linear, rms_norm, rope_, silu_and_mul
 from .kv_cache import allocate_kv_cache, reshape_and_cache_flash
 from .spec_decode import AcceptResult, accept
 
@@ -119,20 +119,18 @@ class RandomLlama:
         d = None
         for li, L in enumerate(self.layers):
             h = ops.rms_norm(x if d is None else d, None if d is None else x, L["ln1"], s.eps)
-            qkv = F.linear(h, L["qkv"])
+            qkv = ops.linear(h, L["qkv"])
             q = qkv[:, : H * D].view(T, H, D)
             k = qkv[:, H * D: (H + Hkv) * D].view(T, Hkv, D)
             v = qkv[:, (H + Hkv) * D:].view(T, Hkv, D)
             ops.rope(q, k, pos, self.cos, self.sin)
             ops.write(kv, li, k, v, slots)
             attn = ops.attend(kv, li, q, meta, self.scale)
-            o = F.linear(attn.reshape(T, H * D), L["o"])
+            o = ops.linear(attn.reshape(T, H * D), L["o"])
             h = ops.rms_norm(o, x, L["ln2"], s.eps)
-            d = F.linear(ops.silu_mul(F.linear(h, L["gate_up"])), L["down"])
+            d = ops.linear(ops.silu_mul(ops.linear(h, L["gate_up"])), L["down"])
         h = ops.rms_norm(d, x, self.norm, s.eps)
-        if logits_out is not None:
-            return torch.matmul(h, self.lm_head.t(), out=logits_out)
-        return F.linear(h, self.lm_head)
+        return ops.linear(h, self.lm_head, out=logits_out)
 
 
 class PagedKV:
@@ -198,6 +196,9 @@ class HipOps:
 
     def silu_mul(self, gate_up):
         return silu_and_mul(gate_up)
+
+    def linear(self, x, w, out=None):
+        return linear(x, w, out=out)
 
     def attend(self, kv: PagedKV, layer, q, meta, scale):
         kc, vc, ks, vs = kv.layers[layer]

@@ -32,6 +32,8 @@
  *   coopt_rms_norm          vLLM rms_norm / fused_add_rms_norm  engine/model.py:234, 236, 249, 254
  *   coopt_rope              vLLM rotary_embedding (neox)    engine/model.py:239
  *   coopt_silu_mul          vLLM silu_and_mul               engine/model.py:251-252
+ *   coopt_linear            nn.Linear projections at decode engine/model.py:236-254
+ *                           / verify row counts             (qkv, o, gate_up, down, lm_head)
  */
 #ifndef COOPT_AMD_H
 #define COOPT_AMD_H
@@ -246,6 +248,23 @@ int coopt_rope(void* q, int64_t q_tok_stride, int64_t q_head_stride, void* k,
                const void* cos, const void* sin, int64_t table_stride, int max_pos, int T, int Hq,
                int Hkv, int D, coopt_stream_t stream);
 int coopt_silu_mul(const void* gate_up, void* out, int64_t T, int F, coopt_stream_t stream);
+
+/*
+ * Linear layer at decode / verify row counts: y[M, N] = x[M, K] w[N, K]^T, bf16 in and out,
+ * fp32 accumulation, no bias -- the projections of the reference's forward (nn.Linear at
+ * engine/model.py:236-254: qkv_proj, o_proj, gate_up_proj, down_proj, and lm_head).
+ *   x  [M, K] row stride ldx; w [N, K] row stride ldw (both 16-byte aligned, strides multiples
+ *   of 8 elements); y [M, N] row stride ldy (8-byte aligned, a multiple of 4).
+ *   1 <= M <= 256, K a multiple of 128, N a multiple of 4.
+ *   workspace: coopt_linear_workspace(M, N, K) bytes (0 = none needed).  Large K is split over
+ *   workgroups whose fp32 partial sums are added in a fixed order, so results are
+ *   deterministic; the summation order differs from a library GEMM's (results agree to bf16
+ *   rounding of the fp32 sum).
+ */
+size_t coopt_linear_workspace(int M, int N, int K);
+int coopt_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, int N, int K,
+                 void* y, int64_t ldy, void* workspace, size_t workspace_bytes,
+                 coopt_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -37,6 +37,12 @@ class OracleOps:
         gate, up = gate_up.chunk(2, dim=-1)
         return torch.nn.functional.silu(gate) * up
 
+    def linear(self, x, w, out=None):
+        # the projections (engine/model.py:236-254): nn.Linear without bias
+        if out is not None:
+            return torch.matmul(x, w.t(), out=out)
+        return torch.nn.functional.linear(x, w)
+
     def write(self, kv, layer, k, v, slots):
         kc, vc, ks, vs = kv.layers[layer]
         slots = slots.cpu()

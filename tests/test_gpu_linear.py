@@ -1,0 +1,109 @@
+"""GPU: coopt_linear (weight-streaming projections at decode / verify row counts) against an
+fp32 reference of the same op, y = x w^T.
+
+Bar: |y - ref| <= 2^-8 |ref| + 2 K 2^-24 sum_k |x_k w_k| per element -- one bf16 rounding
+(unit roundoff 2^-8)
+of the output plus fp32 summation error -- written below as `bound`.  Repeated calls and HIP
+graph replays are bit-identical (fixed-order split-K reduction).
+"""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from iitj_llm_coopt_amd import _lib, fused
+
+pytestmark = pytest.mark.gpu
+
+
+def ref_and_bound(x, w):
+    xf, wf = x.float(), w.float()
+    ref = xf @ wf.t()
+    mag = xf.abs() @ wf.abs().t()
+    K = x.shape[-1]
+    return ref, 2.0 ** -8 * ref.abs() + 2 * K * 2.0 ** -24 * mag + 1e-30
+
+
+def check(y, x, w, label):
+    ref, bound = ref_and_bound(x, w)
+    err = (y.float() - ref).abs()
+    worst = (err / bound).max().item()
+    print(f"[linear {label}] max err/bound {worst:.3f}", flush=True)
+    assert worst <= 1.0, label
+
+
+@pytest.mark.parametrize("M,N,K", [
+    (160, 6144, 4096), (160, 4096, 4096), (160, 4096, 14336), (32, 3072, 2048),
+    (32, 2048, 8192), (64, 16384, 2048), (1, 256, 128), (17, 100, 384), (200, 64, 640),
+    (256, 520, 1152), (5, 4, 128),
+])
+def test_linear_matches_fp32_reference(dev, M, N, K):
+    g = torch.Generator(device=dev).manual_seed(M * 7 + N + K)
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    ws = int(_lib.load().coopt_linear_workspace(M, N, K))
+    print(f"[linear] M={M} N={N} K={K} workspace {ws} B", flush=True)
+    y = fused.linear(x, w)
+    check(y, x, w, f"{M}x{N}x{K}")
+    assert torch.equal(y, fused.linear(x, w))          # deterministic
+
+
+def test_linear_strided_rows_and_out(dev):
+    M, N, K = 40, 272, 1024
+    g = torch.Generator(device=dev).manual_seed(3)
+    xb = torch.randn(M, K + 64, generator=g, device=dev).to(torch.bfloat16)
+    x = xb[:, 32:32 + K]                                  # row stride K + 64, offset 64 B
+    w = (torch.randn(N, K, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    yb = torch.full((M, N + 12), 7.0, device=dev, dtype=torch.bfloat16)
+    y = yb[:, :N]
+    fused.linear(x, w, out=y)
+    check(y, x, w, "strided")
+    assert torch.all(yb[:, N:] == 7.0)                    # nothing written past N
+
+
+def test_linear_large_rows_use_torch(dev):
+    x = torch.randn(300, 256, device=dev).to(torch.bfloat16)
+    w = torch.randn(64, 256, device=dev).to(torch.bfloat16)
+    assert torch.equal(fused.linear(x, w), F.linear(x, w))
+
+
+def test_linear_graph_replay_equals_eager(dev):
+    M, N, K = 160, 4096, 4096
+    g = torch.Generator(device=dev).manual_seed(11)
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        eager = fused.linear(x, w)
+        out = torch.empty_like(eager)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            fused.linear(x, w, out=out)
+    for i in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        x2 = fused.linear(x, w)                           # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(x2, eager)
+
+
+def test_linear_argument_errors(dev):
+    x = torch.randn(4, 128, device=dev).to(torch.bfloat16)
+    w = torch.randn(8, 128, device=dev).to(torch.bfloat16)
+    y = torch.empty(4, 8, device=dev, dtype=torch.bfloat16)
+    L = _lib.load()
+    st = _lib.stream_handle(dev)
+    assert L.coopt_linear(_lib.ptr(x), 128, _lib.ptr(w), 128, 4, 8, 100, _lib.ptr(y), 8, None, 0, st) != 0
+    assert "multiple of 128" in _lib.last_error()
+    assert L.coopt_linear(_lib.ptr(x), 128, _lib.ptr(w), 128, 300, 8, 128, _lib.ptr(y), 8, None, 0, st) != 0
+    need = int(L.coopt_linear_workspace(160, 4096, 4096))
+    assert need > 0
+    xx = torch.empty(160, 4096, device=dev, dtype=torch.bfloat16)
+    ww = torch.empty(4096, 4096, device=dev, dtype=torch.bfloat16)
+    yy = torch.empty(160, 4096, device=dev, dtype=torch.bfloat16)
+    assert L.coopt_linear(_lib.ptr(xx), 4096, _lib.ptr(ww), 4096, 160, 4096, 4096, _lib.ptr(yy), 4096,
+                          None, 0, st) != 0
+    assert "workspace" in _lib.last_error()
