@@ -74,22 +74,22 @@ __global__ __launch_bounds__(64 * WAVES) void linear_kernel(LinArgs a) {
     wrow[nt] = a.w + static_cast<int64_t>(n) * a.ldw + kbeg + 8 * g;
   }
   // X staging: in round r, thread t loads 16 B of row r * kRowsPerRound + t / 16 at byte
-  // 16 (t % 16) of the step; rows >= M are zeros, rows >= 16 MT are not staged.
+  // 16 (t % 16) of the step; rows >= 16 MT are not staged.  Rows in [M, 16 MT) repeat row
+  // M - 1: their outputs are never stored, and an unconditional load keeps the compiler's
+  // load counting exact (a load under a branch makes it wait for every load in flight).
   const int xr_row = threadIdx.x >> 4, xr_col = (threadIdx.x & 15) * 8;
   const uint16_t* xrow[kRounds];
-  bool xok[kRounds], xin[kRounds];
+  bool xin[kRounds];
 #pragma unroll
   for (int r = 0; r < kRounds; ++r) {
     const int m = r * kRowsPerRound + xr_row;
     xin[r] = m < MT * 16;
-    xok[r] = m < a.M;
-    xrow[r] = a.x + static_cast<int64_t>(xok[r] ? m : 0) * a.ldx + kbeg + xr_col;
+    xrow[r] = a.x + static_cast<int64_t>(m < a.M ? m : a.M - 1) * a.ldx + kbeg + xr_col;
   }
 
   auto load_x = [&](int s, u32x4_t (&xr)[kRounds]) {
 #pragma unroll
-    for (int r = 0; r < kRounds; ++r)
-      xr[r] = xok[r] ? ldg16(xrow[r] + s * kKB) : u32x4_t{0, 0, 0, 0};
+    for (int r = 0; r < kRounds; ++r) xr[r] = ldg16(xrow[r] + s * kKB);
   };
   auto load_w = [&](int s, u32x4_t (&wr)[NW][4]) {
 #pragma unroll
@@ -111,16 +111,36 @@ __global__ __launch_bounds__(64 * WAVES) void linear_kernel(LinArgs a) {
 #pragma unroll
     for (int nt = 0; nt < NW; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+  // A fragments of MFMA group j + 1 are read from LDS while group j's MFMAs run, so no MFMA
+  // waits on the latency of the read that feeds it.
+  auto read_frag = [&](int buf, int j, u32x4_t (&fa)[MT]) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      fa[mt] = *reinterpret_cast<const u32x4_t*>(
+          &xs[buf][(mt * 16 + l16) * kPitch + 64 * j + 16 * g]);
+  };
+  auto mfma_group = [&](int j, const u32x4_t (&fa)[MT], const u32x4_t (&wr)[NW][4]) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NW; ++nt) acc[mt][nt] = mfma_bf16(fa[mt], wr[nt][j], acc[mt][nt]);
+  };
+  // (sched_barrier keeps the scheduler from sinking the reads back next to their MFMAs)
   auto compute = [&](int buf, const u32x4_t (&wr)[NW][4]) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const u32x4_t xa = *reinterpret_cast<const u32x4_t*>(
-            &xs[buf][(mt * 16 + l16) * kPitch + 64 * j + 16 * g]);
-#pragma unroll
-        for (int nt = 0; nt < NW; ++nt) acc[mt][nt] = mfma_bf16(xa, wr[nt][j], acc[mt][nt]);
-      }
+    u32x4_t f0[MT], f1[MT];
+    read_frag(buf, 0, f0);
+    read_frag(buf, 1, f1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_group(0, f0, wr);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frag(buf, 2, f0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_group(1, f1, wr);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frag(buf, 3, f1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_group(2, f0, wr);
+    mfma_group(3, f1, wr);
   };
 
   // Pipeline.  W: a ring of PF register buffers, step s + PF loaded right after step s's
