@@ -1,7 +1,7 @@
 // Weight-streaming linear layer for decode / verify row counts: Y[M, N] = X[M, K] W[N, K]^T
 // in bf16 with fp32 accumulation, for M <= 256 (the 32-160 rows of a speculative step).
-// Replaces torch.nn.functional.linear at the reference's projections (engine/model.py:236-254:
-// qkv_proj, o_proj, gate_up_proj, down_proj, lm_head).
+// Replaces torch.nn.functional.linear at the reference's projections (engine/model.py:238,
+// 248, 250, 253: qkv, o, gate_up, down) and the logits projection.
 //
 // At these row counts the layer is a stream over W (2 bytes per weight, read once) with
 // intensity 2M flop/byte, under the bf16 MFMA ridge (~310 flop/byte) up to M = 155; the

@@ -4,7 +4,7 @@ Counterparts of the vLLM ops the reference's forward calls (engine/model.py:234-
   rms_norm(x, weight, eps, residual=None, out=None)   _ops.rms_norm / _ops.fused_add_rms_norm
   rope_(q, k, positions, cos, sin)                     _ops.rotary_embedding (neox, in place)
   silu_and_mul(gate_up, out=None)                      torch.ops._C.silu_and_mul
-  linear(x, weight, out=None)                          the projections (nn.Linear, no bias)
+  linear(x, weight, out=None)                          F.linear projections (model.py:238-253)
 """
 import torch
 import torch.nn.functional as F
@@ -74,7 +74,7 @@ def silu_and_mul(gate_up, out=None):
 
 def linear(x, weight, out=None):
     """x [..., K] @ weight[N, K]^T -> [..., N], bf16 with fp32 accumulation (no bias), as the
-    reference's projections (engine/model.py:236-254).
+    reference's projections (F.linear at engine/model.py:238, 248, 250, 253).
 
     The weight-streaming kernel coopt_linear takes bf16 operands with K a multiple of 128 at
     up to LINEAR_MAX_ROWS rows, and runs where it measured faster than torch's GEMM on MI355X:

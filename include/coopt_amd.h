@@ -32,8 +32,8 @@
  *   coopt_rms_norm          vLLM rms_norm / fused_add_rms_norm  engine/model.py:234, 236, 249, 254
  *   coopt_rope              vLLM rotary_embedding (neox)    engine/model.py:239
  *   coopt_silu_mul          vLLM silu_and_mul               engine/model.py:251-252
- *   coopt_linear            nn.Linear projections at decode engine/model.py:236-254
- *                           / verify row counts             (qkv, o, gate_up, down, lm_head)
+ *   coopt_linear            F.linear projections at decode  engine/model.py:238, 248, 250,
+ *                           / verify row counts             253 (qkv, o, gate_up, down)
  */
 #ifndef COOPT_AMD_H
 #define COOPT_AMD_H
@@ -251,8 +251,8 @@ int coopt_silu_mul(const void* gate_up, void* out, int64_t T, int F, coopt_strea
 
 /*
  * Linear layer at decode / verify row counts: y[M, N] = x[M, K] w[N, K]^T, bf16 in and out,
- * fp32 accumulation, no bias -- the projections of the reference's forward (nn.Linear at
- * engine/model.py:236-254: qkv_proj, o_proj, gate_up_proj, down_proj, and lm_head).
+ * fp32 accumulation, no bias -- the projections of the reference's forward (F.linear at
+ * engine/model.py:238, 248, 250, 253: qkv, o, gate_up, down; and the logits projection).
  *   x  [M, K] row stride ldx; w [N, K] row stride ldw (both 16-byte aligned, strides multiples
  *   of 8 elements); y [M, N] row stride ldy (8-byte aligned, a multiple of 4).
  *   1 <= M <= 256, K a multiple of 128, N a multiple of 4.
