@@ -38,7 +38,7 @@ class OracleOps:
         return torch.nn.functional.silu(gate) * up
 
     def linear(self, x, w, out=None):
-        # the projections (engine/model.py:236-254): nn.Linear without bias
+        # the projections, F.linear without bias (engine/model.py:238, 248, 250, 253)
         if out is not None:
             return torch.matmul(x, w.t(), out=out)
         return torch.nn.functional.linear(x, w)
