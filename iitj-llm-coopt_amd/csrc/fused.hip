@@ -73,6 +73,66 @@ __global__ __launch_bounds__(kThreads) void rms_norm_kernel(const uint16_t* __re
   }
 }
 
+// The same stage with the row held in registers: one read of x (and the residual) and of w,
+// issued together, one block reduction, then the normalisation from registers -- a single
+// global round trip for the short rows of decode and verify steps.  CPT 8-element chunks per
+// thread cover H <= CPT * 8 * kThreads.
+template <int CPT>
+__global__ __launch_bounds__(kThreads) void rms_norm_reg_kernel(const uint16_t* __restrict__ x,
+                                                                uint16_t* __restrict__ residual,
+                                                                const uint16_t* __restrict__ w,
+                                                                uint16_t* __restrict__ out,
+                                                                int H, float eps) {
+  __shared__ float sh[4];
+  const int64_t row = blockIdx.x;
+  const uint16_t* xr = x + row * H;
+  uint16_t* rr = residual ? residual + row * H : nullptr;
+  uint32_t xw[CPT][4], ww[CPT][4];
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int i = (c * kThreads + threadIdx.x) * 8;
+    if (i >= H) continue;
+    const uint4 xv = *reinterpret_cast<const uint4*>(xr + i);
+    const uint4 wv = *reinterpret_cast<const uint4*>(w + i);
+    xw[c][0] = xv.x; xw[c][1] = xv.y; xw[c][2] = xv.z; xw[c][3] = xv.w;
+    ww[c][0] = wv.x; ww[c][1] = wv.y; ww[c][2] = wv.z; ww[c][3] = wv.w;
+    if (rr) {
+      const uint4 rv = *reinterpret_cast<const uint4*>(rr + i);
+      const uint32_t rw[4] = {rv.x, rv.y, rv.z, rv.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a0 = bf16_to_f32(static_cast<uint16_t>(xw[c][e])) + bf16_to_f32(static_cast<uint16_t>(rw[e]));
+        const float a1 = bf16_to_f32(static_cast<uint16_t>(xw[c][e] >> 16)) + bf16_to_f32(static_cast<uint16_t>(rw[e] >> 16));
+        xw[c][e] = round_bf16(a0) | (static_cast<uint32_t>(round_bf16(a1)) << 16);
+      }
+      *reinterpret_cast<uint4*>(rr + i) = make_uint4(xw[c][0], xw[c][1], xw[c][2], xw[c][3]);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float a0 = bf16_to_f32(static_cast<uint16_t>(xw[c][e]));
+      const float a1 = bf16_to_f32(static_cast<uint16_t>(xw[c][e] >> 16));
+      ss += a0 * a0 + a1 * a1;
+    }
+  }
+  const float rs = rsqrtf(block_sum_f32(ss, sh) / static_cast<float>(H) + eps);
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int i = (c * kThreads + threadIdx.x) * 8;
+    if (i >= H) continue;
+    uint32_t ow[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float n0 = bf16_to_f32(round_bf16(bf16_to_f32(static_cast<uint16_t>(xw[c][e])) * rs));
+      const float n1 = bf16_to_f32(round_bf16(bf16_to_f32(static_cast<uint16_t>(xw[c][e] >> 16)) * rs));
+      const float y0 = bf16_to_f32(static_cast<uint16_t>(ww[c][e])) * n0;
+      const float y1 = bf16_to_f32(static_cast<uint16_t>(ww[c][e] >> 16)) * n1;
+      ow[e] = round_bf16(y0) | (static_cast<uint32_t>(round_bf16(y1)) << 16);
+    }
+    *reinterpret_cast<uint4*>(out + row * H + i) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+  }
+}
+
 // In-place neox rotary embedding of q [T, Hq, D] and k [T, Hkv, D]: for i < D/2,
 // (x_i, x_{i+D/2}) -> (x_i c - x_{i+D/2} s, x_{i+D/2} c + x_i s) with c, s = cos/sin[pos][i]
 // from bf16 tables [max_pos, D] (engine/model.py:92-94, 120-124).  One thread per pair.
@@ -140,10 +200,20 @@ extern "C" int coopt_rms_norm(const void* x, void* residual, const void* weight,
                     (residual == nullptr || coopt::aligned16(residual)),
                 "rows must be 16-byte aligned");
   coopt::clear_error();
-  hipLaunchKernelGGL(rms_norm_kernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x),
-                     static_cast<uint16_t*>(residual), static_cast<const uint16_t*>(weight),
-                     static_cast<uint16_t*>(out), hidden, eps);
+  const dim3 grid(static_cast<unsigned>(rows));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  uint16_t* rp = static_cast<uint16_t*>(residual);
+  const uint16_t* wp = static_cast<const uint16_t*>(weight);
+  uint16_t* op = static_cast<uint16_t*>(out);
+  const int cpt = (hidden + kThreads * 8 - 1) / (kThreads * 8);
+  switch (cpt) {
+    case 1: hipLaunchKernelGGL(rms_norm_reg_kernel<1>, grid, dim3(kThreads), 0, s, xp, rp, wp, op, hidden, eps); break;
+    case 2: hipLaunchKernelGGL(rms_norm_reg_kernel<2>, grid, dim3(kThreads), 0, s, xp, rp, wp, op, hidden, eps); break;
+    case 3: hipLaunchKernelGGL(rms_norm_reg_kernel<3>, grid, dim3(kThreads), 0, s, xp, rp, wp, op, hidden, eps); break;
+    case 4: hipLaunchKernelGGL(rms_norm_reg_kernel<4>, grid, dim3(kThreads), 0, s, xp, rp, wp, op, hidden, eps); break;
+    default: hipLaunchKernelGGL(rms_norm_kernel, grid, dim3(kThreads), 0, s, xp, rp, wp, op, hidden, eps);
+  }
   return coopt::check_launch("coopt_rms_norm");
 }
 

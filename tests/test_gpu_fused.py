@@ -16,7 +16,8 @@ def bf16_close(a, ref, ulps=2):
     return bool(((a.float() - ref).abs() <= tol).all())
 
 
-@pytest.mark.parametrize("rows,hidden", [(1, 4096), (160, 4096), (33, 2048), (5, 128)])
+@pytest.mark.parametrize("rows,hidden", [(1, 4096), (160, 4096), (33, 2048), (5, 128), (4, 2056),
+                                         (7, 6144), (3, 8192), (2, 10240)])
 def test_rms_norm_and_fused_add(dev, rows, hidden):
     g = torch.Generator(device=dev).manual_seed(rows)
     x = torch.randn(rows, hidden, generator=g, device=dev).to(torch.bfloat16)
