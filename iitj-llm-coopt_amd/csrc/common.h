@@ -87,6 +87,22 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
   return v;
 }
 
+// Sum of ks (<= 16) fp32 partial slices p[k * slice], k = 0..ks-1, added in order; every
+// load is issued before the first add.
+__device__ __forceinline__ float4 sum_partials4(const float* p, int ks, int64_t slice) {
+  float4 v[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k)
+    if (k < ks) v[k] = *reinterpret_cast<const float4*>(p + k * slice);
+  float4 s = v[0];
+#pragma unroll
+  for (int k = 1; k < 16; ++k)
+    if (k < ks) {
+      s.x += v[k].x; s.y += v[k].y; s.z += v[k].z; s.w += v[k].w;
+    }
+  return s;
+}
+
 __device__ __forceinline__ float wave_sum_f32(float v) {
 #pragma unroll
   for (int m = 1; m < COOPT_WAVE; m <<= 1) v += __shfl_xor(v, m, COOPT_WAVE);

@@ -77,12 +77,17 @@ __global__ __launch_bounds__(kThreads) void rms_norm_kernel(const uint16_t* __re
 // issued together, one block reduction, then the normalisation from registers -- a single
 // global round trip for the short rows of decode and verify steps.  CPT 8-element chunks per
 // thread cover H <= CPT * 8 * kThreads.
+// With `part` set, x is not read: x[row] = bf16(sum of the ks fp32 slices part[k * slice +
+// row * H]) -- the split-K partials of the producing linear layer, reduced here in the order
+// its own reduction uses, so the result is the same as reducing first.
 template <int CPT>
 __global__ __launch_bounds__(kThreads) void rms_norm_reg_kernel(const uint16_t* __restrict__ x,
                                                                 uint16_t* __restrict__ residual,
                                                                 const uint16_t* __restrict__ w,
                                                                 uint16_t* __restrict__ out,
-                                                                int H, float eps) {
+                                                                int H, float eps,
+                                                                const float* __restrict__ part,
+                                                                int ks, int64_t slice) {
   __shared__ float sh[4];
   const int64_t row = blockIdx.x;
   const uint16_t* xr = x + row * H;
@@ -93,9 +98,18 @@ __global__ __launch_bounds__(kThreads) void rms_norm_reg_kernel(const uint16_t* 
   for (int c = 0; c < CPT; ++c) {
     const int i = (c * kThreads + threadIdx.x) * 8;
     if (i >= H) continue;
-    const uint4 xv = *reinterpret_cast<const uint4*>(xr + i);
     const uint4 wv = *reinterpret_cast<const uint4*>(w + i);
-    xw[c][0] = xv.x; xw[c][1] = xv.y; xw[c][2] = xv.z; xw[c][3] = xv.w;
+    if (part) {
+      const float* pr = part + row * H + i;
+      const float4 lo = sum_partials4(pr, ks, slice), hi = sum_partials4(pr + 4, ks, slice);
+      xw[c][0] = round_bf16(lo.x) | (static_cast<uint32_t>(round_bf16(lo.y)) << 16);
+      xw[c][1] = round_bf16(lo.z) | (static_cast<uint32_t>(round_bf16(lo.w)) << 16);
+      xw[c][2] = round_bf16(hi.x) | (static_cast<uint32_t>(round_bf16(hi.y)) << 16);
+      xw[c][3] = round_bf16(hi.z) | (static_cast<uint32_t>(round_bf16(hi.w)) << 16);
+    } else {
+      const uint4 xv = *reinterpret_cast<const uint4*>(xr + i);
+      xw[c][0] = xv.x; xw[c][1] = xv.y; xw[c][2] = xv.z; xw[c][3] = xv.w;
+    }
     ww[c][0] = wv.x; ww[c][1] = wv.y; ww[c][2] = wv.z; ww[c][3] = wv.w;
     if (rr) {
       const uint4 rv = *reinterpret_cast<const uint4*>(rr + i);
@@ -208,13 +222,42 @@ extern "C" int coopt_rms_norm(const void* x, void* residual, const void* weight,
   uint16_t* op = static_cast<uint16_t*>(out);
   const int cpt = (hidden + kThreads * 8 - 1) / (kThreads * 8);
   switch (cpt) {
-    case 1: hipLaunchKernelGGL(rms_norm_reg_kernel<1>, grid, dim3(kThreads), 0, s, xp, rp, wp, op, hidden, eps); break;
-    case 2: hipLaunchKernelGGL(rms_norm_reg_kernel<2>, grid, dim3(kThreads), 0, s, xp, rp, wp, op, hidden, eps); break;
-    case 3: hipLaunchKernelGGL(rms_norm_reg_kernel<3>, grid, dim3(kThreads), 0, s, xp, rp, wp, op, hidden, eps); break;
-    case 4: hipLaunchKernelGGL(rms_norm_reg_kernel<4>, grid, dim3(kThreads), 0, s, xp, rp, wp, op, hidden, eps); break;
+    case 1: hipLaunchKernelGGL(rms_norm_reg_kernel<1>, grid, dim3(kThreads), 0, s, xp, rp, wp, op, hidden, eps, nullptr, 0, 0); break;
+    case 2: hipLaunchKernelGGL(rms_norm_reg_kernel<2>, grid, dim3(kThreads), 0, s, xp, rp, wp, op, hidden, eps, nullptr, 0, 0); break;
+    case 3: hipLaunchKernelGGL(rms_norm_reg_kernel<3>, grid, dim3(kThreads), 0, s, xp, rp, wp, op, hidden, eps, nullptr, 0, 0); break;
+    case 4: hipLaunchKernelGGL(rms_norm_reg_kernel<4>, grid, dim3(kThreads), 0, s, xp, rp, wp, op, hidden, eps, nullptr, 0, 0); break;
     default: hipLaunchKernelGGL(rms_norm_kernel, grid, dim3(kThreads), 0, s, xp, rp, wp, op, hidden, eps);
   }
   return coopt::check_launch("coopt_rms_norm");
+}
+
+extern "C" int coopt_rms_norm_partials(const float* part, int ks, int64_t slice_stride,
+                                       void* residual, const void* weight, void* out,
+                                       int64_t rows, int hidden, float eps,
+                                       coopt_stream_t stream) {
+  COOPT_REQUIRE(rows >= 0 && hidden > 0 && hidden % 8 == 0 && hidden <= kThreads * 8 * 4,
+                "hidden must be a multiple of 8, at most 8192");
+  COOPT_REQUIRE(ks >= 1 && ks <= 16, "1 to 16 partial slices");
+  COOPT_REQUIRE(slice_stride >= rows * hidden && slice_stride % 4 == 0, "bad slice stride");
+  if (rows == 0) return COOPT_OK;
+  COOPT_REQUIRE(part && weight && out, "null pointer");
+  COOPT_REQUIRE(coopt::aligned16(part) && coopt::aligned16(weight) && coopt::aligned16(out) &&
+                    (residual == nullptr || coopt::aligned16(residual)),
+                "rows must be 16-byte aligned");
+  coopt::clear_error();
+  const dim3 grid(static_cast<unsigned>(rows));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint16_t* rp = static_cast<uint16_t*>(residual);
+  const uint16_t* wp = static_cast<const uint16_t*>(weight);
+  uint16_t* op = static_cast<uint16_t*>(out);
+  const int cpt = (hidden + kThreads * 8 - 1) / (kThreads * 8);
+  switch (cpt) {
+    case 1: hipLaunchKernelGGL(rms_norm_reg_kernel<1>, grid, dim3(kThreads), 0, s, nullptr, rp, wp, op, hidden, eps, part, ks, slice_stride); break;
+    case 2: hipLaunchKernelGGL(rms_norm_reg_kernel<2>, grid, dim3(kThreads), 0, s, nullptr, rp, wp, op, hidden, eps, part, ks, slice_stride); break;
+    case 3: hipLaunchKernelGGL(rms_norm_reg_kernel<3>, grid, dim3(kThreads), 0, s, nullptr, rp, wp, op, hidden, eps, part, ks, slice_stride); break;
+    default: hipLaunchKernelGGL(rms_norm_reg_kernel<4>, grid, dim3(kThreads), 0, s, nullptr, rp, wp, op, hidden, eps, part, ks, slice_stride); break;
+  }
+  return coopt::check_launch("coopt_rms_norm_partials");
 }
 
 extern "C" int coopt_rope(void* q, int64_t q_tok_stride, int64_t q_head_stride, void* k,

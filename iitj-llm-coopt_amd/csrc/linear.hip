@@ -37,7 +37,8 @@ struct LinArgs {
   int kt;            // K elements per workgroup (multiple of kKB)
   uint16_t* y;
   int64_t ldy;
-  float* part;       // [gridDim.y, 16 * MT, N] fp32 when gridDim.y > 1
+  float* part;       // [gridDim.y, 16 * MT, N] fp32 when gridDim.y > 1 or force_part
+  int force_part;    // write fp32 partials even for a single K slice
 };
 
 __device__ __forceinline__ f32x4_t mfma_bf16(u32x4_t a, u32x4_t b, f32x4_t c) {
@@ -170,7 +171,7 @@ __global__ __launch_bounds__(64 * WAVES) void linear_kernel(LinArgs a) {
   }
 
   // Epilogue: lane holds rows 16 mt + 4 g + i of column n0 + 16 nt + l16.
-  if (gridDim.y == 1) {
+  if (gridDim.y == 1 && !a.force_part) {
 #pragma unroll
     for (int nt = 0; nt < NW; ++nt) {
       const int n = n0 + nt * 16 + l16;
@@ -206,12 +207,7 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ p
   const int nq = N / 4;
   if (gid >= static_cast<int64_t>(M) * nq) return;
   const int m = static_cast<int>(gid / nq), n = static_cast<int>(gid % nq) * 4;
-  const float* p = part + static_cast<int64_t>(m) * N + n;
-  float4 s = *reinterpret_cast<const float4*>(p);
-  for (int k = 1; k < ks; ++k) {
-    const float4 v = *reinterpret_cast<const float4*>(p + k * slice);
-    s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
-  }
+  const float4 s = sum_partials4(part + static_cast<int64_t>(m) * N + n, ks, slice);
   uint16_t* o = y + static_cast<int64_t>(m) * ldy + n;
   const uint32_t lo = f32_to_bf16(s.x) | (static_cast<uint32_t>(f32_to_bf16(s.y)) << 16);
   const uint32_t hi = f32_to_bf16(s.z) | (static_cast<uint32_t>(f32_to_bf16(s.w)) << 16);
@@ -244,7 +240,7 @@ Plan plan_for(int M, int N, int K) {
   const int nb = (N + cols - 1) / cols;
   const int steps = K / kKB;
   int ks = 1;
-  while (nb * ks * 2 <= 256 && steps / (ks * 2) >= 4) ks *= 2;
+  while (ks < 16 && nb * ks * 2 <= 256 && steps / (ks * 2) >= 4) ks *= 2;
   p.kt = ((steps + ks - 1) / ks) * kKB;
   p.ks = (K + p.kt - 1) / p.kt;
   return p;
@@ -274,29 +270,76 @@ extern "C" size_t coopt_linear_workspace(int M, int N, int K) {
   return p.ks > 1 ? static_cast<size_t>(p.ks) * p.mt * 16 * N * sizeof(float) : 0;
 }
 
+namespace {
+
+// Shared by coopt_linear and coopt_linear_partials: checks, then the split-K launch.  With
+// `partials` every slice (also a single one) goes to the workspace as fp32.
+int run_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, int N, int K,
+               void* y, int64_t ldy, void* workspace, size_t workspace_bytes, bool partials,
+               hipStream_t s, Plan& p);
+
+}  // namespace
+
+extern "C" int coopt_linear_split(int M, int N, int K, int* ks, int* rows_padded) {
+  coopt::clear_error();
+  COOPT_REQUIRE(ks && rows_padded, "null output pointer");
+  COOPT_REQUIRE(M > 0 && M <= 256 && N > 0 && K > 0 && K % kKB == 0, "unsupported shape");
+  const Plan p = plan_for(M, N, K);
+  *ks = p.ks;
+  *rows_padded = p.mt * 16;
+  return COOPT_OK;
+}
+
+extern "C" int coopt_linear_partials(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                                     int M, int N, int K, void* workspace,
+                                     size_t workspace_bytes, coopt_stream_t stream) {
+  coopt::clear_error();
+  Plan p{};
+  return run_linear(x, ldx, w, ldw, M, N, K, nullptr, 0, workspace, workspace_bytes, true,
+                    reinterpret_cast<hipStream_t>(stream), p);
+}
+
 extern "C" int coopt_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, int N,
                             int K, void* y, int64_t ldy, void* workspace, size_t workspace_bytes,
                             coopt_stream_t stream) {
   coopt::clear_error();
+  Plan p{};
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int rc = run_linear(x, ldx, w, ldw, M, N, K, y, ldy, workspace, workspace_bytes, false, s, p);
+  if (rc != COOPT_OK || M == 0 || N == 0 || p.ks == 1) return rc;
+  const int64_t n4 = static_cast<int64_t>(M) * (N / 4);
+  hipLaunchKernelGGL(reduce_kernel, dim3(static_cast<unsigned>((n4 + 255) / 256)), dim3(256), 0,
+                     s, static_cast<const float*>(workspace), p.ks,
+                     static_cast<int64_t>(p.mt) * 16 * N, M, N, static_cast<uint16_t*>(y), ldy);
+  return coopt::check_launch("coopt_linear");
+}
+
+namespace {
+
+int run_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, int N, int K,
+               void* y, int64_t ldy, void* workspace, size_t workspace_bytes, bool partials,
+               hipStream_t s, Plan& p) {
   COOPT_REQUIRE(M >= 0 && N >= 0 && K >= 0, "negative size");
   if (M == 0 || N == 0) return COOPT_OK;
   COOPT_REQUIRE(M <= 256, "M must be <= 256 (decode / verify row counts)");
   COOPT_REQUIRE(K > 0 && K % kKB == 0, "K must be a positive multiple of 128");
   COOPT_REQUIRE(N % 4 == 0, "N must be a multiple of 4");
-  COOPT_REQUIRE(x && w && y, "null pointer");
+  COOPT_REQUIRE(x && w && (y || partials), "null pointer");
   COOPT_REQUIRE(coopt::aligned16(x) && coopt::aligned16(w), "x and w must be 16-byte aligned");
   COOPT_REQUIRE(ldx >= K && ldw >= K && ldx % 8 == 0 && ldw % 8 == 0,
                 "row strides of x and w must be >= K and multiples of 8");
-  COOPT_REQUIRE(ldy >= N && ldy % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0,
+  COOPT_REQUIRE(partials || (ldy >= N && ldy % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0),
                 "y rows must be 8-byte aligned with stride >= N, a multiple of 4");
   COOPT_REQUIRE(static_cast<int64_t>(N) * ldw < (int64_t(1) << 62), "w too large");
-  const Plan p = plan_for(M, N, K);
-  const size_t need = coopt_linear_workspace(M, N, K);
-  COOPT_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr),
-                "workspace smaller than coopt_linear_workspace()");
+  p = plan_for(M, N, K);
+  const size_t need = partials ? static_cast<size_t>(p.ks) * p.mt * 16 * N * sizeof(float)
+                               : coopt_linear_workspace(M, N, K);
+  COOPT_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr) &&
+                    (need == 0 || coopt::aligned16(workspace)),
+                "workspace smaller than required (or misaligned)");
   LinArgs a{static_cast<const uint16_t*>(x), ldx, static_cast<const uint16_t*>(w), ldw, M, N, K,
             p.kt, static_cast<uint16_t*>(y), ldy, static_cast<float*>(workspace)};
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  a.force_part = partials ? 1 : 0;  // fp32 slices even when K is not split
   switch (p.mt) {
     case 1: launch_mt<1>(p, a, s); break;
     case 2: launch_mt<2>(p, a, s); break;
@@ -307,11 +350,7 @@ extern "C" int coopt_linear(const void* x, int64_t ldx, const void* w, int64_t l
     case 12: launch_mt<12>(p, a, s); break;
     default: launch_mt<16>(p, a, s); break;
   }
-  int rc = coopt::check_launch("coopt_linear");
-  if (rc != COOPT_OK || p.ks == 1) return rc;
-  const int64_t n4 = static_cast<int64_t>(M) * (N / 4);
-  hipLaunchKernelGGL(reduce_kernel, dim3(static_cast<unsigned>((n4 + 255) / 256)), dim3(256), 0,
-                     s, static_cast<const float*>(workspace), p.ks,
-                     static_cast<int64_t>(p.mt) * 16 * N, M, N, static_cast<uint16_t*>(y), ldy);
-  return coopt::check_launch("coopt_linear");
+  return coopt::check_launch(partials ? "coopt_linear_partials" : "coopt_linear");
 }
+
+}  // namespace

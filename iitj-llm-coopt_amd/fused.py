@@ -6,12 +6,14 @@ Counterparts of the vLLM ops the reference's forward calls (engine/model.py:234-
   silu_and_mul(gate_up, out=None)                      torch.ops._C.silu_and_mul
   linear(x, weight, out=None)                          F.linear projections (model.py:238-253)
 """
+import ctypes
+
 import torch
 import torch.nn.functional as F
 
 from . import _lib
 
-__all__ = ["rms_norm", "rope_", "silu_and_mul", "linear", "LINEAR_MAX_ROWS"]
+__all__ = ["rms_norm", "rope_", "silu_and_mul", "linear", "LinearPartials", "LINEAR_MAX_ROWS"]
 
 LINEAR_MAX_ROWS = 256
 _WS = _lib.WorkspaceCache()
@@ -22,8 +24,32 @@ def _bf16_rows(t, name):
         raise ValueError(f"{name} must be bf16 with a contiguous last dimension")
 
 
+class LinearPartials:
+    """The unreduced output of linear(..., defer_reduce=True): `ks` fp32 slices of shape
+    [rows_padded, N] in the linear workspace whose sum is the layer's output.  It is valid
+    until the next linear() call on the same stream (which reuses the workspace); rms_norm()
+    reduces it while reading."""
+
+    def __init__(self, buf, ks, rows, rows_padded, n, shape, device):
+        self.buf, self.ks, self.rows, self.rows_padded, self.n = buf, ks, rows, rows_padded, n
+        self.shape, self.device = shape, device
+
+    def reduce(self):
+        """The bf16 output itself (the sum of the slices in order, rounded once)."""
+        part = self.buf[: self.ks * self.rows_padded * self.n * 4].view(torch.float32)
+        part = part.view(self.ks, self.rows_padded, self.n)[:, : self.rows]
+        acc = part[0].clone()
+        for k in range(1, self.ks):
+            acc += part[k]
+        return acc.to(torch.bfloat16).view(self.shape)
+
+
 def rms_norm(x, weight, eps, residual=None, out=None):
-    """out = rmsnorm(x) * weight; with `residual`, first residual += x in place (fused add)."""
+    """out = rmsnorm(x) * weight; with `residual`, first residual += x in place (fused add).
+    x may be a LinearPartials (the split-K output of linear(..., defer_reduce=True)), reduced
+    in the same pass."""
+    if isinstance(x, LinearPartials):
+        return _rms_norm_partials(x, weight, eps, residual, out)
     _lib.require_cuda(x, weight, residual, out)
     for t, n in ((x, "x"), (weight, "weight")):
         _bf16_rows(t, n)
@@ -37,6 +63,22 @@ def rms_norm(x, weight, eps, residual=None, out=None):
     _lib.check(_lib.load().coopt_rms_norm(_lib.ptr(x), _lib.ptr(residual), _lib.ptr(weight),
                                           _lib.ptr(out), x2.shape[0], x2.shape[1], float(eps),
                                           _lib.stream_handle(x.device)), "coopt_rms_norm")
+    return out
+
+
+def _rms_norm_partials(xp, weight, eps, residual, out):
+    _lib.require_cuda(weight, residual, out)
+    _bf16_rows(weight, "weight")
+    if weight.numel() != xp.n or xp.n > 8192:
+        raise ValueError("weight must match the partials' width (at most 8192)")
+    if residual is not None and (tuple(residual.shape) != tuple(xp.shape) or not residual.is_contiguous()):
+        raise ValueError("residual must be contiguous with the layer output's shape")
+    if out is None:
+        out = torch.empty(xp.shape, dtype=torch.bfloat16, device=xp.device)
+    _lib.check(_lib.load().coopt_rms_norm_partials(
+        _lib.ptr(xp.buf), xp.ks, xp.rows_padded * xp.n, _lib.ptr(residual), _lib.ptr(weight),
+        _lib.ptr(out), xp.rows, xp.n, float(eps), _lib.stream_handle(xp.device)),
+        "coopt_rms_norm_partials")
     return out
 
 
@@ -72,7 +114,7 @@ def silu_and_mul(gate_up, out=None):
     return out
 
 
-def linear(x, weight, out=None):
+def linear(x, weight, out=None, defer_reduce=False):
     """x [..., K] @ weight[N, K]^T -> [..., N], bf16 with fp32 accumulation (no bias), as the
     reference's projections (F.linear at engine/model.py:238, 248, 250, 253).
 
@@ -80,7 +122,10 @@ def linear(x, weight, out=None):
     up to LINEAR_MAX_ROWS rows, and runs where it measured faster than torch's GEMM on MI355X:
     up to 64 rows (draft steps), or N <= 8192 outputs at any supported row count (the verify
     step's qkv / o / down projections).  Other shapes -- prefill-sized row counts, and the
-    wide gate_up / lm_head outputs at verify row counts -- go to torch (hipBLASLt)."""
+    wide gate_up / lm_head outputs at verify row counts -- go to torch (hipBLASLt).
+
+    defer_reduce=True (no `out`): on the kernel path, return a LinearPartials instead of the
+    tensor, for rms_norm() to reduce in its own pass; other paths return the tensor."""
     _lib.require_cuda(x, weight, out)
     K = x.shape[-1]
     N = weight.shape[0]
@@ -93,6 +138,15 @@ def linear(x, weight, out=None):
     if x2.stride(-1) != 1 or x2.stride(0) % 8 or weight.stride(-1) != 1 or weight.stride(0) % 8:
         x2 = x2.contiguous()
         weight = weight.contiguous()
+    if defer_reduce and out is None and N <= 8192:
+        ks, rp = ctypes.c_int(0), ctypes.c_int(0)
+        _lib.check(_lib.load().coopt_linear_split(M, N, K, ctypes.byref(ks), ctypes.byref(rp)),
+                   "coopt_linear_split")
+        ws = _WS.get(ks.value * rp.value * N * 4, x.device)
+        _lib.check(_lib.load().coopt_linear_partials(
+            _lib.ptr(x2), x2.stride(0), _lib.ptr(weight), weight.stride(0), M, N, K, _lib.ptr(ws),
+            ws.numel(), _lib.stream_handle(x.device)), "coopt_linear_partials")
+        return LinearPartials(ws, ks.value, M, rp.value, N, x.shape[:-1] + (N,), x.device)
     if out is None:
         out = torch.empty(x.shape[:-1] + (N,), dtype=torch.bfloat16, device=x.device)
     y2 = out.view(-1, N)

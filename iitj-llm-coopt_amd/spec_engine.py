@@ -126,9 +126,10 @@ class RandomLlama:
             ops.rope(q, k, pos, self.cos, self.sin)
             ops.write(kv, li, k, v, slots)
             attn = ops.attend(kv, li, q, meta, self.scale)
-            o = ops.linear(attn.reshape(T, H * D), L["o"])
+            # o and down feed only the fused add + norm, which reduces their split-K partials
+            o = ops.linear(attn.reshape(T, H * D), L["o"], defer_reduce=True)
             h = ops.rms_norm(o, x, L["ln2"], s.eps)
-            d = ops.linear(ops.silu_mul(ops.linear(h, L["gate_up"])), L["down"])
+            d = ops.linear(ops.silu_mul(ops.linear(h, L["gate_up"])), L["down"], defer_reduce=True)
         h = ops.rms_norm(d, x, self.norm, s.eps)
         return ops.linear(h, self.lm_head, out=logits_out)
 
@@ -197,8 +198,8 @@ class HipOps:
     def silu_mul(self, gate_up):
         return silu_and_mul(gate_up)
 
-    def linear(self, x, w, out=None):
-        return linear(x, w, out=out)
+    def linear(self, x, w, out=None, defer_reduce=False):
+        return linear(x, w, out=out, defer_reduce=defer_reduce)
 
     def attend(self, kv: PagedKV, layer, q, meta, scale):
         kc, vc, ks, vs = kv.layers[layer]

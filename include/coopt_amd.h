@@ -248,6 +248,15 @@ int coopt_rope(void* q, int64_t q_tok_stride, int64_t q_head_stride, void* k,
                const void* cos, const void* sin, int64_t table_stride, int max_pos, int T, int Hq,
                int Hkv, int D, coopt_stream_t stream);
 int coopt_silu_mul(const void* gate_up, void* out, int64_t T, int F, coopt_stream_t stream);
+/*
+ * coopt_rms_norm with x given as the fp32 split-K partials of the linear layer that produced
+ * it (coopt_linear_partials): x[row] = bf16(sum over k < ks, in order, of
+ * part[k * slice_stride + row * hidden + :]) -- the value coopt_linear would have written --
+ * then the fused add and the norm as coopt_rms_norm.  hidden <= 8192, 1 <= ks <= 16.
+ */
+int coopt_rms_norm_partials(const float* part, int ks, int64_t slice_stride, void* residual,
+                            const void* weight, void* out, int64_t rows, int hidden, float eps,
+                            coopt_stream_t stream);
 
 /*
  * Linear layer at decode / verify row counts: y[M, N] = x[M, K] w[N, K]^T, bf16 in and out,
@@ -262,6 +271,15 @@ int coopt_silu_mul(const void* gate_up, void* out, int64_t T, int F, coopt_strea
  *   rounding of the fp32 sum).
  */
 size_t coopt_linear_workspace(int M, int N, int K);
+/*
+ * The split-K plan of coopt_linear for (M, N, K): *ks K slices, each a [*rows_padded, N] fp32
+ * block of partial sums.  coopt_linear_partials runs the same kernel but leaves all ks slices
+ * in the workspace (ks * rows_padded * N * 4 bytes, also when ks == 1) instead of reducing
+ * them, for a consumer that reduces while it reads -- coopt_rms_norm_partials below.
+ */
+int coopt_linear_split(int M, int N, int K, int* ks, int* rows_padded);
+int coopt_linear_partials(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, int N,
+                          int K, void* workspace, size_t workspace_bytes, coopt_stream_t stream);
 int coopt_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, int N, int K,
                  void* y, int64_t ldy, void* workspace, size_t workspace_bytes,
                  coopt_stream_t stream);

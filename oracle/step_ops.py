@@ -37,7 +37,7 @@ class OracleOps:
         gate, up = gate_up.chunk(2, dim=-1)
         return torch.nn.functional.silu(gate) * up
 
-    def linear(self, x, w, out=None):
+    def linear(self, x, w, out=None, defer_reduce=False):
         # the projections, F.linear without bias (engine/model.py:238, 248, 250, 253)
         if out is not None:
             return torch.matmul(x, w.t(), out=out)

@@ -107,3 +107,28 @@ def test_linear_argument_errors(dev):
     assert L.coopt_linear(_lib.ptr(xx), 4096, _lib.ptr(ww), 4096, 160, 4096, 4096, _lib.ptr(yy), 4096,
                           None, 0, st) != 0
     assert "workspace" in _lib.last_error()
+
+
+@pytest.mark.parametrize("M,N,K", [(160, 4096, 4096), (160, 4096, 14336), (32, 2048, 2048),
+                                   (32, 2048, 8192), (17, 264, 256), (64, 2048, 128)])
+def test_deferred_reduction_into_rms_norm_is_bit_exact(dev, M, N, K):
+    """linear(defer_reduce=True) + rms_norm(partials) == linear() + rms_norm(), bit for bit,
+    with and without the fused residual add (the reduction order is the same)."""
+    g = torch.Generator(device=dev).manual_seed(M + N + K)
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    ln = (1 + 0.1 * torch.randn(N, generator=g, device=dev)).to(torch.bfloat16)
+    res = torch.randn(M, N, generator=g, device=dev).to(torch.bfloat16)
+    y = fused.linear(x, w)
+    part = fused.linear(x, w, defer_reduce=True)
+    assert isinstance(part, fused.LinearPartials)
+    print(f"[defer] M={M} N={N} K={K}: {part.ks} slice(s) of {part.rows_padded} rows", flush=True)
+    assert torch.equal(part.reduce(), y)
+    want = fused.rms_norm(y, ln, 1e-5)
+    got = fused.rms_norm(part, ln, 1e-5)
+    assert torch.equal(got, want)
+    r1, r2 = res.clone(), res.clone()
+    want = fused.rms_norm(y, ln, 1e-5, residual=r1)
+    part = fused.linear(x, w, defer_reduce=True)
+    got = fused.rms_norm(part, ln, 1e-5, residual=r2)
+    assert torch.equal(got, want) and torch.equal(r2, r1)
