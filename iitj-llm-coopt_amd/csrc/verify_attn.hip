@@ -27,10 +27,15 @@
 //           16 lanes: coalesced) and the transpose to "8 keys of one d" is a byte select in
 //           registers (v_perm / v_cvt_f32_ubyte) -- no LDS staging.  Lane l's accumulators
 //           hold row m and d = (4g + i)*(D/16) + dt.
-// INT8 KV: every K and V code is dequantised to bf16(float(code) * scale) -- the value
+// INT8 KV.  K: every code is dequantised to bf16(float(code) * scale) -- the value
 // dequantize() returns (engine/kv_tier_manager.py:41), which the reference attends over --
-// as (code + 128) * s - 128 * s in one fma, exact before the single bf16 rounding; the
-// MFMA stages are then those of the bf16 path.
+// as (code + 128) * s - 128 * s in one fma, exact before the single bf16 rounding, so the
+// score MFMAs see the reference's operands.  V: the codes enter the PV MFMAs
+// (v_mfma_f32_16x16x32_f16) as exact fp16 integers -- two byte selects place (code + 128)
+// under a 0x64 exponent byte, giving 1024 + code + 128 exactly, and one packed fp16 add
+// removes the 1152 -- and each key's V scale is folded into its probability, fp16(p * s_v).
+// That replaces bf16(p) * bf16(code * s_v) by one fp16 rounding of the product (11 bits
+// against two 8-bit roundings) at a third of the VALU work per V element.
 #include <math.h>
 
 #include "common.h"
@@ -79,8 +84,28 @@ __device__ __forceinline__ f32x4_t mfma_bf16(u32x4_t a, u32x4_t b, f32x4_t c) {
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f32x4_t mfma_f16(u32x4_t a, u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+// Two fp32 -> packed fp16x2, round to nearest even.
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), f16x2_t));
+}
+
+// Two (code + 128) bytes already placed as the low bytes of two fp16 words whose high bytes
+// are 0x64 -> the fp16 pair (code, code): 1024 + u is exact in fp16, and so is u - 128.
+__device__ __forceinline__ uint32_t codes_f16x2(uint32_t biased) {
+  const f16x2_t v = __builtin_bit_cast(f16x2_t, biased) + f16x2_t{-1152.0f16, -1152.0f16};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 // Two fp32 -> packed bf16x2, round to nearest even (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
@@ -327,22 +352,32 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
       for (int j = 0; j < 8; ++j)
 #pragma unroll
         for (int w = 0; w < Raw::kVWords; ++w) vx[j][w] = INT8 ? (raw.v[j][w] ^ 0x80808080u) : raw.v[j][w];
+      if constexpr (INT8) {
+        // exact fp16 codes; the V scales go into P (below).  Two byte selects interleave
+        // keys j0, j1 over four d's, two more place each pair under the 0x64 exponent bytes.
+        constexpr uint32_t k64 = 0x64646464u;
 #pragma unroll
-      for (int dt = 0; dt < kDt; ++dt)
+        for (int w = 0; w < Raw::kVWords; ++w)
 #pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) {
-          const int j0 = 2 * e2, j1 = 2 * e2 + 1;  // keys of k-elements 2*e2, 2*e2+1
-          if constexpr (INT8) {
-            const int w = dt >> 2, byte = dt & 3;
-            const float s0 = scale_of(raw.vs[j0 >> 2], j0 & 3), s1 = scale_of(raw.vs[j1 >> 2], j1 & 3);
-            const float x0 = dequant_byte(vx[j0][w], byte, s0, -128.0f * s0);
-            const float x1 = dequant_byte(vx[j1][w], byte, s1, -128.0f * s1);
-            va[dt][e2] = pack_bf16x2(x0, x1);
-          } else {
+          for (int e2 = 0; e2 < 4; ++e2) {
+            const int j0 = 2 * e2, j1 = 2 * e2 + 1;  // keys of k-elements 2*e2, 2*e2+1
+            const uint32_t lo = __builtin_amdgcn_perm(vx[j1][w], vx[j0][w], 0x05010400u);
+            const uint32_t hi = __builtin_amdgcn_perm(vx[j1][w], vx[j0][w], 0x07030602u);
+            va[4 * w + 0][e2] = codes_f16x2(__builtin_amdgcn_perm(k64, lo, 0x04010400u));
+            va[4 * w + 1][e2] = codes_f16x2(__builtin_amdgcn_perm(k64, lo, 0x04030402u));
+            va[4 * w + 2][e2] = codes_f16x2(__builtin_amdgcn_perm(k64, hi, 0x04010400u));
+            va[4 * w + 3][e2] = codes_f16x2(__builtin_amdgcn_perm(k64, hi, 0x04030402u));
+          }
+      } else {
+#pragma unroll
+        for (int dt = 0; dt < kDt; ++dt)
+#pragma unroll
+          for (int e2 = 0; e2 < 4; ++e2) {
+            const int j0 = 2 * e2, j1 = 2 * e2 + 1;  // keys of k-elements 2*e2, 2*e2+1
             const int w = dt >> 1;
             va[dt][e2] = __builtin_amdgcn_perm(vx[j1][w], vx[j0][w], (dt & 1) ? 0x07060302u : 0x05040100u);
           }
-        }
+      }
     }
 
     // ---- scores: S^T = K . Q^T, K operands built per k-step ----
@@ -438,10 +473,22 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
           psum += p[kt][i];
         }
       l_run[rt] += psum;
-      pb[rt][0] = pack_bf16x2(p[0][0], p[0][1]);
-      pb[rt][1] = pack_bf16x2(p[0][2], p[0][3]);
-      pb[rt][2] = pack_bf16x2(p[1][0], p[1][1]);
-      pb[rt][3] = pack_bf16x2(p[1][2], p[1][3]);
+      if constexpr (INT8) {
+        // P' = p * s_v of the lane's key j = 4 kt + i, in fp16 next to the fp16 codes
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) p[kt][i] *= scale_of(raw.vs[kt], i);
+        pb[rt][0] = pack_f16x2(p[0][0], p[0][1]);
+        pb[rt][1] = pack_f16x2(p[0][2], p[0][3]);
+        pb[rt][2] = pack_f16x2(p[1][0], p[1][1]);
+        pb[rt][3] = pack_f16x2(p[1][2], p[1][3]);
+      } else {
+        pb[rt][0] = pack_bf16x2(p[0][0], p[0][1]);
+        pb[rt][1] = pack_bf16x2(p[0][2], p[0][3]);
+        pb[rt][2] = pack_bf16x2(p[1][0], p[1][1]);
+        pb[rt][3] = pack_bf16x2(p[1][2], p[1][3]);
+      }
     }
 
     // ---- O^T += V^T . P^T ----
@@ -450,7 +497,7 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
         const u32x4_t pbv = {pb[rt][0], pb[rt][1], pb[rt][2], pb[rt][3]};
-        o[rt][dt] = mfma_bf16(va[dt], pbv, o[rt][dt]);
+        o[rt][dt] = INT8 ? mfma_f16(va[dt], pbv, o[rt][dt]) : mfma_bf16(va[dt], pbv, o[rt][dt]);
       }
   };
 

@@ -4,8 +4,8 @@ package's drop-in surfaces (which call the C ABI).
 Bar: INT8/INT4 codes and fp16 scales bit-exact (torch-GPU semantics of
 engine/kv_tier_manager.py:21-31); accepted lengths and tokens bit-exact except where the
 fixture's margin marks a tie (< 1e-6, printed); attention within 2e-2 (bf16 KV) and 5e-2
-(INT8 KV) of the float64 result in |out - ref| / max(1, |ref|), and the INT8 path within one
-bf16 rounding of the bf16 path on the dequantised cache.
+(INT8 KV) of the float64 result in |out - ref| / max(1, |ref|), and the INT8 path within 2^-5
+of the bf16 path on the dequantised cache.
 """
 import os
 
@@ -140,5 +140,6 @@ def test_attention_kernel_matches_fixture(dev):
     print(f"[attention_tiny] scaled err int8 {err8:.3g} bf16 {errb:.3g} (max-abs {raw:.3g})",
           flush=True)
     assert errb <= 2e-2 and err8 <= 5e-2
-    # same bf16 operands, only the fp32 summation order inside the score MFMAs differs
-    assert ((out8.float() - outb.float()).abs() / outb.float().abs().clamp(min=1.0)).max() <= 2.0 ** -7
+    # K operands identical; V enters as exact fp16 codes with fp16(p * s_v) against
+    # bf16(p) * bf16(code * s_v) on the bf16 path
+    assert ((out8.float() - outb.float()).abs() / outb.float().abs().clamp(min=1.0)).max() <= 2.0 ** -5
