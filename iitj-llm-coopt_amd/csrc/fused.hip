@@ -175,19 +175,37 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(uint16_t* __restrict__ q
   base[i + half] = round_bf16(x2 * c + x1 * s);
 }
 
+__device__ __forceinline__ uint32_t pack_sum_bf16(float a, float b) {
+  return round_bf16(a) | (static_cast<uint32_t>(round_bf16(b)) << 16);
+}
+
 // out[t, j] = silu(gu[t, j]) * gu[t, F + j] (engine/model.py:250-253), 8 elements per thread.
+// With `part` set, gu is not read: gu[t] = bf16(sum of the ks fp32 slices part[k * slice +
+// t * 2F]), the split-K partials of the gate_up projection, reduced in its own order.
 __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __restrict__ gu,
                                                             uint16_t* __restrict__ out, int64_t T,
-                                                            int F) {
+                                                            int F, const float* __restrict__ part,
+                                                            int ks, int64_t slice) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   const int per_row = F / 8;
   if (gid >= T * per_row) return;
   const int64_t t = gid / per_row;
   const int j = static_cast<int>(gid % per_row) * 8;
-  const uint4 gv = *reinterpret_cast<const uint4*>(gu + t * 2 * F + j);
-  const uint4 uv = *reinterpret_cast<const uint4*>(gu + t * 2 * F + F + j);
-  const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
-  const uint32_t uw[4] = {uv.x, uv.y, uv.z, uv.w};
+  uint32_t gw[4], uw[4];
+  if (part) {
+    const float* pg = part + t * 2 * F + j;
+    const float4 g0 = sum_partials4(pg, ks, slice), g1 = sum_partials4(pg + 4, ks, slice);
+    const float4 u0 = sum_partials4(pg + F, ks, slice), u1 = sum_partials4(pg + F + 4, ks, slice);
+    gw[0] = pack_sum_bf16(g0.x, g0.y); gw[1] = pack_sum_bf16(g0.z, g0.w);
+    gw[2] = pack_sum_bf16(g1.x, g1.y); gw[3] = pack_sum_bf16(g1.z, g1.w);
+    uw[0] = pack_sum_bf16(u0.x, u0.y); uw[1] = pack_sum_bf16(u0.z, u0.w);
+    uw[2] = pack_sum_bf16(u1.x, u1.y); uw[3] = pack_sum_bf16(u1.z, u1.w);
+  } else {
+    const uint4 gv = *reinterpret_cast<const uint4*>(gu + t * 2 * F + j);
+    const uint4 uv = *reinterpret_cast<const uint4*>(gu + t * 2 * F + F + j);
+    gw[0] = gv.x; gw[1] = gv.y; gw[2] = gv.z; gw[3] = gv.w;
+    uw[0] = uv.x; uw[1] = uv.y; uw[2] = uv.z; uw[3] = uv.w;
+  }
   uint32_t ow[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -288,6 +306,23 @@ extern "C" int coopt_silu_mul(const void* gate_up, void* out, int64_t T, int F,
   const int64_t total = T * (F / 8);
   hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)),
                      dim3(kThreads), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(out), T, F);
+                     static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(out), T, F,
+                     nullptr, 0, 0);
   return coopt::check_launch("coopt_silu_mul");
+}
+
+extern "C" int coopt_silu_mul_partials(const float* part, int ks, int64_t slice_stride, void* out,
+                                       int64_t T, int F, coopt_stream_t stream) {
+  COOPT_REQUIRE(T >= 0 && F > 0 && F % 8 == 0, "F must be a multiple of 8");
+  COOPT_REQUIRE(ks >= 1 && ks <= 16, "1 to 16 partial slices");
+  COOPT_REQUIRE(slice_stride >= T * 2 * F && slice_stride % 4 == 0, "bad slice stride");
+  if (T == 0) return COOPT_OK;
+  COOPT_REQUIRE(part && out && coopt::aligned16(part) && coopt::aligned16(out),
+                "null or misaligned pointer");
+  coopt::clear_error();
+  const int64_t total = T * (F / 8);
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, static_cast<hipStream_t>(stream), nullptr,
+                     static_cast<uint16_t*>(out), T, F, part, ks, slice_stride);
+  return coopt::check_launch("coopt_silu_mul_partials");
 }

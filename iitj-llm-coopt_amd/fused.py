@@ -28,7 +28,7 @@ class LinearPartials:
     """The unreduced output of linear(..., defer_reduce=True): `ks` fp32 slices of shape
     [rows_padded, N] in the linear workspace whose sum is the layer's output.  It is valid
     until the next linear() call on the same stream (which reuses the workspace); rms_norm()
-    reduces it while reading."""
+    and silu_and_mul() reduce it while reading."""
 
     def __init__(self, buf, ks, rows, rows_padded, n, shape, device):
         self.buf, self.ks, self.rows, self.rows_padded, self.n = buf, ks, rows, rows_padded, n
@@ -101,7 +101,20 @@ def rope_(q, k, positions, cos, sin):
 
 
 def silu_and_mul(gate_up, out=None):
-    """[T, 2F] -> [T, F]: silu(gate) * up."""
+    """[T, 2F] -> [T, F]: silu(gate) * up.  gate_up may be a LinearPartials (the split-K output
+    of linear(..., defer_reduce=True)), reduced in the same pass."""
+    if isinstance(gate_up, LinearPartials):
+        xp = gate_up
+        _lib.require_cuda(out)
+        F = xp.n // 2
+        if xp.n % 16:
+            raise ValueError("gate_up width must be a multiple of 16")
+        if out is None:
+            out = torch.empty(xp.shape[:-1] + (F,), dtype=torch.bfloat16, device=xp.device)
+        _lib.check(_lib.load().coopt_silu_mul_partials(
+            _lib.ptr(xp.buf), xp.ks, xp.rows_padded * xp.n, _lib.ptr(out), xp.rows, F,
+            _lib.stream_handle(xp.device)), "coopt_silu_mul_partials")
+        return out
     _lib.require_cuda(gate_up, out)
     _bf16_rows(gate_up, "gate_up")
     if not gate_up.is_contiguous():
@@ -125,7 +138,8 @@ def linear(x, weight, out=None, defer_reduce=False):
     wide gate_up / lm_head outputs at verify row counts -- go to torch (hipBLASLt).
 
     defer_reduce=True (no `out`): on the kernel path, return a LinearPartials instead of the
-    tensor, for rms_norm() to reduce in its own pass; other paths return the tensor."""
+    tensor, for rms_norm() or silu_and_mul() to reduce in their own pass; other paths return
+    the tensor."""
     _lib.require_cuda(x, weight, out)
     K = x.shape[-1]
     N = weight.shape[0]
@@ -138,7 +152,7 @@ def linear(x, weight, out=None, defer_reduce=False):
     if x2.stride(-1) != 1 or x2.stride(0) % 8 or weight.stride(-1) != 1 or weight.stride(0) % 8:
         x2 = x2.contiguous()
         weight = weight.contiguous()
-    if defer_reduce and out is None and N <= 8192:
+    if defer_reduce and out is None:
         ks, rp = ctypes.c_int(0), ctypes.c_int(0)
         _lib.check(_lib.load().coopt_linear_split(M, N, K, ctypes.byref(ks), ctypes.byref(rp)),
                    "coopt_linear_split")

@@ -126,10 +126,12 @@ class RandomLlama:
             ops.rope(q, k, pos, self.cos, self.sin)
             ops.write(kv, li, k, v, slots)
             attn = ops.attend(kv, li, q, meta, self.scale)
-            # o and down feed only the fused add + norm, which reduces their split-K partials
+            # o, gate_up and down feed only the fused add + norm or SiLU, which reduce their
+            # split-K partials as they read them
             o = ops.linear(attn.reshape(T, H * D), L["o"], defer_reduce=True)
             h = ops.rms_norm(o, x, L["ln2"], s.eps)
-            d = ops.linear(ops.silu_mul(ops.linear(h, L["gate_up"])), L["down"], defer_reduce=True)
+            gu = ops.linear(h, L["gate_up"], defer_reduce=True)
+            d = ops.linear(ops.silu_mul(gu), L["down"], defer_reduce=True)
         h = ops.rms_norm(d, x, self.norm, s.eps)
         return ops.linear(h, self.lm_head, out=logits_out)
 

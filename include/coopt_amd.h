@@ -254,6 +254,13 @@ int coopt_silu_mul(const void* gate_up, void* out, int64_t T, int F, coopt_strea
  * part[k * slice_stride + row * hidden + :]) -- the value coopt_linear would have written --
  * then the fused add and the norm as coopt_rms_norm.  hidden <= 8192, 1 <= ks <= 16.
  */
+/*
+ * coopt_silu_mul with gate_up given as fp32 split-K partials (coopt_linear_partials of the
+ * gate_up projection): gate_up[t] = bf16(sum over k < ks, in order, of
+ * part[k * slice_stride + t * 2F + :]), then silu(gate) * up as coopt_silu_mul.  1 <= ks <= 16.
+ */
+int coopt_silu_mul_partials(const float* part, int ks, int64_t slice_stride, void* out,
+                            int64_t T, int F, coopt_stream_t stream);
 int coopt_rms_norm_partials(const float* part, int ks, int64_t slice_stride, void* residual,
                             const void* weight, void* out, int64_t rows, int hidden, float eps,
                             coopt_stream_t stream);

@@ -132,3 +132,15 @@ def test_deferred_reduction_into_rms_norm_is_bit_exact(dev, M, N, K):
     part = fused.linear(x, w, defer_reduce=True)
     got = fused.rms_norm(part, ln, 1e-5, residual=r2)
     assert torch.equal(got, want) and torch.equal(r2, r1)
+
+
+@pytest.mark.parametrize("M,F,K", [(32, 8192, 2048), (64, 8192, 2048), (5, 64, 256)])
+def test_deferred_reduction_into_silu_mul_is_bit_exact(dev, M, F, K):
+    """linear(defer_reduce=True) + silu_and_mul(partials) == linear() + silu_and_mul()."""
+    g = torch.Generator(device=dev).manual_seed(M + F + K)
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn(2 * F, K, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    want = fused.silu_and_mul(fused.linear(x, w))
+    part = fused.linear(x, w, defer_reduce=True)
+    print(f"[defer silu] M={M} F={F} K={K}: {part.ks} slice(s)", flush=True)
+    assert torch.equal(fused.silu_and_mul(part), want)
