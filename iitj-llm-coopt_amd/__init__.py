@@ -17,7 +17,8 @@ from .attention import flash_attn_varlen_func, paged_attention
 from .batch import Batch, WorkItem, build_batch, build_padded_batch
 from .block_manager import BlockManager, OutOfBlocks
 from .kv_blocks import allocate_block_major_kv, copy_blocks, migrate_out_of
-from .kv_cache import allocate_kv_cache, dequantize, quantize, reshape_and_cache_flash
+from .kv_cache import (allocate_kv_cache, dequantize, qkv_rope_and_cache, quantize,
+                       reshape_and_cache_flash)
 from .kv_tier import KVTierManager, SwappedKV, swap_in_blocks, swap_out_blocks
 from .spec_decode import AcceptResult, accept, sample, softmax, verify
 
@@ -26,5 +27,5 @@ __all__ = [
     "build_padded_batch", "BlockManager", "OutOfBlocks", "allocate_kv_cache", "dequantize",
     "quantize", "reshape_and_cache_flash", "AcceptResult", "accept", "sample", "softmax",
     "verify", "KVTierManager", "SwappedKV", "swap_in_blocks", "swap_out_blocks",
-    "allocate_block_major_kv", "copy_blocks", "migrate_out_of",
+    "allocate_block_major_kv", "copy_blocks", "migrate_out_of", "qkv_rope_and_cache",
 ]

@@ -40,6 +40,9 @@ SIGNATURES = {
     "coopt_linear_partials": (_i, [_p, _i64, _p, _i64, _i, _i, _i, _p, _sz, _p]),
     "coopt_rms_norm_partials": (_i, [_p, _i, _i64, _p, _p, _p, _i64, _i, _f, _p]),
     "coopt_silu_mul_partials": (_i, [_p, _i, _i64, _p, _i64, _i, _p]),
+    "coopt_qkv_epilogue": (_i, [_i, _p, _i64, _p, _i, _i64, _p, _p, _p, _i64, _i, _p, _i64, _i64,
+                                _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i, _i, _i,
+                                _i, _i, _i64, _p]),
     "coopt_verify_attention_workspace": (_sz, [_i, _i, _i, _i, _i, _i]),
     "coopt_verify_attention": (_i, [_i, _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _i64,
                                     _i64, _i64, _p, _i64, _p, _p, _i, _i, _i, _i, _i, _i64, _i,

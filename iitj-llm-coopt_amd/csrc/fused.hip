@@ -171,8 +171,10 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(uint16_t* __restrict__ q
   const float c = bf16_to_f32(cos[p * tab_stride + i]);
   const float s = bf16_to_f32(sin[p * tab_stride + i]);
   const float x1 = bf16_to_f32(base[i]), x2 = bf16_to_f32(base[i + half]);
-  base[i] = round_bf16(x1 * c - x2 * s);
-  base[i + half] = round_bf16(x2 * c + x1 * s);
+  // explicit fma forms, shared with the fused qkv epilogue (one rounding of x1 c - x2 s via
+  // fma(x1, c, -(x2 s)), and of x2 c + x1 s via fma(x2, c, x1 s))
+  base[i] = round_bf16(fmaf(x1, c, -(x2 * s)));
+  base[i + half] = round_bf16(fmaf(x2, c, x1 * s));
 }
 
 __device__ __forceinline__ uint32_t pack_sum_bf16(float a, float b) {

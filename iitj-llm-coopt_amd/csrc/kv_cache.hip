@@ -31,28 +31,13 @@ __device__ __forceinline__ int quant_code(float x, float s32) {
 // (an aligned power-of-two group inside the wave) cover one vector, and each lane handles
 // the same chunk of K and of V, so every load and store is a 16- or 8-byte access.
 // ---------------------------------------------------------------------------------------
+// Lane c of a G-lane group stores elements [8c, 8c + 8) of one (token, head) K and V vector
+// at cache element offset c_off: bf16 as is, or INT8 codes with the group's fp16 scale at
+// s_off (kv_tier_manager.quantize(x, 8) per vector, engine/kv_tier_manager.py:21-31).
 template <int G, bool INT8>
-__global__ __launch_bounds__(256) void kv_write_kernel(
-    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t k_ts, int64_t k_hs,
-    int64_t v_ts, int64_t v_hs, void* __restrict__ kc, void* __restrict__ vc, int64_t c_bs, int64_t c_ts, int64_t c_hs,
-    uint16_t* __restrict__ ks, uint16_t* __restrict__ vs, int64_t s_bs, int64_t s_ts, int64_t s_hs,
-    const int64_t* __restrict__ slot_mapping, int T, int Hkv, int block_size, int64_t num_slots) {
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int c = static_cast<int>(gid % G);
-  const int64_t vec = gid / G;
-  // Groups are aligned inside the wave, so a whole group leaves together.
-  if (vec >= static_cast<int64_t>(T) * Hkv) return;
-  const int t = static_cast<int>(vec / Hkv);
-  const int h = static_cast<int>(vec % Hkv);
-  const int64_t slot = slot_mapping[t];
-  if (slot < 0 || slot >= num_slots) return;
-  const int64_t blk = slot / block_size;
-  const int64_t off = slot % block_size;
-
-  const uint4 kr = *reinterpret_cast<const uint4*>(k + t * k_ts + h * k_hs + c * 8);
-  const uint4 vr = *reinterpret_cast<const uint4*>(v + t * v_ts + h * v_hs + c * 8);
-  const int64_t c_off = blk * c_bs + off * c_ts + h * c_hs + c * 8;
-
+__device__ __forceinline__ void store_kv_chunk(uint4 kr, uint4 vr, void* kc, void* vc,
+                                               int64_t c_off, uint16_t* ks, uint16_t* vs,
+                                               int64_t s_off, int c) {
   if constexpr (!INT8) {
     *reinterpret_cast<uint4*>(static_cast<uint16_t*>(kc) + c_off) = kr;
     *reinterpret_cast<uint4*>(static_cast<uint16_t*>(vc) + c_off) = vr;
@@ -85,11 +70,135 @@ __global__ __launch_bounds__(256) void kv_write_kernel(
     *reinterpret_cast<uint2*>(static_cast<int8_t*>(kc) + c_off) = make_uint2(kq[0], kq[1]);
     *reinterpret_cast<uint2*>(static_cast<int8_t*>(vc) + c_off) = make_uint2(vq[0], vq[1]);
     if (c == 0) {
-      const int64_t s_off = blk * s_bs + off * s_ts + h * s_hs;
       ks[s_off] = f32_to_f16(ksc);
       vs[s_off] = f32_to_f16(vsc);
     }
   }
+}
+
+template <int G, bool INT8>
+__global__ __launch_bounds__(256) void kv_write_kernel(
+    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t k_ts, int64_t k_hs,
+    int64_t v_ts, int64_t v_hs, void* __restrict__ kc, void* __restrict__ vc, int64_t c_bs, int64_t c_ts, int64_t c_hs,
+    uint16_t* __restrict__ ks, uint16_t* __restrict__ vs, int64_t s_bs, int64_t s_ts, int64_t s_hs,
+    const int64_t* __restrict__ slot_mapping, int T, int Hkv, int block_size, int64_t num_slots) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int c = static_cast<int>(gid % G);
+  const int64_t vec = gid / G;
+  // Groups are aligned inside the wave, so a whole group leaves together.
+  if (vec >= static_cast<int64_t>(T) * Hkv) return;
+  const int t = static_cast<int>(vec / Hkv);
+  const int h = static_cast<int>(vec % Hkv);
+  const int64_t slot = slot_mapping[t];
+  if (slot < 0 || slot >= num_slots) return;
+  const int64_t blk = slot / block_size;
+  const int64_t off = slot % block_size;
+
+  const uint4 kr = *reinterpret_cast<const uint4*>(k + t * k_ts + h * k_hs + c * 8);
+  const uint4 vr = *reinterpret_cast<const uint4*>(v + t * v_ts + h * v_hs + c * 8);
+  const int64_t c_off = blk * c_bs + off * c_ts + h * c_hs + c * 8;
+  store_kv_chunk<G, INT8>(kr, vr, kc, vc, c_off, ks, vs, blk * s_bs + off * s_ts + h * s_hs, c);
+}
+
+// ---------------------------------------------------------------------------------------
+// qkv epilogue: the chain  F.linear(h, qkv).split -> rotary_embedding(q, k) ->
+// reshape_and_cache_flash(k, v)  of engine/model.py:238-243 after the qkv projection, in one
+// launch.  A G-lane group (G = D/8) owns one (token, head) vector of the T x (Hq + Hkv) q and
+// k heads; k groups also carry their token's v head.  The input row is either the bf16 qkv
+// output or the fp32 split-K partials of the projection (reduced here in the order
+// coopt_linear's reduction uses, then rounded to bf16 as it would be).  RoPE (neox halves)
+// pairs element i with i + D/2, which lives in lane c ^ (G/2) of the same group: one
+// shuffle per word.  q heads go to q_out; k (rotated) and v go to the paged cache exactly as
+// coopt_kv_write stores them, and rows with slot < 0 write no cache entry.
+// ---------------------------------------------------------------------------------------
+struct QkvArgs {
+  const uint16_t* qkv;
+  int64_t qkv_ts;
+  const float* part;
+  int ks;
+  int64_t slice;
+  const int64_t* pos;
+  const uint16_t* cos;
+  const uint16_t* sin;
+  int64_t tab_stride;
+  int max_pos;
+  uint16_t* q_out;
+  int64_t q_ts, q_hs;
+  void* kc;
+  void* vc;
+  int64_t c_bs, c_ts, c_hs;
+  uint16_t* k_scale;
+  uint16_t* v_scale;
+  int64_t s_bs, s_ts, s_hs;
+  const int64_t* slot_mapping;
+  int T, Hq, Hkv, D, block_size;
+  int64_t num_slots;
+};
+
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+  return f32_to_bf16(a) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+}
+
+// Elements [col, col + 8) of row t: bf16 from the qkv output, or bf16(sum of the partials).
+__device__ __forceinline__ uint4 qkv_chunk(const QkvArgs& a, int t, int64_t col) {
+  if (a.part) {
+    const float* p = a.part + static_cast<int64_t>(t) * (a.Hq + 2 * a.Hkv) * a.D + col;
+    const float4 lo = sum_partials4(p, a.ks, a.slice), hi = sum_partials4(p + 4, a.ks, a.slice);
+    return make_uint4(pack2_bf16(lo.x, lo.y), pack2_bf16(lo.z, lo.w), pack2_bf16(hi.x, hi.y),
+                      pack2_bf16(hi.z, hi.w));
+  }
+  return *reinterpret_cast<const uint4*>(a.qkv + static_cast<int64_t>(t) * a.qkv_ts + col);
+}
+
+template <int G, bool INT8>
+__global__ __launch_bounds__(256) void qkv_epilogue_kernel(QkvArgs a) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int c = static_cast<int>(gid % G);
+  const int64_t vec = gid / G;
+  const int heads = a.Hq + a.Hkv;
+  if (vec >= static_cast<int64_t>(a.T) * heads) return;  // whole groups leave together
+  const int t = static_cast<int>(vec / heads), h = static_cast<int>(vec % heads);
+  const int D = G * 8;
+  const uint4 xr = qkv_chunk(a, t, static_cast<int64_t>(h) * D + c * 8);
+  // partner words (elements i +- D/2) from lane c ^ (G/2)
+  uint32_t xw[4] = {xr.x, xr.y, xr.z, xr.w}, pw[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) pw[e] = __shfl_xor(xw[e], G / 2, COOPT_WAVE);
+  int64_t p = a.pos[t];
+  p = p < 0 ? 0 : (p >= a.max_pos ? a.max_pos - 1 : p);
+  const bool first = c < G / 2;
+  const int i0 = (first ? c : c - G / 2) * 8;
+  const uint16_t* cp = a.cos + p * a.tab_stride + i0;
+  const uint16_t* sp = a.sin + p * a.tab_stride + i0;
+  const uint4 cr = *reinterpret_cast<const uint4*>(cp), sr = *reinterpret_cast<const uint4*>(sp);
+  const uint32_t cw[4] = {cr.x, cr.y, cr.z, cr.w}, sw[4] = {sr.x, sr.y, sr.z, sr.w};
+  uint32_t yw[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float y[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const float x = bf16_to_f32(static_cast<uint16_t>(xw[e] >> (16 * hh)));
+      const float xp = bf16_to_f32(static_cast<uint16_t>(pw[e] >> (16 * hh)));
+      const float cs = bf16_to_f32(static_cast<uint16_t>(cw[e] >> (16 * hh)));
+      const float sn = bf16_to_f32(static_cast<uint16_t>(sw[e] >> (16 * hh)));
+      // first half: x1 c - x2 s; second half: x2 c + x1 s (x = own element, xp = partner)
+      y[hh] = first ? fmaf(x, cs, -(xp * sn)) : fmaf(x, cs, xp * sn);
+    }
+    yw[e] = pack2_bf16(y[0], y[1]);
+  }
+  const uint4 yr = make_uint4(yw[0], yw[1], yw[2], yw[3]);
+  if (h < a.Hq) {
+    *reinterpret_cast<uint4*>(a.q_out + t * a.q_ts + h * a.q_hs + c * 8) = yr;
+    return;
+  }
+  const int hk = h - a.Hq;
+  const int64_t slot = a.slot_mapping[t];
+  if (slot < 0 || slot >= a.num_slots) return;  // padding row: the group leaves together
+  const uint4 vr = qkv_chunk(a, t, static_cast<int64_t>(a.Hq + a.Hkv + hk) * D + c * 8);
+  const int64_t blk = slot / a.block_size, off = slot % a.block_size;
+  store_kv_chunk<G, INT8>(yr, vr, a.kc, a.vc, blk * a.c_bs + off * a.c_ts + hk * a.c_hs + c * 8,
+                          a.k_scale, a.v_scale, blk * a.s_bs + off * a.s_ts + hk * a.s_hs, c);
 }
 
 template <bool INT8>
@@ -404,6 +513,78 @@ int dispatch_swap(bool out, int bits, int cache_dtype, const void* cache, int64_
 }
 
 }  // namespace
+
+extern "C" int coopt_qkv_epilogue(int cache_dtype, const void* qkv, int64_t qkv_tok_stride,
+                                  const float* part, int ks, int64_t slice_stride,
+                                  const int64_t* positions, const void* cos, const void* sin,
+                                  int64_t table_stride, int max_pos, void* q_out,
+                                  int64_t q_tok_stride, int64_t q_head_stride, void* k_cache,
+                                  void* v_cache, int64_t c_blk_stride, int64_t c_tok_stride,
+                                  int64_t c_head_stride, void* k_scale, void* v_scale,
+                                  int64_t s_blk_stride, int64_t s_tok_stride,
+                                  int64_t s_head_stride, const int64_t* slot_mapping, int T,
+                                  int Hq, int Hkv, int D, int block_size, int64_t num_blocks,
+                                  coopt_stream_t stream) {
+  coopt::clear_error();
+  COOPT_REQUIRE(cache_dtype == COOPT_DT_BF16 || cache_dtype == COOPT_DT_I8,
+                "cache_dtype must be COOPT_DT_BF16 or COOPT_DT_I8");
+  COOPT_REQUIRE(T >= 0 && Hq > 0 && Hkv > 0 && block_size > 0 && num_blocks > 0 && max_pos > 0,
+                "bad sizes");
+  COOPT_REQUIRE(D == 64 || D == 128 || D == 256, "D must be 64, 128 or 256");
+  if (T == 0) return COOPT_OK;
+  COOPT_REQUIRE((qkv != nullptr) != (part != nullptr), "give exactly one of qkv and part");
+  COOPT_REQUIRE(positions && cos && sin && q_out && k_cache && v_cache && slot_mapping,
+                "null pointer");
+  if (part) {
+    COOPT_REQUIRE(ks >= 1 && ks <= 16, "1 to 16 partial slices");
+    COOPT_REQUIRE(coopt::aligned16(part) && slice_stride % 4 == 0 &&
+                      slice_stride >= static_cast<int64_t>(T) * (Hq + 2 * Hkv) * D,
+                  "partials must be 16-byte aligned [ks, >= T, (Hq + 2 Hkv) D] fp32");
+  } else {
+    COOPT_REQUIRE(coopt::aligned16(qkv) && qkv_tok_stride % 8 == 0 &&
+                      qkv_tok_stride >= static_cast<int64_t>(Hq + 2 * Hkv) * D,
+                  "qkv rows must be 16-byte aligned, at least (Hq + 2 Hkv) D wide");
+  }
+  COOPT_REQUIRE(coopt::aligned16(cos) && coopt::aligned16(sin) && table_stride % 8 == 0 &&
+                    table_stride >= D / 2,
+                "cos/sin rows must be 16-byte aligned with at least D/2 entries");
+  COOPT_REQUIRE(coopt::aligned16(q_out) && q_tok_stride % 8 == 0 && q_head_stride % 8 == 0,
+                "q_out rows must be 16-byte aligned");
+  const bool int8 = cache_dtype == COOPT_DT_I8;
+  if (int8) {
+    COOPT_REQUIRE(k_scale && v_scale, "INT8 cache needs k_scale and v_scale");
+    COOPT_REQUIRE((reinterpret_cast<uintptr_t>(k_cache) & 7u) == 0 &&
+                      (reinterpret_cast<uintptr_t>(v_cache) & 7u) == 0 && c_blk_stride % 8 == 0 &&
+                      c_tok_stride % 8 == 0 && c_head_stride % 8 == 0,
+                  "INT8 cache rows must be 8-byte aligned");
+  } else {
+    COOPT_REQUIRE(coopt::aligned16(k_cache) && coopt::aligned16(v_cache) &&
+                      c_blk_stride % 8 == 0 && c_tok_stride % 8 == 0 && c_head_stride % 8 == 0,
+                  "bf16 cache rows must be 16-byte aligned");
+  }
+  QkvArgs a{static_cast<const uint16_t*>(qkv), qkv_tok_stride, part, ks, slice_stride, positions,
+            static_cast<const uint16_t*>(cos), static_cast<const uint16_t*>(sin), table_stride,
+            max_pos, static_cast<uint16_t*>(q_out), q_tok_stride, q_head_stride, k_cache, v_cache,
+            c_blk_stride, c_tok_stride, c_head_stride, static_cast<uint16_t*>(k_scale),
+            static_cast<uint16_t*>(v_scale), s_blk_stride, s_tok_stride, s_head_stride,
+            slot_mapping, T, Hq, Hkv, D, block_size, num_blocks * block_size};
+  const int G = D / 8;
+  const int64_t threads = static_cast<int64_t>(T) * (Hq + Hkv) * G;
+  const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+#define COOPT_QKV(GV)                                                                        \
+  case GV:                                                                                   \
+    if (int8) hipLaunchKernelGGL((qkv_epilogue_kernel<GV, true>), grid, dim3(256), 0, st, a); \
+    else hipLaunchKernelGGL((qkv_epilogue_kernel<GV, false>), grid, dim3(256), 0, st, a);    \
+    break;
+  switch (G) {
+    COOPT_QKV(8)
+    COOPT_QKV(16)
+    COOPT_QKV(32)
+  }
+#undef COOPT_QKV
+  return coopt::check_launch("coopt_qkv_epilogue");
+}
 
 extern "C" int coopt_kv_write(int cache_dtype, const void* k, const void* v, int64_t k_tok_stride,
                               int64_t k_head_stride, int64_t v_tok_stride, int64_t v_head_stride,

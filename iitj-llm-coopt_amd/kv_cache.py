@@ -4,6 +4,7 @@ Drop-in surfaces (reference paths under mohsinmubarak/iitj-llm-coopt):
   quantize(x, bits) / dequantize(q, scale, bits, dtype)   engine/kv_tier_manager.py:21-41
   reshape_and_cache_flash(k, v, k_cache, v_cache, slot_mapping, kv_cache_dtype, k_scale,
                           v_scale)                         engine/model.py:242-243 (vLLM op)
+  qkv_rope_and_cache(qkv, positions, cos, sin, ...)        engine/model.py:238-243 in one launch
 
 Cache layouts.  bf16 ("auto"): k_cache/v_cache [num_blocks, block_size, Hkv, D] bf16, possibly
 a strided per-layer view of a block-major buffer (engine/elastic.py:74-77).  INT8 ("int8"):
@@ -15,7 +16,8 @@ import torch
 
 from . import _lib
 
-__all__ = ["quantize", "dequantize", "reshape_and_cache_flash", "allocate_kv_cache"]
+__all__ = ["quantize", "dequantize", "reshape_and_cache_flash", "allocate_kv_cache",
+           "qkv_rope_and_cache"]
 
 
 def quantize(x: torch.Tensor, bits: int):
@@ -140,3 +142,62 @@ def reshape_and_cache_flash(k, v, k_cache, v_cache, slot_mapping, kv_cache_dtype
                                   _lib.ptr(ks), _lib.ptr(vs), sstr[0], sstr[1], sstr[2],
                                   _lib.ptr(slot_mapping), T, Hkv, D, bs, NB,
                                   _lib.stream_handle(k.device)), "coopt_kv_write")
+
+
+def qkv_rope_and_cache(qkv, positions, cos, sin, k_cache, v_cache, slot_mapping, num_heads,
+                       num_kv_heads, head_dim, kv_cache_dtype="auto", k_scale=None,
+                       v_scale=None, q_out=None):
+    """The chain after the qkv projection (engine/model.py:238-243) in one launch: split q/k/v,
+    neox RoPE on q and k, k and v into the paged cache (as reshape_and_cache_flash), and
+    return q [T, num_heads, head_dim].  `qkv` is the projection's bf16 output [T, (Hq + 2 Hkv)
+    D] or its fused.LinearPartials (split-K partials, reduced here).  Bit for bit the same as
+    rope_ + reshape_and_cache_flash on the reduced output."""
+    from .fused import LinearPartials
+
+    Hq, Hkv, D = int(num_heads), int(num_kv_heads), int(head_dim)
+    width = (Hq + 2 * Hkv) * D
+    part = qkv if isinstance(qkv, LinearPartials) else None
+    if part is not None:
+        if part.n != width:
+            raise ValueError(f"partials are {part.n} wide, expected {width}")
+        T, dev = part.rows, part.device
+        qkv_t = None
+    else:
+        _lib.require_cuda(qkv)
+        if qkv.dtype != torch.bfloat16 or qkv.dim() != 2 or qkv.shape[1] != width or qkv.stride(1) != 1:
+            raise ValueError(f"qkv must be bf16 [T, {width}] with contiguous rows")
+        T, dev, qkv_t = qkv.shape[0], qkv.device, qkv
+    _lib.require_cuda(positions, cos, sin, k_cache, v_cache, slot_mapping)
+    _check_cache_pair(k_cache, v_cache)
+    NB, bs, cH, cD = k_cache.shape
+    if (cH, cD) != (Hkv, D):
+        raise ValueError(f"cache heads/dim {(cH, cD)} != ({Hkv}, {D})")
+    if slot_mapping.dtype != torch.int64 or slot_mapping.numel() != T:
+        raise ValueError("slot_mapping must be int64 with one entry per token")
+    if positions.dtype != torch.int64 or positions.numel() != T:
+        raise ValueError("positions must be int64 with one entry per token")
+    if cos.shape != sin.shape or cos.stride() != sin.stride() or cos.shape[1] < D // 2 or \
+            cos.dtype != torch.bfloat16 or cos.stride(1) != 1:
+        raise ValueError("cos/sin tables must be bf16 [max_pos, >= D/2] alike")
+    if kv_cache_dtype == "auto":
+        code, ks, vs, sstr = _lib.DT_BF16, None, None, (0, 0, 0)
+    elif kv_cache_dtype == "int8":
+        if k_scale is None or v_scale is None or k_scale.stride() != v_scale.stride():
+            raise ValueError("'int8' caches need alike k_scale and v_scale scale caches")
+        code, ks, vs, sstr = _lib.DT_I8, k_scale, v_scale, k_scale.stride()
+    else:
+        raise ValueError(f"kv_cache_dtype must be 'auto' or 'int8', got {kv_cache_dtype!r}")
+    if q_out is None:
+        q_out = torch.empty((T, Hq, D), dtype=torch.bfloat16, device=dev)
+    positions, slot_mapping = positions.contiguous(), slot_mapping.contiguous()
+    cs = k_cache.stride()
+    _lib.check(_lib.load().coopt_qkv_epilogue(
+        code, _lib.ptr(qkv_t), 0 if qkv_t is None else qkv_t.stride(0),
+        None if part is None else _lib.ptr(part.buf), 0 if part is None else part.ks,
+        0 if part is None else part.rows_padded * part.n,
+        _lib.ptr(positions), _lib.ptr(cos), _lib.ptr(sin), cos.stride(0),
+        cos.shape[0], _lib.ptr(q_out), q_out.stride(0), q_out.stride(1), _lib.ptr(k_cache),
+        _lib.ptr(v_cache), cs[0], cs[1], cs[2], _lib.ptr(ks), _lib.ptr(vs), sstr[0], sstr[1],
+        sstr[2], _lib.ptr(slot_mapping), T, Hq, Hkv, D, bs, NB,
+        _lib.stream_handle(dev)), "coopt_qkv_epilogue")
+    return q_out

@@ -28,7 +28,7 @@ import torch.nn.functional as F
 from . import _lib
 from .attention import paged_attention, workspace_bytes
 from .fused import linear, rms_norm, rope_, silu_and_mul
-from .kv_cache import allocate_kv_cache, reshape_and_cache_flash
+from .kv_cache import allocate_kv_cache, qkv_rope_and_cache, reshape_and_cache_flash
 from .spec_decode import AcceptResult, accept
 
 __all__ = ["LlamaShape", "TARGET_LLAMA31_8B", "DRAFT_LLAMA32_1B", "RandomLlama", "PagedKV",
@@ -119,12 +119,10 @@ class RandomLlama:
         d = None
         for li, L in enumerate(self.layers):
             h = ops.rms_norm(x if d is None else d, None if d is None else x, L["ln1"], s.eps)
-            qkv = ops.linear(h, L["qkv"])
-            q = qkv[:, : H * D].view(T, H, D)
-            k = qkv[:, H * D: (H + Hkv) * D].view(T, Hkv, D)
-            v = qkv[:, (H + Hkv) * D:].view(T, Hkv, D)
-            ops.rope(q, k, pos, self.cos, self.sin)
-            ops.write(kv, li, k, v, slots)
+            # qkv projection, RoPE and the KV write: split-K partials straight into one
+            # epilogue launch that writes q and the paged cache (engine/model.py:238-243)
+            qkv = ops.linear(h, L["qkv"], defer_reduce=True)
+            q = ops.qkv_epilogue(kv, li, qkv, pos, self.cos, self.sin, slots, H, Hkv, D)
             attn = ops.attend(kv, li, q, meta, self.scale)
             # o, gate_up and down feed only the fused add + norm or SiLU, which reduce their
             # split-K partials as they read them
@@ -196,6 +194,11 @@ class HipOps:
 
     def rope(self, q, k, pos, cos, sin):
         rope_(q, k, pos, cos, sin)
+
+    def qkv_epilogue(self, kv: "PagedKV", layer, qkv, pos, cos, sin, slots, H, Hkv, D):
+        kc, vc, ks, vs = kv.layers[layer]
+        return qkv_rope_and_cache(qkv, pos, cos, sin, kc, vc, slots, H, Hkv, D, kv.kv_dtype,
+                                  ks, vs)
 
     def silu_mul(self, gate_up):
         return silu_and_mul(gate_up)

@@ -26,6 +26,8 @@
  *   coopt_dequantize        dequantize
  *   coopt_kv_swap_out /     quantize(cache[blocks], bits) / engine/kv_tier_manager.py:93-101
  *   coopt_kv_swap_in        cache[blocks] = dequantize(..)  engine/kv_tier_manager.py:113-119
+ *   coopt_qkv_epilogue      split + rotary_embedding +      engine/model.py:238-243
+ *                           reshape_and_cache_flash
  *   coopt_kv_copy_blocks    buf[dst].copy_(buf[src]) per    engine/elastic.py:131 via
  *                           migrated block                  engine/block_manager.py:165-187
  *   coopt_softmax           torch.softmax(logits / T)       engine/spec_decode.py:16
@@ -91,6 +93,31 @@ int coopt_kv_write(int cache_dtype,
                    int64_t s_blk_stride, int64_t s_tok_stride, int64_t s_head_stride,
                    const int64_t* slot_mapping, int T, int Hkv, int D, int block_size,
                    int64_t num_blocks, coopt_stream_t stream);
+
+/*
+ * The step after the qkv projection in one launch: split q/k/v, neox RoPE on q and k, q to
+ * q_out, k and v into the paged cache -- the chain  q, k, v = F.linear(h, qkv).split(...);
+ * rotary_embedding(positions, q, k, ...); reshape_and_cache_flash(k, v, ...)  at
+ * engine/model.py:238-243.
+ *   input: either qkv [T, (Hq + 2 Hkv) D] bf16 (row stride qkv_tok_stride, part NULL), or
+ *          part: the projection's fp32 split-K partials (coopt_linear_partials: ks slices of
+ *          slice_stride floats, rows (Hq + 2 Hkv) D wide), reduced in coopt_linear's order
+ *          and rounded to bf16 first (qkv NULL).
+ *   RoPE: as coopt_rope (cos/sin bf16 [max_pos, table_stride], positions clamped).
+ *   q_out [T, Hq, D] bf16 (strides q_tok_stride, q_head_stride); the cache arguments are
+ *   those of coopt_kv_write, including slot < 0 for rows that write no entry.
+ *   D in {64, 128, 256}.  Results equal coopt_linear + coopt_rope + coopt_kv_write bit for bit.
+ */
+int coopt_qkv_epilogue(int cache_dtype, const void* qkv, int64_t qkv_tok_stride,
+                       const float* part, int ks, int64_t slice_stride,
+                       const int64_t* positions, const void* cos, const void* sin,
+                       int64_t table_stride, int max_pos, void* q_out, int64_t q_tok_stride,
+                       int64_t q_head_stride, void* k_cache, void* v_cache,
+                       int64_t c_blk_stride, int64_t c_tok_stride, int64_t c_head_stride,
+                       void* k_scale, void* v_scale, int64_t s_blk_stride,
+                       int64_t s_tok_stride, int64_t s_head_stride,
+                       const int64_t* slot_mapping, int T, int Hq, int Hkv, int D,
+                       int block_size, int64_t num_blocks, coopt_stream_t stream);
 
 /*
  * Symmetric absmax codec over contiguous rows, kv_tier_manager.quantize / dequantize

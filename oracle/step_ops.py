@@ -37,6 +37,16 @@ class OracleOps:
         gate, up = gate_up.chunk(2, dim=-1)
         return torch.nn.functional.silu(gate) * up
 
+    def qkv_epilogue(self, kv, layer, qkv, pos, cos, sin, slots, H, Hkv, D):
+        # engine/model.py:238-243: split, RoPE on q and k, K/V into the paged cache
+        T = qkv.shape[0]
+        q = qkv[:, : H * D].view(T, H, D)
+        k = qkv[:, H * D: (H + Hkv) * D].view(T, Hkv, D)
+        v = qkv[:, (H + Hkv) * D:].view(T, Hkv, D)
+        self.rope(q, k, pos, cos, sin)
+        self.write(kv, layer, k, v, slots)
+        return q
+
     def linear(self, x, w, out=None, defer_reduce=False):
         # the projections, F.linear without bias (engine/model.py:238, 248, 250, 253)
         if out is not None:
