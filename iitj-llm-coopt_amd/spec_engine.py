@@ -324,7 +324,7 @@ class SpecDecoder:
         return F.linear(h, model.lm_head)
 
     # ---- one speculative step -------------------------------------------------------------
-    def _rows(self, model, kv, start, S, tokens, real):
+    def _rows(self, model, kv, start, S, tokens, real, logits_out=None):
         """Forward S rows per sequence at positions start..start+S-1; rows with real=False are
         padding (KV write skipped, seq_len = start + S as in the padded graph layout)."""
         B = self.B
@@ -334,7 +334,8 @@ class SpecDecoder:
             slots = torch.where(real.reshape(-1), slots, torch.full_like(slots, -1))
         seq_lens = (start + S).to(torch.int32)
         meta = (self.cu[S], seq_lens, S, self.max_len)
-        return model.forward(self.ops, kv, tokens.reshape(-1), pos.reshape(-1), slots, meta)
+        return model.forward(self.ops, kv, tokens.reshape(-1), pos.reshape(-1), slots, meta,
+                             logits_out=logits_out)
 
     @torch.inference_mode()
     def step(self):
@@ -354,13 +355,12 @@ class SpecDecoder:
         self.draft_tok[:, 0] = tok
         for i in range(1, g):
             start = n - 1 + i
-            logits = self._rows(self.d, self.dkv, start, 1, self.draft_tok[:, i - 1].long(), None)
-            self.draft_logits[:, i] = logits
+            self._rows(self.d, self.dkv, start, 1, self.draft_tok[:, i - 1].long(), None,
+                       logits_out=self.draft_logits[:, i])
             self.draft_tok[:, i] = self.ops.sample(self.draft_logits[:, i], u_draft[i], T)
         # target verify over [last token] + drafts
         vt = torch.cat([torch.gather(self.hist, 1, (n - 1).unsqueeze(1)), self.draft_tok.long()], 1)
-        tl = self._rows(self.t, self.tkv, n - 1, g + 1, vt, None)
-        self.target_logits.copy_(tl)
+        self._rows(self.t, self.tkv, n - 1, g + 1, vt, None, logits_out=self.target_logits)
         res = self.ops.accept(self.target_logits.view(B, g + 1, -1), self.draft_logits,
                               self.draft_tok, T, u_acc, u_res, out=self.res)
         acc = res.accepted_len.long()
