@@ -278,6 +278,24 @@ def migrate_case(torch, M, dev, seed, pairs=256):
     return res
 
 
+def linear_case(torch, M, dev, rows, n, k, seed):
+    """One projection of the step through fused.linear (coopt_linear: split-K partials plus
+    the reduction launch at these shapes): x [rows, k] @ w[n, k]^T, bf16, N(0,1) x, N(0, 0.02^2)
+    weights.  Algorithmic bytes: the weight, x and y once each."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    x = torch.randn(rows, k, generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    y = torch.empty(rows, n, dtype=torch.bfloat16, device=dev)
+
+    def fn():
+        M.fused.linear(x, w, out=y)
+
+    res = rate({"rows": rows, "n": n, "k": k, "flops": 2 * rows * n * k},
+               n * k * 2 + rows * k * 2 + rows * n * 2, *time_launches(torch, dev, fn))
+    res["TFLOP_s"] = 2 * rows * n * k / (res["avg_us"] * 1e-6) / 1e12
+    return res
+
+
 def copy_case(torch, M, dev, seed):
     """A plain streaming kernel of known size (torch.neg over 1 GiB of bf16: 1 GiB read,
     1 GiB written): the calibration for FETCH_SIZE / WRITE_SIZE and a practical HBM ceiling."""
@@ -317,6 +335,11 @@ KERNEL_CASES = {
     "kv_swap_out_4096tok": lambda t, M, d, s: kv_swap_case(t, M, d, s),
     "kv_tier_roundtrip": lambda t, M, d, s: kv_tier_case(t, M, d, s),
     "kv_migrate_256x2MiB": lambda t, M, d, s: migrate_case(t, M, d, s),
+    # the step's weight-streaming projections: target qkv / down at the verify rows
+    # (B (gamma+1) = 160), draft lm_head at the draft rows (B = 32)
+    "linear_m160_qkv": lambda t, M, d, s: linear_case(t, M, d, 160, 6144, 4096, s),
+    "linear_m160_down": lambda t, M, d, s: linear_case(t, M, d, 160, 4096, 14336, s),
+    "linear_m32_lm_head": lambda t, M, d, s: linear_case(t, M, d, 32, 128256, 2048, s),
     "copy": lambda t, M, d, s: copy_case(t, M, d, s),
 }
 
@@ -407,6 +430,17 @@ def summarize(paths):
         print("|---|---|---|---|")
         for k, (c, t) in sorted(fam.items(), key=lambda kv: -kv[1][1]):
             print(f"| `{k}` | {c} | {t:.0f} | {t / busy * 100:.1f}% |")
+        shapes = {}
+        for r in win:
+            key = (_short(r["Kernel_Name"]), f"{r['Grid_Size_X']}x{r['Grid_Size_Y']}x{r['Grid_Size_Z']}")
+            d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            shapes.setdefault(key, []).append(d)
+        print("\nsame window by launch shape (top 30 by total time):")
+        print("| kernel | grid (threads) | launches | avg us | total us | share |")
+        print("|---|---|---|---|---|---|")
+        for (k, g), ds in sorted(shapes.items(), key=lambda kv: -sum(kv[1]))[:30]:
+            print(f"| `{k}` | {g} | {len(ds)} | {sum(ds) / len(ds):.1f} | {sum(ds):.0f} | "
+                  f"{sum(ds) / busy * 100:.1f}% |")
         print()
     trace = {}
     for r in trace_rows:
@@ -428,7 +462,7 @@ def summarize(paths):
     if not agg:
         return
     mean = {k: tot / n for k, (n, tot) in agg.items()}
-    print("\n| kernel | grid (threads) | counter | dispatches | mean per dispatch (KiB) |")
+    print("\n| kernel | grid (threads) | counter | dispatches | mean per dispatch (FETCH_SIZE / WRITE_SIZE in KiB) |")
     print("|---|---|---|---|---|")
     for (k, grid, c), (n, tot) in sorted(agg.items()):
         print(f"| `{k}` | {grid} | {c} | {n} | {tot / n:.1f} |")
@@ -439,6 +473,29 @@ def summarize(paths):
             scale[c] = known / (v * 1024)
     for c, f in sorted(scale.items()):
         print(f"\ncalibration {c}: x{f:.4f} (copy kernel moving 1 GiB each way)")
+    sized = sorted({(k, g) for (k, g, c) in agg if c in scale})
+    if sized:
+        print("\n| kernel | grid (threads) | calibrated read MB / dispatch | calibrated write MB / dispatch |")
+        print("|---|---|---|---|")
+        for k, g in sized:
+            cols = []
+            for c in ("FETCH_SIZE", "WRITE_SIZE"):
+                v = mean.get((k, g, c))
+                cols.append("-" if v is None or c not in scale else f"{v * 1024 * scale[c] / 1e6:.2f}")
+            print(f"| `{k}` | {g} | {cols[0]} | {cols[1]} |")
+    mops = [key for key in agg if key[2].startswith("SQ_INSTS_VALU_MFMA_MOPS_")]
+    if mops:
+        # MOPS counters count MFMA multiply/add operations / 512, summed over the chip
+        print("\n| kernel | grid (threads) | counter | MFMA GFLOP / dispatch |")
+        print("|---|---|---|---|")
+        for k, g, c in sorted(mops):
+            print(f"| `{k}` | {g} | {c} | {mean[(k, g, c)] * 512 / 1e9:.3f} |")
+    util = sorted(key for key in agg if key[2] == "MfmaUtil")
+    if util:
+        print("\n| kernel | grid (threads) | MfmaUtil % (MFMA busy cycles / (GPU active cycles x SIMDs)) |")
+        print("|---|---|---|")
+        for k, g, c in util:
+            print(f"| `{k}` | {g} | {mean[(k, g, c)]:.2f} |")
     if set(scale) == {"FETCH_SIZE", "WRITE_SIZE"}:
         # calls = dispatches of the main kernel; merge dispatches (if any) add to the same calls
         main = [(k, g) for (k, g, c) in agg if k.startswith(ROOFLINE_KERNELS[0]) and c == "FETCH_SIZE"]
