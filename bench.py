@@ -92,14 +92,14 @@ def rate(res, nbytes, avg, med):
     return res
 
 
-def attention_case(torch, M, dev, ctx, qlen, kv_dtype, seed):
+def attention_case(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128):
     """Verify attention over len(ctx) sequences with ctx[b] cached tokens and q_len new rows
-    each (seq_len = ctx + q_len), Hq 32 / Hkv 8, D 128, block size 16, block tables a seeded
-    permutation of a shared pool.  K/V are N(0,1) with 1% x20 outliers, quantised on write for
-    INT8."""
+    each (seq_len = ctx + q_len), Hq 32 / Hkv 8, head size D (128: the target; 64: the draft),
+    block size 16, block tables a seeded permutation of a shared pool.  K/V are N(0,1) with 1%
+    x20 outliers, quantised on write for INT8."""
     import numpy as np
 
-    Hq, Hkv, D, bs = 32, 8, 128, 16
+    Hq, Hkv, bs = 32, 8, 16
     ctx = np.asarray(ctx, np.int64)
     B = len(ctx)
     seq = ctx + qlen
@@ -135,7 +135,7 @@ def attention_case(torch, M, dev, ctx, qlen, kv_dtype, seed):
     def fn():
         M.paged_attention(q, kc, vc, cu, sl, table, qlen, max_k, D ** -0.5, ks, vs, out, ws)
 
-    res = {"kv": kv_dtype, "batch": B, "q_len": qlen, "ctx_min": int(ctx.min()),
+    res = {"kv": kv_dtype, "head_dim": D, "batch": B, "q_len": qlen, "ctx_min": int(ctx.min()),
            "ctx_max": int(ctx.max()), "ctx_mean": float(ctx.mean())}
     return rate(res, nbytes, *time_launches(torch, dev, fn))
 
@@ -326,6 +326,11 @@ KERNEL_CASES = {
     "attention_config4_g2": lambda t, M, d, s: attention_case(t, M, d, config_ctx(s, 64, 4096, 16384), 3, "int8", s),
     "attention_config4_g4": lambda t, M, d, s: attention_case(t, M, d, config_ctx(s, 64, 4096, 16384), 5, "int8", s),
     "attention_config4_g8": lambda t, M, d, s: attention_case(t, M, d, config_ctx(s, 64, 4096, 16384), 9, "int8", s),
+    # the bench step's own attention launches (prompt 1024 + the tokens of the timed steps):
+    # target verify (INT8, q_len 5), draft proposals (bf16, D 64, 1 row) and catch-up (2 rows)
+    "attention_step_target": lambda t, M, d, s: attention_case(t, M, d, [1100] * 32, 5, "int8", s),
+    "attention_step_draft": lambda t, M, d, s: attention_case(t, M, d, [1100] * 32, 1, "auto", s, D=64),
+    "attention_step_draft_q2": lambda t, M, d, s: attention_case(t, M, d, [1100] * 32, 2, "auto", s, D=64),
     # config 1 (B=8) and the metric's B=32
     "accept_b8": lambda t, M, d, s: accept_case(t, M, d, 8, 4, 128256, s),
     "accept_b32": lambda t, M, d, s: accept_case(t, M, d, 32, 4, 128256, s),
