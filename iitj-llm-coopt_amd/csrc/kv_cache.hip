@@ -19,11 +19,45 @@ __device__ __forceinline__ float quant_scale(float amax) {
   return fmaxf(amax, kClampMin) * (1.0f / static_cast<float>(QMAX));
 }
 
+// code = rint(fl(x / s32)) clamped to [-QMAX, QMAX], fl the IEEE fp32 quotient, computed as
+// rint(x * r32) with r32 = v_rcp_f32(s32) (1 ulp).  Because s32 >= amax / 127 up to rounding,
+// |x / s32| < 128, where an ulp is at most 2^-17: the reciprocal's relative error (2^-23)
+// and the product's rounding leave x * r32 within 2.5 ulp of x / s32, hence within 3 ulp
+// (< 2^-14) of fl(x / s32), so both round to the same integer unless x * r32 lies within
+// kNearTie of a half-integer.  There the IEEE division decides.
+// The result is the IEEE path's for every input (ties included), at a fraction of its work.
+constexpr float kNearTie = 0x1p-14f;
+
 template <int QMAX>
-__device__ __forceinline__ int quant_code(float x, float s32) {
-  float r = rintf(x / s32);
+__device__ __forceinline__ int quant_code(float x, float s32, float r32) {
+  const float q = x * r32;
+  float r = rintf(q);
+  if (fabsf(q - r) >= 0.5f - kNearTie) r = rintf(x / s32);
   r = fminf(fmaxf(r, -static_cast<float>(QMAX)), static_cast<float>(QMAX));
   return static_cast<int>(r);
+}
+
+// quant_code of the 8 bf16 elements in w[0..3] (element 2i in the low half of w[i]), with one
+// branch for the lane: if any element is near a boundary, all 8 take the IEEE division.
+template <int QMAX>
+__device__ __forceinline__ void quant_codes8(const uint32_t (&w)[4], float s32, int (&code)[8]) {
+  const float r32 = __builtin_amdgcn_rcpf(s32);
+  float x[8], r[8];
+  bool near = false;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    x[e] = bf16_to_f32(static_cast<uint16_t>(w[e / 2] >> (16 * (e & 1))));
+    const float q = x[e] * r32;
+    r[e] = rintf(q);
+    near |= fabsf(q - r[e]) >= 0.5f - kNearTie;
+  }
+  if (near) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = rintf(x[e] / s32);
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    code[e] = static_cast<int>(fminf(fmaxf(r[e], -static_cast<float>(QMAX)), static_cast<float>(QMAX)));
 }
 
 // ---------------------------------------------------------------------------------------
@@ -57,15 +91,14 @@ __device__ __forceinline__ void store_kv_chunk(uint4 kr, uint4 vr, void* kc, voi
     vmax = group_max_u32<G>(vmax);
     const float ksc = quant_scale<127>(bf16_to_f32(static_cast<uint16_t>(kmax)));
     const float vsc = quant_scale<127>(bf16_to_f32(static_cast<uint16_t>(vmax)));
+    int kcode[8], vcode[8];
+    quant_codes8<127>(kw, ksc, kcode);
+    quant_codes8<127>(vw, vsc, vcode);
     uint32_t kq[2] = {0, 0}, vq[2] = {0, 0};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const uint16_t kb = static_cast<uint16_t>(kw[i / 2] >> (16 * (i & 1)));
-      const uint16_t vb = static_cast<uint16_t>(vw[i / 2] >> (16 * (i & 1)));
-      const uint32_t kc8 = static_cast<uint32_t>(quant_code<127>(bf16_to_f32(kb), ksc)) & 0xffu;
-      const uint32_t vc8 = static_cast<uint32_t>(quant_code<127>(bf16_to_f32(vb), vsc)) & 0xffu;
-      kq[i / 4] |= kc8 << (8 * (i & 3));
-      vq[i / 4] |= vc8 << (8 * (i & 3));
+      kq[i / 4] |= (static_cast<uint32_t>(kcode[i]) & 0xffu) << (8 * (i & 3));
+      vq[i / 4] |= (static_cast<uint32_t>(vcode[i]) & 0xffu) << (8 * (i & 3));
     }
     *reinterpret_cast<uint2*>(static_cast<int8_t*>(kc) + c_off) = make_uint2(kq[0], kq[1]);
     *reinterpret_cast<uint2*>(static_cast<int8_t*>(vc) + c_off) = make_uint2(vq[0], vq[1]);
@@ -81,18 +114,19 @@ __global__ __launch_bounds__(256) void kv_write_kernel(
     const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t k_ts, int64_t k_hs,
     int64_t v_ts, int64_t v_hs, void* __restrict__ kc, void* __restrict__ vc, int64_t c_bs, int64_t c_ts, int64_t c_hs,
     uint16_t* __restrict__ ks, uint16_t* __restrict__ vs, int64_t s_bs, int64_t s_ts, int64_t s_hs,
-    const int64_t* __restrict__ slot_mapping, int T, int Hkv, int block_size, int64_t num_slots) {
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int c = static_cast<int>(gid % G);
-  const int64_t vec = gid / G;
+    const int64_t* __restrict__ slot_mapping, int T, int bs_shift, int block_size, int64_t num_slots) {
+  // grid: x covers T tokens x G lanes (32-bit, checked by the host), y the KV head
+  const int lid = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+  const int c = lid & (G - 1);
+  const int t = lid / G;
   // Groups are aligned inside the wave, so a whole group leaves together.
-  if (vec >= static_cast<int64_t>(T) * Hkv) return;
-  const int t = static_cast<int>(vec / Hkv);
-  const int h = static_cast<int>(vec % Hkv);
+  if (t >= T) return;
+  const int h = blockIdx.y;
   const int64_t slot = slot_mapping[t];
   if (slot < 0 || slot >= num_slots) return;
-  const int64_t blk = slot / block_size;
-  const int64_t off = slot % block_size;
+  // power-of-two block sizes (bs_shift >= 0) take a shift and a mask
+  const int64_t blk = bs_shift >= 0 ? slot >> bs_shift : slot / block_size;
+  const int64_t off = bs_shift >= 0 ? slot & ((int64_t{1} << bs_shift) - 1) : slot % block_size;
 
   const uint4 kr = *reinterpret_cast<const uint4*>(k + t * k_ts + h * k_hs + c * 8);
   const uint4 vr = *reinterpret_cast<const uint4*>(v + t * v_ts + h * v_hs + c * 8);
@@ -133,6 +167,7 @@ struct QkvArgs {
   const int64_t* slot_mapping;
   int T, Hq, Hkv, D, block_size;
   int64_t num_slots;
+  int bs_shift;  // log2(block_size) when it is a power of two, else -1
 };
 
 __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
@@ -152,12 +187,12 @@ __device__ __forceinline__ uint4 qkv_chunk(const QkvArgs& a, int t, int64_t col)
 
 template <int G, bool INT8>
 __global__ __launch_bounds__(256) void qkv_epilogue_kernel(QkvArgs a) {
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int c = static_cast<int>(gid % G);
-  const int64_t vec = gid / G;
-  const int heads = a.Hq + a.Hkv;
-  if (vec >= static_cast<int64_t>(a.T) * heads) return;  // whole groups leave together
-  const int t = static_cast<int>(vec / heads), h = static_cast<int>(vec % heads);
+  // grid: x covers T tokens x G lanes (32-bit, checked by the host), y the q / k head
+  const int lid = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+  const int c = lid & (G - 1);
+  const int t = lid / G;
+  if (t >= a.T) return;  // whole groups leave together
+  const int h = blockIdx.y;
   const int D = G * 8;
   const uint4 xr = qkv_chunk(a, t, static_cast<int64_t>(h) * D + c * 8);
   // partner words (elements i +- D/2) from lane c ^ (G/2)
@@ -196,7 +231,8 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(QkvArgs a) {
   const int64_t slot = a.slot_mapping[t];
   if (slot < 0 || slot >= a.num_slots) return;  // padding row: the group leaves together
   const uint4 vr = qkv_chunk(a, t, static_cast<int64_t>(a.Hq + a.Hkv + hk) * D + c * 8);
-  const int64_t blk = slot / a.block_size, off = slot % a.block_size;
+  const int64_t blk = a.bs_shift >= 0 ? slot >> a.bs_shift : slot / a.block_size;
+  const int64_t off = a.bs_shift >= 0 ? slot & ((int64_t{1} << a.bs_shift) - 1) : slot % a.block_size;
   store_kv_chunk<G, INT8>(yr, vr, a.kc, a.vc, blk * a.c_bs + off * a.c_ts + hk * a.c_hs + c * 8,
                           a.k_scale, a.v_scale, blk * a.s_bs + off * a.s_ts + hk * a.s_hs, c);
 }
@@ -206,13 +242,15 @@ int launch_kv_write(int G, const uint16_t* k, const uint16_t* v, int64_t k_ts, i
                     int64_t v_ts, int64_t v_hs, void* kc, void* vc, int64_t c_bs, int64_t c_ts, int64_t c_hs, uint16_t* ks,
                     uint16_t* vs, int64_t s_bs, int64_t s_ts, int64_t s_hs, const int64_t* slot,
                     int T, int Hkv, int block_size, int64_t num_slots, hipStream_t stream) {
-  const int64_t threads = static_cast<int64_t>(T) * Hkv * G;
-  const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+  const int64_t lanes = static_cast<int64_t>(T) * G;
+  COOPT_REQUIRE(lanes <= 0x7fffff00LL && Hkv <= 65535, "T * D / 8 must stay below 2^31, Hkv <= 65535");
+  const dim3 grid(static_cast<unsigned>((lanes + 255) / 256), static_cast<unsigned>(Hkv));
+  const int bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
 #define COOPT_KVW(GV)                                                                         \
   case GV:                                                                                    \
     hipLaunchKernelGGL((kv_write_kernel<GV, INT8>), grid, dim3(256), 0, stream, k, v, k_ts, k_hs, \
-                       v_ts, v_hs, kc, vc, c_bs, c_ts, c_hs, ks, vs, s_bs, s_ts, s_hs, slot, T, Hkv, \
-                       block_size, num_slots);                                                \
+                       v_ts, v_hs, kc, vc, c_bs, c_ts, c_hs, ks, vs, s_bs, s_ts, s_hs, slot, T, \
+                       bs_shift, block_size, num_slots);                                      \
     break;
   switch (G) {
     COOPT_KVW(1)
@@ -259,9 +297,10 @@ __global__ __launch_bounds__(256) void quantize_kernel(const T* __restrict__ x, 
   }
   amax = wave_max_f32(amax);
   const float s32 = quant_scale<QMAX>(amax);
+  const float r32 = __builtin_amdgcn_rcpf(s32);
   for (int i = 2 * lane; i < D; i += 128) {
-    const int c0 = quant_code<QMAX>(load_elem(xr + i), s32);
-    const int c1 = quant_code<QMAX>(load_elem(xr + i + 1), s32);
+    const int c0 = quant_code<QMAX>(load_elem(xr + i), s32, r32);
+    const int c1 = quant_code<QMAX>(load_elem(xr + i + 1), s32, r32);
     if constexpr (BITS == 8) {
       const uint16_t pair = static_cast<uint16_t>((c0 & 0xff) | ((c1 & 0xff) << 8));
       *reinterpret_cast<uint16_t*>(q + row * D + i) = pair;
@@ -363,9 +402,7 @@ __global__ __launch_bounds__(256) void swap_out_kernel(
       amax = group_max_u32<G>(amax);
       const float s32 = quant_scale<QMAX>(bf16_to_f32(static_cast<uint16_t>(amax)));
       int code[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        code[e] = quant_code<QMAX>(bf16_to_f32(static_cast<uint16_t>(w[e / 2] >> (16 * (e & 1)))), s32);
+      quant_codes8<QMAX>(w, s32, code);
       if constexpr (BITS == 8) {
         uint32_t b[2] = {0, 0};
 #pragma unroll
@@ -567,10 +604,12 @@ extern "C" int coopt_qkv_epilogue(int cache_dtype, const void* qkv, int64_t qkv_
             max_pos, static_cast<uint16_t*>(q_out), q_tok_stride, q_head_stride, k_cache, v_cache,
             c_blk_stride, c_tok_stride, c_head_stride, static_cast<uint16_t*>(k_scale),
             static_cast<uint16_t*>(v_scale), s_blk_stride, s_tok_stride, s_head_stride,
-            slot_mapping, T, Hq, Hkv, D, block_size, num_blocks * block_size};
+            slot_mapping, T, Hq, Hkv, D, block_size, num_blocks * block_size,
+            (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1};
   const int G = D / 8;
-  const int64_t threads = static_cast<int64_t>(T) * (Hq + Hkv) * G;
-  const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+  const int64_t lanes = static_cast<int64_t>(T) * G;
+  COOPT_REQUIRE(lanes <= 0x7fffff00LL && Hq + Hkv <= 65535, "T * D / 8 must stay below 2^31");
+  const dim3 grid(static_cast<unsigned>((lanes + 255) / 256), static_cast<unsigned>(Hq + Hkv));
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
 #define COOPT_QKV(GV)                                                                        \
   case GV:                                                                                   \

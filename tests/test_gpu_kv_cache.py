@@ -140,6 +140,48 @@ def test_kv_write_int8_edge_vectors(dev):
     assert codes[3, 0] == -127 and codes[3, -1] == 127
 
 
+def near_tie_vectors(rows, D, qmax, seed):
+    """bf16 vectors whose quotients x / scale lie within 2^-12 of a half-integer (or on one):
+    element 0 of each row is its amax, the rest are bf16 values picked by exact fp32 division
+    (numpy), so the rounding of the quotient decides the code."""
+    rng = np.random.default_rng(seed)
+    bf = np.arange(0x3c00, 0x4400, dtype=np.uint32)         # bf16 bit patterns in [2^-7, 2^9)
+    vals = (bf << 16).view(np.float32)
+    out = np.zeros((rows, D), np.float32)
+    for r in range(rows):
+        amax = vals[rng.integers(len(vals) // 2, len(vals))]
+        s = np.float32(max(amax, np.float32(1e-8))) * np.float32(1.0 / qmax)
+        q = (vals / s).astype(np.float32)
+        frac = np.abs(q - np.floor(q) - np.float32(0.5))
+        cand = vals[(frac <= 2.0 ** -12) & (vals <= amax)]
+        pick = rng.choice(cand, D - 1) if len(cand) else np.zeros(D - 1, np.float32)
+        sign = np.where(rng.random(D - 1) < 0.5, -1.0, 1.0).astype(np.float32)
+        out[r, 0], out[r, 1:] = amax, pick * sign
+    return torch.from_numpy(out).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_quantise_near_ties_bit_exact(dev, bits):
+    """Quotients on or next to a rounding boundary: the kernels' reciprocal-based quotient
+    must give the IEEE division's codes (torch on this GPU, and the oracle) there too."""
+    qmax = 127 if bits == 8 else 7
+    x = near_tie_vectors(512, 128, qmax, seed=bits).to(dev)
+    q, sc = M.quantize(x, bits)
+    rq, rs = reference_quantize_on_device(x, bits)
+    assert torch.equal(q, rq) and torch.equal(sc, rs)
+    oq, osc = OC.quantize(x.float().cpu().numpy(), bits)
+    assert np.array_equal(q.cpu().numpy(), oq)
+    if bits == 8:   # the fused KV write (and its qkv-epilogue twin) share the code path
+        kx = x.view(64, 8, 128)
+        kc, vc, ks, vs = M.allocate_kv_cache(8, 16, 8, 128, "int8", device=dev)
+        slots = torch.randperm(128, device=dev)[:64]
+        M.reshape_and_cache_flash(kx, kx, kc, vc, slots, "int8", ks, vs)
+        blk, off = slots // 16, slots % 16
+        assert torch.equal(kc[blk, off], rq.view(64, 8, 128)) and torch.equal(vc[blk, off], rq.view(64, 8, 128))
+        assert torch.equal(ks[blk, off], rs.view(64, 8))
+    report(f"[near-ties bits={bits}] 512 x 128 near-boundary quotients bit-exact")
+
+
 @pytest.mark.parametrize("bits", [8, 4])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_codec_round_trip_bit_exact(dev, bits, dtype):
