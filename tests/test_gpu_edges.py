@@ -1,0 +1,93 @@
+"""GPU edge cases of the hot path: empty inputs, sequences without rows or without context,
+single-key sequences, one-sequence batches.  Same bars as the per-op tests: bit-exact for
+codes, copies and tokens; attention within the bf16 / INT8 tolerances of the float64 oracle
+(0 for rows whose visible range is empty, as oracle.paged.attention defines)."""
+import numpy as np
+import pytest
+import torch
+
+import iitj_llm_coopt_amd as M
+from oracle import accept as OA
+from test_gpu_attention import TOL_BF16, TOL_INT8, Pool
+
+pytestmark = pytest.mark.gpu
+
+
+def report(msg):
+    print(msg, flush=True)
+
+
+@pytest.mark.parametrize("kv", ["auto", "int8"])
+def test_kv_write_with_no_tokens_is_a_no_op(dev, kv):
+    kc, vc, ks, vs = M.allocate_kv_cache(4, 16, 8, 128, kv, device=dev)
+    empty = torch.empty(0, 8, 128, dtype=torch.bfloat16, device=dev)
+    M.reshape_and_cache_flash(empty, empty, kc, vc, torch.empty(0, dtype=torch.int64, device=dev),
+                              kv, ks, vs)
+    torch.cuda.synchronize()
+    assert int((kc != 0).sum()) == 0 and int((vc != 0).sum()) == 0
+
+
+@pytest.mark.parametrize("kv,D", [("auto", 128), ("int8", 128), ("auto", 64), ("int8", 64)])
+def test_attention_rowless_contextless_and_single_key_sequences(dev, kv, D):
+    """q_lens [2, 0, 3, 1, 5]; contexts [0, 40, 0, 0, 200]: a sequence made only of its
+    candidates (causal among them), one with cached keys but no query rows (no output rows),
+    a single-key sequence, and an ordinary one."""
+    pool = Pool([0, 40, 0, 0, 200], [2, 0, 3, 1, 5], 32, 8, D, dev, kv, seed=11)
+    out = pool.run()
+    assert out.shape == (11, 32, D) and bool(torch.isfinite(out.float()).all())
+    err, mabs = pool.max_err(out, seqs=[0, 2, 3, 4])   # sequence 1 has no rows to check
+    report(f"[edges {kv} D={D}] error {err:.3g} (max-abs {mabs:.3g})")
+    assert err <= (TOL_INT8 if kv == "int8" else TOL_BF16)
+
+
+def test_attention_with_no_query_rows_at_all(dev):
+    """Every sequence has q_len 0: the call succeeds and writes nothing."""
+    kc, vc, _, _ = M.allocate_kv_cache(8, 16, 8, 128, "auto", device=dev)
+    q = torch.empty(0, 32, 128, dtype=torch.bfloat16, device=dev)
+    cu = torch.zeros(3, dtype=torch.int32, device=dev)
+    sl = torch.tensor([5, 20], dtype=torch.int32, device=dev)
+    table = torch.arange(4, dtype=torch.int32, device=dev).view(2, 2)
+    out = M.flash_attn_varlen_func(q=q, k=kc, v=vc, cu_seqlens_q=cu, max_seqlen_q=1,
+                                   seqused_k=sl, max_seqlen_k=20, softmax_scale=128 ** -0.5,
+                                   causal=True, block_table=table)
+    torch.cuda.synchronize()
+    assert out.shape == (0, 32, 128)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_quantize_zero_rows(dev, bits):
+    x = torch.empty(0, 128, dtype=torch.bfloat16, device=dev)
+    q, s = M.quantize(x, bits)
+    assert q.shape[0] == 0 and s.shape == (0,)
+
+
+def test_copy_blocks_with_no_pairs_and_swap_of_no_blocks(dev):
+    buf, _, _ = M.allocate_block_major_kv(8, 2, 16, 8, 128, device=dev)
+    buf.view(torch.int16).random_(generator=torch.Generator(device=dev).manual_seed(1))
+    before = buf.clone()
+    M.copy_blocks(buf, [], [])
+    torch.cuda.synchronize()
+    assert torch.equal(buf.view(torch.int16), before.view(torch.int16))   # raw bits (NaN patterns)
+    kc, _, _, _ = M.allocate_kv_cache(8, 16, 8, 128, "auto", device=dev)
+    q, s = M.swap_out_blocks(kc, torch.empty(0, dtype=torch.int64, device=dev), 8)
+    assert q.shape[0] == 0 and s.shape[0] == 0
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2, 3])
+def test_accept_one_sequence_one_draft_token(dev, seed):
+    """B = 1, gamma = 1 at the full vocabulary, against the oracle (ties reported)."""
+    gen = torch.Generator(device=dev).manual_seed(40 + seed)
+    V = 128256
+    tl = torch.randn(1, 2, V, generator=gen, device=dev) * 2
+    dl = (tl[:, :1] + torch.randn(1, 1, V, generator=gen, device=dev) * 0.5).contiguous()
+    dt = torch.randint(0, V, (1, 1), generator=gen, device=dev)
+    if seed % 2:
+        dt[0, 0] = int(tl[0, 0].argmax())
+    ua = torch.rand(1, 1, generator=gen, device=dev)
+    ur = torch.rand(1, generator=gen, device=dev)
+    res = M.accept(tl, dl, dt, 1.0, ua, ur)
+    acc, toks, marg = OA.accept_batch(tl.cpu().numpy(), dl.cpu().numpy(), dt.cpu().numpy(), 1.0,
+                                      ua.cpu().numpy(), ur.cpu().numpy())
+    same = int(res.accepted_len[0]) == int(acc[0]) and np.array_equal(res.tokens[0].cpu().numpy(), toks[0])
+    report(f"[accept B=1 g=1 seed={seed}] accepted {int(res.accepted_len[0])}, margin {marg[0]:.3g}")
+    assert same or marg[0] < 1e-6
