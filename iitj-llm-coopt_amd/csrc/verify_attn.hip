@@ -1,12 +1,13 @@
 // Paged GQA verification attention for gfx950 (replaces flash_attn_varlen_func at
 // engine/model.py:244-247 for the speculative-verify shapes: a few query rows per sequence).
 //
-// Work decomposition.  Grid (context split, KV head, sequence); 256 threads = 4 waves.  All
-// G = Hq/Hkv query heads of a KV head and all n query rows of the sequence are packed into
-// R = G*n "rows" (row r = head_local * n + j), so each K/V byte is read once per KV head.
-// A block covers `split` keys of one (sequence, KV head); its 4 waves take 32-key tiles in
-// turn, each with its own online softmax, and double-buffer them: the loads of a wave's next
-// tile are in flight while it computes the current one.  The waves merge through LDS.  With
+// Work decomposition.  Grid (context split, KV head, sequence); 8 waves per block (4 at 64
+// rows).  All G = Hq/Hkv query heads of a KV head and all n query rows of the sequence are
+// packed into R = G*n "rows" (row r = head_local * n + j), so each K/V byte is read once per
+// KV head.  A block covers `split` keys of one (sequence, KV head); its waves take 32-key
+// tiles in turn, each with its own online softmax, and double-buffer them: the loads of a
+// wave's next tile are in flight while it computes the current one.  The waves merge through
+// LDS, each into its own region in one round, summed while the output is written.  With
 // one split the block writes the bf16 output; otherwise it writes its (max, sum) and
 // unnormalised fp32 rows to the workspace and a second launch (merge_kernel, one block per
 // (KV head, sequence)) combines the splits -- the kernel boundary orders the two, so no block
@@ -165,7 +166,13 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
   constexpr int kOPitch = D + 4;       // fp32 row pitch of the merged output in LDS
   constexpr int kQPitch = D * 2 + 16;  // byte pitch of a staged Q row (16 rows -> distinct banks)
   constexpr int kQBytes = kRows * kQPitch;
-  constexpr int kOBytes = kRows * kOPitch * 4;
+  // The waves merge through kRegions LDS regions of kRows x kOPitch fp32: one per wave when
+  // they fit in 144 KB (up to 32 rows at D = 128), else one per two waves.
+  constexpr int kRegionFloats = kRows * kOPitch;
+  constexpr int kLdsBudget = 144 * 1024;
+  constexpr int kRegions = kWaves * kRegionFloats * 4 <= kLdsBudget ? kWaves
+                           : ((kWaves / 2) * kRegionFloats * 4 <= kLdsBudget ? kWaves / 2 : 1);
+  constexpr int kOBytes = kRegions * kRegionFloats * 4;
   __shared__ __attribute__((aligned(16))) unsigned char lds[kQBytes > kOBytes ? kQBytes : kOBytes];
   __shared__ float sm_m[kWaves][kRows];
   __shared__ float sm_l[kWaves][kRows];
@@ -552,7 +559,7 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
   }
   __syncthreads();  // Q in LDS is dead; the merge below reuses the space
 
-  // ---- merge the 4 waves ----
+  // ---- merge the waves ----
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     l_run[rt] += __shfl_xor(l_run[rt], 16, 64);
@@ -582,22 +589,24 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
     }
   }
   // lane's accumulators: row rt*16 + l16, d = (4g + i) * kDt + dt -- kDt contiguous floats
-  // for each (rt, i)
+  // for each (rt, i).  Wave w stores them into region w % kRegions in round w / kRegions
+  // (later rounds add); the output pass below sums the regions in order.
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    if (wave == w) {
+  for (int round = 0; round < kWaves / kRegions; ++round) {
+    if (wave / kRegions == round) {
+      float* region = osh + (wave % kRegions) * kRegionFloats;
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
         const int r = rt * 16 + l16;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float* dst = osh + r * kOPitch + (grp * 4 + i) * kDt;
+          float* dst = region + r * kOPitch + (grp * 4 + i) * kDt;
 #pragma unroll
           for (int d4 = 0; d4 < kDt / 4; ++d4) {
             const f32x4_t x = {o[rt][d4 * 4 + 0][i], o[rt][d4 * 4 + 1][i], o[rt][d4 * 4 + 2][i],
                                o[rt][d4 * 4 + 3][i]};
             f32x4_t* dp = reinterpret_cast<f32x4_t*>(dst + 4 * d4);
-            if (w == 0) *dp = x;
+            if (round == 0) *dp = x;
             else *dp = *dp + x;
           }
         }
@@ -605,6 +614,17 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
     }
     __syncthreads();
   }
+  // row r, elements [8c, 8c + 8) of the merged (unnormalised) output
+  auto merged8 = [&](int r, int c, f32x4_t& lo, f32x4_t& hi) {
+    const float* src = osh + r * kOPitch + c * 8;
+    lo = *reinterpret_cast<const f32x4_t*>(src);
+    hi = *reinterpret_cast<const f32x4_t*>(src + 4);
+#pragma unroll
+    for (int g = 1; g < kRegions; ++g) {
+      lo += *reinterpret_cast<const f32x4_t*>(src + g * kRegionFloats);
+      hi += *reinterpret_cast<const f32x4_t*>(src + g * kRegionFloats + 4);
+    }
+  };
 
   constexpr int kCh = D / 8;  // 8-element chunks per row
   const int64_t item = static_cast<int64_t>(b) * a.Hkv + hkv;
@@ -613,10 +633,13 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
       const int r = idx / kCh, c = idx % kCh;
       const float Lr = sm_L[r];
       const float inv = Lr > 0.0f ? 1.0f / Lr : 0.0f;
-      const float* src = osh + r * kOPitch + c * 8;
+      f32x4_t lo, hi;
+      merged8(r, c, lo, hi);
       u32x4_t v;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = pack_bf16x2(src[2 * e] * inv, src[2 * e + 1] * inv);
+      v[0] = pack_bf16x2(lo[0] * inv, lo[1] * inv);
+      v[1] = pack_bf16x2(lo[2] * inv, lo[3] * inv);
+      v[2] = pack_bf16x2(hi[0] * inv, hi[1] * inv);
+      v[3] = pack_bf16x2(hi[2] * inv, hi[3] * inv);
       const int hl = r / n, j = r - hl * n;
       uint16_t* dst = a.out + static_cast<int64_t>(q0 + j) * a.o_ts +
                       static_cast<int64_t>(hkv * a.G + hl) * a.o_hs + c * 8;
@@ -629,10 +652,11 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
   const int64_t pbase = (item * a.max_splits + sidx) * a.rmax;
   for (int idx = tid; idx < R * kCh; idx += kBlock) {
     const int r = idx / kCh, c = idx % kCh;
-    const float* src = osh + r * kOPitch + c * 8;
+    f32x4_t lo, hi;
+    merged8(r, c, lo, hi);
     float* dst = a.part_o + (pbase + r) * D + c * 8;
-    reinterpret_cast<f32x4_t*>(dst)[0] = f32x4_t{src[0], src[1], src[2], src[3]};
-    reinterpret_cast<f32x4_t*>(dst)[1] = f32x4_t{src[4], src[5], src[6], src[7]};
+    reinterpret_cast<f32x4_t*>(dst)[0] = lo;
+    reinterpret_cast<f32x4_t*>(dst)[1] = hi;
   }
   if (tid < R) a.part_ml[pbase + tid] = make_float2(sm_M[tid], sm_L[tid]);
 }
