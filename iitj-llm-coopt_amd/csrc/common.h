@@ -103,6 +103,37 @@ __device__ __forceinline__ float4 sum_partials4(const float* p, int ks, int64_t 
   return s;
 }
 
+// The same sum for ks <= KS (a compile-time bound): the KS loads are unconditional -- slice
+// indices past ks - 1 repeat the last slice, which hits the cache -- so a caller can issue
+// every load of several groups before the first add, and the compiler's wait counts stay
+// exact (a load under a branch makes it wait for every load in flight).  Same order of adds
+// as sum_partials4, so the same result.
+template <int KS>
+struct Partials4 {
+  float4 v[KS];
+  __device__ __forceinline__ void load(const float* p, int ks, int64_t slice) {
+#pragma unroll
+    for (int k = 0; k < KS; ++k)
+      v[k] = *reinterpret_cast<const float4*>(p + static_cast<int64_t>(k < ks ? k : ks - 1) * slice);
+  }
+  __device__ __forceinline__ float4 sum(int ks) const {
+    float4 s = v[0];
+#pragma unroll
+    for (int k = 1; k < KS; ++k)
+      if (k < ks) {
+        s.x += v[k].x; s.y += v[k].y; s.z += v[k].z; s.w += v[k].w;
+      }
+    return s;
+  }
+};
+
+// Smallest power of two >= ks (ks in [1, 16]).
+inline int partials_bound(int ks) {
+  int b = 1;
+  while (b < ks) b <<= 1;
+  return b;
+}
+
 __device__ __forceinline__ float wave_sum_f32(float v) {
 #pragma unroll
   for (int m = 1; m < COOPT_WAVE; m <<= 1) v += __shfl_xor(v, m, COOPT_WAVE);

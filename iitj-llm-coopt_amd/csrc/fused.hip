@@ -147,6 +147,105 @@ __global__ __launch_bounds__(kThreads) void rms_norm_reg_kernel(const uint16_t* 
   }
 }
 
+// rms_norm_reg_kernel's partials path with the slice count bounded at compile time (KS):
+// every load of the row -- w, the residual and the KS partial slices of each chunk -- is
+// issued before the first add, so the row costs one global round trip.  Same arithmetic and
+// order as rms_norm_reg_kernel, so the same result.  The residual is required (the fused
+// add that follows every projection reduced this way).
+template <int CPT, int KS>
+__global__ __launch_bounds__(kThreads) void rms_norm_part_kernel(uint16_t* __restrict__ residual,
+                                                                 const uint16_t* __restrict__ w,
+                                                                 uint16_t* __restrict__ out, int H,
+                                                                 float eps,
+                                                                 const float* __restrict__ part,
+                                                                 int ks, int64_t slice) {
+  __shared__ float sh[4];
+  const int64_t row = blockIdx.x;
+  uint16_t* rr = residual + row * H;
+  Partials4<KS> plo[CPT], phi[CPT];
+  uint4 wv[CPT], rv[CPT];
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int i = (c * kThreads + threadIdx.x) * 8;
+    const int il = i < H ? i : H - 8;  // past-the-row chunks load the last one, never stored
+    wv[c] = *reinterpret_cast<const uint4*>(w + il);
+    rv[c] = *reinterpret_cast<const uint4*>(rr + il);
+    const float* pr = part + row * H + il;
+    plo[c].load(pr, ks, slice);
+    phi[c].load(pr + 4, ks, slice);
+  }
+  uint32_t xw[CPT][4];
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int i = (c * kThreads + threadIdx.x) * 8;
+    const float4 lo = plo[c].sum(ks), hi = phi[c].sum(ks);
+    xw[c][0] = round_bf16(lo.x) | (static_cast<uint32_t>(round_bf16(lo.y)) << 16);
+    xw[c][1] = round_bf16(lo.z) | (static_cast<uint32_t>(round_bf16(lo.w)) << 16);
+    xw[c][2] = round_bf16(hi.x) | (static_cast<uint32_t>(round_bf16(hi.y)) << 16);
+    xw[c][3] = round_bf16(hi.z) | (static_cast<uint32_t>(round_bf16(hi.w)) << 16);
+    const uint32_t rw[4] = {rv[c].x, rv[c].y, rv[c].z, rv[c].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float a0 = bf16_to_f32(static_cast<uint16_t>(xw[c][e])) + bf16_to_f32(static_cast<uint16_t>(rw[e]));
+      const float a1 = bf16_to_f32(static_cast<uint16_t>(xw[c][e] >> 16)) + bf16_to_f32(static_cast<uint16_t>(rw[e] >> 16));
+      xw[c][e] = round_bf16(a0) | (static_cast<uint32_t>(round_bf16(a1)) << 16);
+    }
+    if (i < H) {
+      *reinterpret_cast<uint4*>(rr + i) = make_uint4(xw[c][0], xw[c][1], xw[c][2], xw[c][3]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a0 = bf16_to_f32(static_cast<uint16_t>(xw[c][e]));
+        const float a1 = bf16_to_f32(static_cast<uint16_t>(xw[c][e] >> 16));
+        ss += a0 * a0 + a1 * a1;
+      }
+    }
+  }
+  const float rs = rsqrtf(block_sum_f32(ss, sh) / static_cast<float>(H) + eps);
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int i = (c * kThreads + threadIdx.x) * 8;
+    if (i >= H) continue;
+    const uint32_t ww[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
+    uint32_t ow[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float n0 = bf16_to_f32(round_bf16(bf16_to_f32(static_cast<uint16_t>(xw[c][e])) * rs));
+      const float n1 = bf16_to_f32(round_bf16(bf16_to_f32(static_cast<uint16_t>(xw[c][e] >> 16)) * rs));
+      const float y0 = bf16_to_f32(static_cast<uint16_t>(ww[e])) * n0;
+      const float y1 = bf16_to_f32(static_cast<uint16_t>(ww[e] >> 16)) * n1;
+      ow[e] = round_bf16(y0) | (static_cast<uint32_t>(round_bf16(y1)) << 16);
+    }
+    *reinterpret_cast<uint4*>(out + row * H + i) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+  }
+}
+
+template <int CPT>
+bool launch_rms_part(int kb, dim3 grid, hipStream_t s, uint16_t* rp, const uint16_t* wp,
+                     uint16_t* op, int hidden, float eps, const float* part, int ks,
+                     int64_t slice) {
+  // at most 32 float4 of partials in registers per thread
+  switch (kb) {
+    case 1: hipLaunchKernelGGL((rms_norm_part_kernel<CPT, 1>), grid, dim3(kThreads), 0, s, rp, wp, op, hidden, eps, part, ks, slice); return true;
+    case 2: hipLaunchKernelGGL((rms_norm_part_kernel<CPT, 2>), grid, dim3(kThreads), 0, s, rp, wp, op, hidden, eps, part, ks, slice); return true;
+    case 4: hipLaunchKernelGGL((rms_norm_part_kernel<CPT, 4>), grid, dim3(kThreads), 0, s, rp, wp, op, hidden, eps, part, ks, slice); return true;
+    case 8:
+      if constexpr (CPT <= 2) {
+        hipLaunchKernelGGL((rms_norm_part_kernel<CPT, 8>), grid, dim3(kThreads), 0, s, rp, wp, op, hidden, eps, part, ks, slice);
+        return true;
+      }
+      return false;
+    case 16:
+      if constexpr (CPT <= 1) {
+        hipLaunchKernelGGL((rms_norm_part_kernel<CPT, 16>), grid, dim3(kThreads), 0, s, rp, wp, op, hidden, eps, part, ks, slice);
+        return true;
+      }
+      return false;
+    default:
+      return false;
+  }
+}
+
 // In-place neox rotary embedding of q [T, Hq, D] and k [T, Hkv, D]: for i < D/2,
 // (x_i, x_{i+D/2}) -> (x_i c - x_{i+D/2} s, x_{i+D/2} c + x_i s) with c, s = cos/sin[pos][i]
 // from bf16 tables [max_pos, D] (engine/model.py:92-94, 120-124).  One thread per pair.
@@ -184,6 +283,9 @@ __device__ __forceinline__ uint32_t pack_sum_bf16(float a, float b) {
 // out[t, j] = silu(gu[t, j]) * gu[t, F + j] (engine/model.py:250-253), 8 elements per thread.
 // With `part` set, gu is not read: gu[t] = bf16(sum of the ks fp32 slices part[k * slice +
 // t * 2F]), the split-K partials of the gate_up projection, reduced in its own order.
+// KS > 0: partials with the slice count bounded at compile time, all 4 * KS loads issued
+// before the first add (one global round trip); KS = 0: the runtime-bounded path.
+template <int KS>
 __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __restrict__ gu,
                                                             uint16_t* __restrict__ out, int64_t T,
                                                             int F, const float* __restrict__ part,
@@ -196,8 +298,18 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __re
   uint32_t gw[4], uw[4];
   if (part) {
     const float* pg = part + t * 2 * F + j;
-    const float4 g0 = sum_partials4(pg, ks, slice), g1 = sum_partials4(pg + 4, ks, slice);
-    const float4 u0 = sum_partials4(pg + F, ks, slice), u1 = sum_partials4(pg + F + 4, ks, slice);
+    float4 g0, g1, u0, u1;
+    if constexpr (KS > 0) {
+      Partials4<KS> pg0, pg1, pu0, pu1;
+      pg0.load(pg, ks, slice);
+      pg1.load(pg + 4, ks, slice);
+      pu0.load(pg + F, ks, slice);
+      pu1.load(pg + F + 4, ks, slice);
+      g0 = pg0.sum(ks); g1 = pg1.sum(ks); u0 = pu0.sum(ks); u1 = pu1.sum(ks);
+    } else {
+      g0 = sum_partials4(pg, ks, slice); g1 = sum_partials4(pg + 4, ks, slice);
+      u0 = sum_partials4(pg + F, ks, slice); u1 = sum_partials4(pg + F + 4, ks, slice);
+    }
     gw[0] = pack_sum_bf16(g0.x, g0.y); gw[1] = pack_sum_bf16(g0.z, g0.w);
     gw[2] = pack_sum_bf16(g1.x, g1.y); gw[3] = pack_sum_bf16(g1.z, g1.w);
     uw[0] = pack_sum_bf16(u0.x, u0.y); uw[1] = pack_sum_bf16(u0.z, u0.w);
@@ -271,6 +383,17 @@ extern "C" int coopt_rms_norm_partials(const float* part, int ks, int64_t slice_
   const uint16_t* wp = static_cast<const uint16_t*>(weight);
   uint16_t* op = static_cast<uint16_t*>(out);
   const int cpt = (hidden + kThreads * 8 - 1) / (kThreads * 8);
+  if (rp != nullptr) {
+    const int kb = partials_bound(ks);
+    bool done = false;
+    switch (cpt) {
+      case 1: done = launch_rms_part<1>(kb, grid, s, rp, wp, op, hidden, eps, part, ks, slice_stride); break;
+      case 2: done = launch_rms_part<2>(kb, grid, s, rp, wp, op, hidden, eps, part, ks, slice_stride); break;
+      case 3: done = launch_rms_part<3>(kb, grid, s, rp, wp, op, hidden, eps, part, ks, slice_stride); break;
+      case 4: done = launch_rms_part<4>(kb, grid, s, rp, wp, op, hidden, eps, part, ks, slice_stride); break;
+    }
+    if (done) return coopt::check_launch("coopt_rms_norm_partials");
+  }
   switch (cpt) {
     case 1: hipLaunchKernelGGL(rms_norm_reg_kernel<1>, grid, dim3(kThreads), 0, s, nullptr, rp, wp, op, hidden, eps, part, ks, slice_stride); break;
     case 2: hipLaunchKernelGGL(rms_norm_reg_kernel<2>, grid, dim3(kThreads), 0, s, nullptr, rp, wp, op, hidden, eps, part, ks, slice_stride); break;
@@ -306,7 +429,7 @@ extern "C" int coopt_silu_mul(const void* gate_up, void* out, int64_t T, int F,
                 "null or misaligned pointer");
   coopt::clear_error();
   const int64_t total = T * (F / 8);
-  hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)),
+  hipLaunchKernelGGL(silu_mul_kernel<0>, dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)),
                      dim3(kThreads), 0, static_cast<hipStream_t>(stream),
                      static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(out), T, F,
                      nullptr, 0, 0);
@@ -323,8 +446,15 @@ extern "C" int coopt_silu_mul_partials(const float* part, int ks, int64_t slice_
                 "null or misaligned pointer");
   coopt::clear_error();
   const int64_t total = T * (F / 8);
-  hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)),
-                     dim3(kThreads), 0, static_cast<hipStream_t>(stream), nullptr,
-                     static_cast<uint16_t*>(out), T, F, part, ks, slice_stride);
+  const dim3 grid(static_cast<unsigned>((total + kThreads - 1) / kThreads));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  uint16_t* op = static_cast<uint16_t*>(out);
+  switch (partials_bound(ks)) {  // at most 32 float4 of partials in registers per thread
+    case 1: hipLaunchKernelGGL(silu_mul_kernel<1>, grid, dim3(kThreads), 0, st, nullptr, op, T, F, part, ks, slice_stride); break;
+    case 2: hipLaunchKernelGGL(silu_mul_kernel<2>, grid, dim3(kThreads), 0, st, nullptr, op, T, F, part, ks, slice_stride); break;
+    case 4: hipLaunchKernelGGL(silu_mul_kernel<4>, grid, dim3(kThreads), 0, st, nullptr, op, T, F, part, ks, slice_stride); break;
+    case 8: hipLaunchKernelGGL(silu_mul_kernel<8>, grid, dim3(kThreads), 0, st, nullptr, op, T, F, part, ks, slice_stride); break;
+    default: hipLaunchKernelGGL(silu_mul_kernel<0>, grid, dim3(kThreads), 0, st, nullptr, op, T, F, part, ks, slice_stride); break;
+  }
   return coopt::check_launch("coopt_silu_mul_partials");
 }

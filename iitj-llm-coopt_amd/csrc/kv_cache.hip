@@ -185,7 +185,34 @@ __device__ __forceinline__ uint4 qkv_chunk(const QkvArgs& a, int t, int64_t col)
   return *reinterpret_cast<const uint4*>(a.qkv + static_cast<int64_t>(t) * a.qkv_ts + col);
 }
 
-template <int G, bool INT8>
+// Elements [col, col + 8) of row t, loaded now and returned by get(): with KS > 0 the fp32
+// partials (slice count bounded by KS at compile time, every load unconditional), else
+// qkv_chunk's bf16 row or runtime-bounded partials.
+template <int KS>
+struct QkvChunk {
+  Partials4<(KS > 0 ? KS : 1)> lo, hi;
+  uint4 raw;
+  __device__ __forceinline__ void load(const QkvArgs& a, int t, int64_t col) {
+    if constexpr (KS > 0) {
+      const float* p = a.part + static_cast<int64_t>(t) * (a.Hq + 2 * a.Hkv) * a.D + col;
+      lo.load(p, a.ks, a.slice);
+      hi.load(p + 4, a.ks, a.slice);
+    } else {
+      raw = qkv_chunk(a, t, col);
+    }
+  }
+  __device__ __forceinline__ uint4 get(const QkvArgs& a) const {
+    if constexpr (KS > 0) {
+      const float4 l = lo.sum(a.ks), h = hi.sum(a.ks);
+      return make_uint4(pack2_bf16(l.x, l.y), pack2_bf16(l.z, l.w), pack2_bf16(h.x, h.y),
+                        pack2_bf16(h.z, h.w));
+    } else {
+      return raw;
+    }
+  }
+};
+
+template <int G, bool INT8, int KS>
 __global__ __launch_bounds__(256) void qkv_epilogue_kernel(QkvArgs a) {
   // grid: x covers T tokens x G lanes (32-bit, checked by the host), y the q / k head
   const int lid = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
@@ -193,19 +220,27 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(QkvArgs a) {
   const int t = lid / G;
   if (t >= a.T) return;  // whole groups leave together
   const int h = blockIdx.y;
+  const bool is_k = h >= a.Hq;  // uniform over the block
+  const int hk = h - a.Hq;
   const int D = G * 8;
-  const uint4 xr = qkv_chunk(a, t, static_cast<int64_t>(h) * D + c * 8);
-  // partner words (elements i +- D/2) from lane c ^ (G/2)
-  uint32_t xw[4] = {xr.x, xr.y, xr.z, xr.w}, pw[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) pw[e] = __shfl_xor(xw[e], G / 2, COOPT_WAVE);
+  // Issue order: the position (and slot), then the row's chunks; the wait for the position
+  // (the cos/sin addresses) then leaves the chunk loads in flight.
   int64_t p = a.pos[t];
+  const int64_t slot = is_k ? a.slot_mapping[t] : -1;
+  QkvChunk<KS> xc, vc;
+  xc.load(a, t, static_cast<int64_t>(h) * D + c * 8);
+  if (is_k) vc.load(a, t, static_cast<int64_t>(a.Hq + a.Hkv + hk) * D + c * 8);
   p = p < 0 ? 0 : (p >= a.max_pos ? a.max_pos - 1 : p);
   const bool first = c < G / 2;
   const int i0 = (first ? c : c - G / 2) * 8;
   const uint16_t* cp = a.cos + p * a.tab_stride + i0;
   const uint16_t* sp = a.sin + p * a.tab_stride + i0;
   const uint4 cr = *reinterpret_cast<const uint4*>(cp), sr = *reinterpret_cast<const uint4*>(sp);
+  const uint4 xr = xc.get(a);
+  // partner words (elements i +- D/2) from lane c ^ (G/2)
+  uint32_t xw[4] = {xr.x, xr.y, xr.z, xr.w}, pw[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) pw[e] = __shfl_xor(xw[e], G / 2, COOPT_WAVE);
   const uint32_t cw[4] = {cr.x, cr.y, cr.z, cr.w}, sw[4] = {sr.x, sr.y, sr.z, sr.w};
   uint32_t yw[4];
 #pragma unroll
@@ -223,14 +258,12 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(QkvArgs a) {
     yw[e] = pack2_bf16(y[0], y[1]);
   }
   const uint4 yr = make_uint4(yw[0], yw[1], yw[2], yw[3]);
-  if (h < a.Hq) {
+  if (!is_k) {
     *reinterpret_cast<uint4*>(a.q_out + t * a.q_ts + h * a.q_hs + c * 8) = yr;
     return;
   }
-  const int hk = h - a.Hq;
-  const int64_t slot = a.slot_mapping[t];
   if (slot < 0 || slot >= a.num_slots) return;  // padding row: the group leaves together
-  const uint4 vr = qkv_chunk(a, t, static_cast<int64_t>(a.Hq + a.Hkv + hk) * D + c * 8);
+  const uint4 vr = vc.get(a);
   const int64_t blk = a.bs_shift >= 0 ? slot >> a.bs_shift : slot / a.block_size;
   const int64_t off = a.bs_shift >= 0 ? slot & ((int64_t{1} << a.bs_shift) - 1) : slot % a.block_size;
   store_kv_chunk<G, INT8>(yr, vr, a.kc, a.vc, blk * a.c_bs + off * a.c_ts + hk * a.c_hs + c * 8,
@@ -611,10 +644,23 @@ extern "C" int coopt_qkv_epilogue(int cache_dtype, const void* qkv, int64_t qkv_
   COOPT_REQUIRE(lanes <= 0x7fffff00LL && Hq + Hkv <= 65535, "T * D / 8 must stay below 2^31");
   const dim3 grid(static_cast<unsigned>((lanes + 255) / 256), static_cast<unsigned>(Hq + Hkv));
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-#define COOPT_QKV(GV)                                                                        \
-  case GV:                                                                                   \
-    if (int8) hipLaunchKernelGGL((qkv_epilogue_kernel<GV, true>), grid, dim3(256), 0, st, a); \
-    else hipLaunchKernelGGL((qkv_epilogue_kernel<GV, false>), grid, dim3(256), 0, st, a);    \
+  // partials with at most 8 slices: the compile-time-bounded loader (all loads up front)
+  const int kb = part ? partials_bound(ks) : 0;
+  const int kbound = kb <= 8 ? kb : 0;
+#define COOPT_QKV_KS(GV, KSV)                                                                   \
+  case KSV:                                                                                     \
+    if (int8) hipLaunchKernelGGL((qkv_epilogue_kernel<GV, true, KSV>), grid, dim3(256), 0, st, a); \
+    else hipLaunchKernelGGL((qkv_epilogue_kernel<GV, false, KSV>), grid, dim3(256), 0, st, a);    \
+    break;
+#define COOPT_QKV(GV)          \
+  case GV:                     \
+    switch (kbound) {          \
+      COOPT_QKV_KS(GV, 0)      \
+      COOPT_QKV_KS(GV, 1)      \
+      COOPT_QKV_KS(GV, 2)      \
+      COOPT_QKV_KS(GV, 4)      \
+      COOPT_QKV_KS(GV, 8)      \
+    }                          \
     break;
   switch (G) {
     COOPT_QKV(8)
@@ -622,6 +668,7 @@ extern "C" int coopt_qkv_epilogue(int cache_dtype, const void* qkv, int64_t qkv_
     COOPT_QKV(32)
   }
 #undef COOPT_QKV
+#undef COOPT_QKV_KS
   return coopt::check_launch("coopt_qkv_epilogue");
 }
 
