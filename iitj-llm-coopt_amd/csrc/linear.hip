@@ -200,6 +200,8 @@ __global__ __launch_bounds__(64 * WAVES) void linear_kernel(LinArgs a) {
 }
 
 // y[m, n] = bf16(sum over slices s = 0..ks-1, in order, of part[s, m, n]); 4 columns a thread.
+// KS: compile-time bound on ks (all loads issued before the first add), 0 = runtime bound.
+template <int KS>
 __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ part, int ks,
                                                      int64_t slice, int M, int N,
                                                      uint16_t* __restrict__ y, int64_t ldy) {
@@ -207,7 +209,15 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ p
   const int nq = N / 4;
   if (gid >= static_cast<int64_t>(M) * nq) return;
   const int m = static_cast<int>(gid / nq), n = static_cast<int>(gid % nq) * 4;
-  const float4 s = sum_partials4(part + static_cast<int64_t>(m) * N + n, ks, slice);
+  const float* p = part + static_cast<int64_t>(m) * N + n;
+  float4 s;
+  if constexpr (KS > 0) {
+    Partials4<KS> pl;
+    pl.load(p, ks, slice);
+    s = pl.sum(ks);
+  } else {
+    s = sum_partials4(p, ks, slice);
+  }
   uint16_t* o = y + static_cast<int64_t>(m) * ldy + n;
   const uint32_t lo = f32_to_bf16(s.x) | (static_cast<uint32_t>(f32_to_bf16(s.y)) << 16);
   const uint32_t hi = f32_to_bf16(s.z) | (static_cast<uint32_t>(f32_to_bf16(s.w)) << 16);
@@ -308,9 +318,17 @@ extern "C" int coopt_linear(const void* x, int64_t ldx, const void* w, int64_t l
   int rc = run_linear(x, ldx, w, ldw, M, N, K, y, ldy, workspace, workspace_bytes, false, s, p);
   if (rc != COOPT_OK || M == 0 || N == 0 || p.ks == 1) return rc;
   const int64_t n4 = static_cast<int64_t>(M) * (N / 4);
-  hipLaunchKernelGGL(reduce_kernel, dim3(static_cast<unsigned>((n4 + 255) / 256)), dim3(256), 0,
-                     s, static_cast<const float*>(workspace), p.ks,
-                     static_cast<int64_t>(p.mt) * 16 * N, M, N, static_cast<uint16_t*>(y), ldy);
+  const dim3 grid(static_cast<unsigned>((n4 + 255) / 256));
+  const float* part = static_cast<const float*>(workspace);
+  const int64_t slice = static_cast<int64_t>(p.mt) * 16 * N;
+  uint16_t* yp = static_cast<uint16_t*>(y);
+  switch (partials_bound(p.ks)) {
+    case 2: hipLaunchKernelGGL(reduce_kernel<2>, grid, dim3(256), 0, s, part, p.ks, slice, M, N, yp, ldy); break;
+    case 4: hipLaunchKernelGGL(reduce_kernel<4>, grid, dim3(256), 0, s, part, p.ks, slice, M, N, yp, ldy); break;
+    case 8: hipLaunchKernelGGL(reduce_kernel<8>, grid, dim3(256), 0, s, part, p.ks, slice, M, N, yp, ldy); break;
+    case 16: hipLaunchKernelGGL(reduce_kernel<16>, grid, dim3(256), 0, s, part, p.ks, slice, M, N, yp, ldy); break;
+    default: hipLaunchKernelGGL(reduce_kernel<0>, grid, dim3(256), 0, s, part, p.ks, slice, M, N, yp, ldy); break;
+  }
   return coopt::check_launch("coopt_linear");
 }
 
