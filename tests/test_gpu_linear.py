@@ -109,8 +109,11 @@ def test_linear_argument_errors(dev):
     assert "workspace" in _lib.last_error()
 
 
+# (160, 4096, 4352) splits K 7 ways: a slice count that is not a power of two, so the
+# consumers' compile-time-bounded loaders (bound 8) repeat the last slice without adding it.
 @pytest.mark.parametrize("M,N,K", [(160, 4096, 4096), (160, 4096, 14336), (32, 2048, 2048),
-                                   (32, 2048, 8192), (17, 264, 256), (64, 2048, 128)])
+                                   (32, 2048, 8192), (17, 264, 256), (64, 2048, 128),
+                                   (160, 4096, 4352)])
 def test_deferred_reduction_into_rms_norm_is_bit_exact(dev, M, N, K):
     """linear(defer_reduce=True) + rms_norm(partials) == linear() + rms_norm(), bit for bit,
     with and without the fused residual add (the reduction order is the same)."""
@@ -134,7 +137,8 @@ def test_deferred_reduction_into_rms_norm_is_bit_exact(dev, M, N, K):
     assert torch.equal(got, want) and torch.equal(r2, r1)
 
 
-@pytest.mark.parametrize("M,F,K", [(32, 8192, 2048), (64, 8192, 2048), (5, 64, 256)])
+@pytest.mark.parametrize("M,F,K", [(32, 8192, 2048), (64, 8192, 2048), (5, 64, 256),
+                                   (32, 512, 4224)])   # the last splits K 7 ways
 def test_deferred_reduction_into_silu_mul_is_bit_exact(dev, M, F, K):
     """linear(defer_reduce=True) + silu_and_mul(partials) == linear() + silu_and_mul()."""
     g = torch.Generator(device=dev).manual_seed(M + F + K)

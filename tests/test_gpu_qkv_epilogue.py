@@ -24,7 +24,8 @@ def tables(D, max_pos, dev):
 
 @pytest.mark.parametrize("kv", ["auto", "int8"])
 @pytest.mark.parametrize("T,Hq,Hkv,D,K", [(160, 32, 8, 128, 4096), (32, 32, 8, 64, 2048),
-                                          (7, 4, 2, 128, 256)])
+                                          (7, 4, 2, 128, 256),
+                                          (160, 8, 2, 64, 4352)])   # K split 7 ways
 @pytest.mark.parametrize("deferred", [False, True])
 def test_epilogue_equals_unfused_chain(dev, kv, T, Hq, Hkv, D, K, deferred):
     g = torch.Generator(device=dev).manual_seed(T + D + K)
