@@ -19,7 +19,8 @@ from .block_manager import BlockManager, OutOfBlocks
 from .kv_blocks import allocate_block_major_kv, copy_blocks, migrate_out_of
 from .kv_cache import (allocate_kv_cache, dequantize, qkv_rope_and_cache, quantize,
                        reshape_and_cache_flash)
-from .kv_tier import KVTierManager, SwappedKV, swap_in_blocks, swap_out_blocks
+from .kv_tier import (KVTierManager, SwappedKV, swap_in_blocks, swap_in_caches, swap_out_blocks,
+                      swap_out_caches)
 from .spec_decode import AcceptResult, accept, sample, softmax, verify
 
 __all__ = [
@@ -28,4 +29,5 @@ __all__ = [
     "quantize", "reshape_and_cache_flash", "AcceptResult", "accept", "sample", "softmax",
     "verify", "KVTierManager", "SwappedKV", "swap_in_blocks", "swap_out_blocks",
     "allocate_block_major_kv", "copy_blocks", "migrate_out_of", "qkv_rope_and_cache",
+    "swap_out_caches", "swap_in_caches",
 ]

@@ -32,6 +32,10 @@ SIGNATURES = {
                                _i, _i64, _p, _p, _p]),
     "coopt_kv_swap_in": (_i, [_i, _i, _p, _p, _p, _i, _i, _i, _i, _i64, _p, _i64, _i64, _i64, _p,
                               _i64, _i64, _i64, _p]),
+    "coopt_kv_swap_out_caches": (_i, [_i, _i, _i, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p,
+                                      _i, _i, _i, _i, _i64, _p, _p, _p]),
+    "coopt_kv_swap_in_caches": (_i, [_i, _i, _i, _p, _p, _p, _i, _i, _i, _i, _i64, _p, _p, _i64,
+                                     _i64, _i64, _i64, _i64, _i64, _p]),
     "coopt_dequantize": (_i, [_i, _p, _p, _i64, _i, _i, _p, _p]),
     "coopt_kv_copy_blocks": (_i, [_p, _i, _p, _p, _i, _i64, _p]),
     "coopt_linear_workspace": (_sz, [_i, _i, _i]),

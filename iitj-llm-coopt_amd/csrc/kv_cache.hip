@@ -393,12 +393,25 @@ struct SwapElt {  // bytes of 8 elements in the swapped format
   static constexpr int kBytes = BITS == 16 ? 16 : (BITS == 8 ? 8 : 4);
 };
 
+// Up to kMaxSwapCaches caches (e.g. the K and V caches of every layer) of one shape and
+// strides, swapped by one launch: grid.y picks the cache, and cache i's swapped rows sit at
+// q + i * q_stride bytes and scale + i * s_stride elements.
+constexpr int kMaxSwapCaches = 64;
+struct CacheSet {
+  const void* c[kMaxSwapCaches];
+  uint16_t* s[kMaxSwapCaches];  // INT8 caches: their fp16 scale caches
+};
+
 template <int G, int BITS, bool SRC8>
 __global__ __launch_bounds__(256) void swap_out_kernel(
-    const void* __restrict__ cache, int64_t c_bs, int64_t c_ts, int64_t c_hs,
-    const uint16_t* __restrict__ cscale, int64_t s_bs, int64_t s_ts, int64_t s_hs,
+    CacheSet cs, int64_t c_bs, int64_t c_ts, int64_t c_hs, int64_t s_bs, int64_t s_ts, int64_t s_hs,
     const int64_t* __restrict__ ids, int nid, int bs, int Hkv, int64_t num_blocks,
-    unsigned char* __restrict__ q, uint16_t* __restrict__ scale) {
+    unsigned char* __restrict__ q, uint16_t* __restrict__ scale, int64_t q_stride,
+    int64_t s_stride) {
+  const void* __restrict__ cache = cs.c[blockIdx.y];
+  const uint16_t* __restrict__ cscale = cs.s[blockIdx.y];
+  q += blockIdx.y * q_stride;
+  scale += blockIdx.y * s_stride;
   constexpr int D = G * 8;
   constexpr int kOut = SwapElt<BITS>::kBytes;
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -455,10 +468,14 @@ __global__ __launch_bounds__(256) void swap_out_kernel(
 
 template <int G, int BITS, bool DST8>
 __global__ __launch_bounds__(256) void swap_in_kernel(
-    const unsigned char* __restrict__ q, const uint16_t* __restrict__ scale,
-    const int64_t* __restrict__ ids, int nid, int bs, int Hkv, int64_t num_blocks,
-    void* __restrict__ cache, int64_t c_bs, int64_t c_ts, int64_t c_hs,
-    uint16_t* __restrict__ cscale, int64_t s_bs, int64_t s_ts, int64_t s_hs) {
+    const unsigned char* __restrict__ q, const uint16_t* __restrict__ scale, int64_t q_stride,
+    int64_t s_stride, const int64_t* __restrict__ ids, int nid, int bs, int Hkv,
+    int64_t num_blocks, CacheSet cs, int64_t c_bs, int64_t c_ts, int64_t c_hs, int64_t s_bs,
+    int64_t s_ts, int64_t s_hs) {
+  void* __restrict__ cache = const_cast<void*>(cs.c[blockIdx.y]);
+  uint16_t* __restrict__ cscale = cs.s[blockIdx.y];
+  q += blockIdx.y * q_stride;
+  scale += blockIdx.y * s_stride;
   constexpr int D = G * 8;
   constexpr int kIn = SwapElt<BITS>::kBytes;
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -505,23 +522,24 @@ __global__ __launch_bounds__(256) void swap_in_kernel(
 }
 
 template <int BITS, bool I8>
-int launch_swap(bool out, int G, const void* cache, int64_t c_bs, int64_t c_ts, int64_t c_hs,
-                void* cscale, int64_t s_bs, int64_t s_ts, int64_t s_hs, const int64_t* ids, int nid,
-                int bs, int Hkv, int64_t num_blocks, void* q, void* scale, hipStream_t stream) {
+int launch_swap(bool out, int G, const CacheSet& cs, int n, int64_t c_bs, int64_t c_ts, int64_t c_hs,
+                int64_t s_bs, int64_t s_ts, int64_t s_hs, const int64_t* ids, int nid,
+                int bs, int Hkv, int64_t num_blocks, void* q, void* scale, int64_t q_stride,
+                int64_t s_stride, hipStream_t stream) {
   const int64_t threads = static_cast<int64_t>(nid) * bs * Hkv * G;
-  const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+  const dim3 grid(static_cast<unsigned>((threads + 255) / 256), static_cast<unsigned>(n));
 #define COOPT_SW(GV)                                                                              \
   case GV:                                                                                        \
     if (out)                                                                                      \
-      hipLaunchKernelGGL((swap_out_kernel<GV, BITS, I8>), grid, dim3(256), 0, stream, cache, c_bs, \
-                         c_ts, c_hs, static_cast<const uint16_t*>(cscale), s_bs, s_ts, s_hs, ids, nid, \
-                         bs, Hkv, num_blocks, static_cast<unsigned char*>(q),                    \
-                         static_cast<uint16_t*>(scale));                                         \
+      hipLaunchKernelGGL((swap_out_kernel<GV, BITS, I8>), grid, dim3(256), 0, stream, cs, c_bs,   \
+                         c_ts, c_hs, s_bs, s_ts, s_hs, ids, nid, bs, Hkv, num_blocks,             \
+                         static_cast<unsigned char*>(q), static_cast<uint16_t*>(scale), q_stride, \
+                         s_stride);                                                               \
     else                                                                                          \
       hipLaunchKernelGGL((swap_in_kernel<GV, BITS, I8>), grid, dim3(256), 0, stream,             \
                          static_cast<const unsigned char*>(q), static_cast<const uint16_t*>(scale), \
-                         ids, nid, bs, Hkv, num_blocks, const_cast<void*>(cache), c_bs, c_ts, c_hs, \
-                         static_cast<uint16_t*>(cscale), s_bs, s_ts, s_hs);                      \
+                         q_stride, s_stride, ids, nid, bs, Hkv, num_blocks, cs, c_bs, c_ts, c_hs, \
+                         s_bs, s_ts, s_hs);                                                       \
     break;
   switch (G) {
     COOPT_SW(1)
@@ -564,22 +582,51 @@ int check_swap(int bits, int cache_dtype, const void* cache, int64_t c_bs, int64
   return COOPT_OK;
 }
 
-int dispatch_swap(bool out, int bits, int cache_dtype, const void* cache, int64_t c_bs, int64_t c_ts,
-                  int64_t c_hs, void* cscale, int64_t s_bs, int64_t s_ts, int64_t s_hs,
+int dispatch_swap(bool out, int bits, int cache_dtype, const CacheSet& cs, int n, int64_t c_bs,
+                  int64_t c_ts, int64_t c_hs, int64_t s_bs, int64_t s_ts, int64_t s_hs,
                   const int64_t* ids, int nid, int bs, int Hkv, int D, int64_t num_blocks, void* q,
-                  void* scale, hipStream_t s) {
+                  void* scale, int64_t q_stride, int64_t s_stride, hipStream_t s) {
   const int G = D / 8;
   if (cache_dtype == COOPT_DT_I8)
-    return launch_swap<8, true>(out, G, cache, c_bs, c_ts, c_hs, cscale, s_bs, s_ts, s_hs, ids, nid, bs,
-                                Hkv, num_blocks, q, scale, s);
+    return launch_swap<8, true>(out, G, cs, n, c_bs, c_ts, c_hs, s_bs, s_ts, s_hs, ids, nid, bs, Hkv,
+                                num_blocks, q, scale, q_stride, s_stride, s);
   if (bits == 16)
-    return launch_swap<16, false>(out, G, cache, c_bs, c_ts, c_hs, cscale, s_bs, s_ts, s_hs, ids, nid,
-                                  bs, Hkv, num_blocks, q, scale, s);
+    return launch_swap<16, false>(out, G, cs, n, c_bs, c_ts, c_hs, s_bs, s_ts, s_hs, ids, nid, bs, Hkv,
+                                  num_blocks, q, scale, q_stride, s_stride, s);
   if (bits == 8)
-    return launch_swap<8, false>(out, G, cache, c_bs, c_ts, c_hs, cscale, s_bs, s_ts, s_hs, ids, nid, bs,
-                                 Hkv, num_blocks, q, scale, s);
-  return launch_swap<4, false>(out, G, cache, c_bs, c_ts, c_hs, cscale, s_bs, s_ts, s_hs, ids, nid, bs,
-                               Hkv, num_blocks, q, scale, s);
+    return launch_swap<8, false>(out, G, cs, n, c_bs, c_ts, c_hs, s_bs, s_ts, s_hs, ids, nid, bs, Hkv,
+                                 num_blocks, q, scale, q_stride, s_stride, s);
+  return launch_swap<4, false>(out, G, cs, n, c_bs, c_ts, c_hs, s_bs, s_ts, s_hs, ids, nid, bs, Hkv,
+                               num_blocks, q, scale, q_stride, s_stride, s);
+}
+
+// Swapped bytes of one cache's rows (codes; scales are nid * bs * Hkv fp16).
+int64_t swap_q_bytes(int bits, int nid, int bs, int Hkv, int D) {
+  return static_cast<int64_t>(nid) * bs * Hkv * (D / 8) * (bits == 16 ? 16 : (bits == 8 ? 8 : 4));
+}
+
+// n caches in launches of up to kMaxSwapCaches; caches[i] (and scales[i]) swap with the
+// rows at q + i * swap_q_bytes and scale + i * nid * bs * Hkv.
+int swap_caches(bool out, int bits, int cache_dtype, int n, const void* const* caches,
+                const void* const* scales, int64_t c_bs, int64_t c_ts, int64_t c_hs, int64_t s_bs,
+                int64_t s_ts, int64_t s_hs, const int64_t* ids, int nid, int bs, int Hkv, int D,
+                int64_t num_blocks, void* q, void* scale, hipStream_t s) {
+  const int64_t qb = swap_q_bytes(bits, nid, bs, Hkv, D);
+  const int64_t sb = static_cast<int64_t>(nid) * bs * Hkv;
+  for (int i0 = 0; i0 < n; i0 += kMaxSwapCaches) {
+    const int m = n - i0 < kMaxSwapCaches ? n - i0 : kMaxSwapCaches;
+    CacheSet cs{};
+    for (int i = 0; i < m; ++i) {
+      cs.c[i] = caches[i0 + i];
+      cs.s[i] = scales ? static_cast<uint16_t*>(const_cast<void*>(scales[i0 + i])) : nullptr;
+    }
+    unsigned char* qc = static_cast<unsigned char*>(q) + i0 * qb;
+    uint16_t* sc = scale ? static_cast<uint16_t*>(scale) + i0 * sb : nullptr;
+    const int rc = dispatch_swap(out, bits, cache_dtype, cs, m, c_bs, c_ts, c_hs, s_bs, s_ts, s_hs,
+                                 ids, nid, bs, Hkv, D, num_blocks, qc, sc, qb, sb, s);
+    if (rc != COOPT_OK) return rc;
+  }
+  return COOPT_OK;
 }
 
 }  // namespace
@@ -797,10 +844,9 @@ extern "C" int coopt_kv_swap_out(int bits, int cache_dtype, const void* cache,
                             cache_scale, block_ids, num_ids, block_size, Hkv, D, num_blocks, q, scale);
   if (rc != COOPT_OK || num_ids == 0) return rc;
   coopt::clear_error();
-  return dispatch_swap(true, bits, cache_dtype, cache, c_blk_stride, c_tok_stride, c_head_stride,
-                       const_cast<void*>(cache_scale), s_blk_stride, s_tok_stride, s_head_stride,
-                       block_ids, num_ids, block_size, Hkv, D, num_blocks, q, scale,
-                       static_cast<hipStream_t>(stream));
+  return swap_caches(true, bits, cache_dtype, 1, &cache, &cache_scale, c_blk_stride, c_tok_stride,
+                     c_head_stride, s_blk_stride, s_tok_stride, s_head_stride, block_ids, num_ids,
+                     block_size, Hkv, D, num_blocks, q, scale, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int coopt_kv_swap_in(int bits, int cache_dtype, const void* q, const void* scale,
@@ -813,8 +859,59 @@ extern "C" int coopt_kv_swap_in(int bits, int cache_dtype, const void* q, const 
                             cache_scale, block_ids, num_ids, block_size, Hkv, D, num_blocks, q, scale);
   if (rc != COOPT_OK || num_ids == 0) return rc;
   coopt::clear_error();
-  return dispatch_swap(false, bits, cache_dtype, cache, c_blk_stride, c_tok_stride, c_head_stride,
-                       cache_scale, s_blk_stride, s_tok_stride, s_head_stride, block_ids, num_ids,
-                       block_size, Hkv, D, num_blocks, const_cast<void*>(q), const_cast<void*>(scale),
-                       static_cast<hipStream_t>(stream));
+  const void* c = cache;
+  const void* cs = cache_scale;
+  return swap_caches(false, bits, cache_dtype, 1, &c, &cs, c_blk_stride, c_tok_stride,
+                     c_head_stride, s_blk_stride, s_tok_stride, s_head_stride, block_ids, num_ids,
+                     block_size, Hkv, D, num_blocks, const_cast<void*>(q), const_cast<void*>(scale),
+                     static_cast<hipStream_t>(stream));
+}
+
+extern "C" int coopt_kv_swap_out_caches(int bits, int cache_dtype, int num_caches,
+                                        const void* const* caches, const void* const* cache_scales,
+                                        int64_t c_blk_stride, int64_t c_tok_stride,
+                                        int64_t c_head_stride, int64_t s_blk_stride,
+                                        int64_t s_tok_stride, int64_t s_head_stride,
+                                        const int64_t* block_ids, int num_ids, int block_size,
+                                        int Hkv, int D, int64_t num_blocks, void* q, void* scale,
+                                        coopt_stream_t stream) {
+  COOPT_REQUIRE(num_caches >= 0 && (num_caches == 0 || caches), "bad cache list");
+  for (int i = 0; i < num_caches; ++i) {
+    const int rc = check_swap(bits, cache_dtype, caches[i], c_blk_stride, c_tok_stride,
+                              c_head_stride, cache_scales ? cache_scales[i] : nullptr, block_ids,
+                              num_ids, block_size, Hkv, D, num_blocks, q, scale);
+    if (rc != COOPT_OK) return rc;
+  }
+  if (num_caches == 0 || num_ids == 0) return COOPT_OK;
+  coopt::clear_error();
+  return swap_caches(true, bits, cache_dtype, num_caches, caches, cache_scales, c_blk_stride,
+                     c_tok_stride, c_head_stride, s_blk_stride, s_tok_stride, s_head_stride,
+                     block_ids, num_ids, block_size, Hkv, D, num_blocks, q, scale,
+                     static_cast<hipStream_t>(stream));
+}
+
+extern "C" int coopt_kv_swap_in_caches(int bits, int cache_dtype, int num_caches, const void* q,
+                                       const void* scale, const int64_t* block_ids, int num_ids,
+                                       int block_size, int Hkv, int D, int64_t num_blocks,
+                                       void* const* caches, void* const* cache_scales,
+                                       int64_t c_blk_stride, int64_t c_tok_stride,
+                                       int64_t c_head_stride, int64_t s_blk_stride,
+                                       int64_t s_tok_stride, int64_t s_head_stride,
+                                       coopt_stream_t stream) {
+  COOPT_REQUIRE(num_caches >= 0 && (num_caches == 0 || caches), "bad cache list");
+  for (int i = 0; i < num_caches; ++i) {
+    const int rc = check_swap(bits, cache_dtype, caches[i], c_blk_stride, c_tok_stride,
+                              c_head_stride, cache_scales ? cache_scales[i] : nullptr, block_ids,
+                              num_ids, block_size, Hkv, D, num_blocks, q, scale);
+    if (rc != COOPT_OK) return rc;
+  }
+  if (num_caches == 0 || num_ids == 0) return COOPT_OK;
+  coopt::clear_error();
+  return swap_caches(false, bits, cache_dtype, num_caches,
+                     reinterpret_cast<const void* const*>(caches),
+                     reinterpret_cast<const void* const*>(cache_scales),
+                     c_blk_stride, c_tok_stride, c_head_stride, s_blk_stride, s_tok_stride,
+                     s_head_stride, block_ids, num_ids, block_size, Hkv, D, num_blocks,
+                     const_cast<void*>(q), const_cast<void*>(scale),
+                     static_cast<hipStream_t>(stream));
 }

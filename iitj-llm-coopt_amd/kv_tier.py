@@ -23,7 +23,8 @@ import torch
 
 from . import _lib
 
-__all__ = ["SwappedKV", "KVTierManager", "swap_out_blocks", "swap_in_blocks"]
+__all__ = ["SwappedKV", "KVTierManager", "swap_out_blocks", "swap_in_blocks", "swap_out_caches",
+           "swap_in_caches"]
 
 
 @dataclass
@@ -115,6 +116,98 @@ def swap_in_blocks(q, scale, bits: int, block_ids, cache, cache_scale=None):
     return cache
 
 
+def _uniform_caches(caches, scales):
+    """(dtype code, cache strides, scale strides) shared by every cache, or None."""
+    c0 = caches[0]
+    for c, sc in zip(caches, scales):
+        _check_cache(c, sc)
+        if c.shape != c0.shape or c.stride() != c0.stride() or c.dtype != c0.dtype or c.device != c0.device:
+            return None
+    code = _cache_code(c0)
+    ss = (0, 0, 0)
+    if code == _lib.DT_I8:
+        s0 = scales[0]
+        if any(sc.stride() != s0.stride() for sc in scales):
+            return None
+        ss = s0.stride()
+    return code, c0.stride(), ss
+
+
+def _pointer_array(ts):
+    import ctypes
+    arr = (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])
+    return arr, ctypes.addressof(arr)
+
+
+def swap_out_caches(caches, block_ids, bits: int, scales=None, out=None, out_scale=None):
+    """swap_out_blocks over a list of caches of one shape, dtype and strides (the K and V caches
+    of every layer) in one launch -> (q [n, ...], scale [n, ...]); cache i's rows are q[i] and
+    scale[i], bit-identical to swap_out_blocks(caches[i], ...).  Caches that differ in layout
+    are swapped one launch each."""
+    n = len(caches)
+    scales = list(scales) if scales is not None else [None] * n
+    _lib.require_cuda(caches[0], block_ids)
+    ids = block_ids.to(torch.int64).contiguous()
+    nb = ids.numel()
+    qshape, qdtype, sshape = _swap_shapes(caches[0], nb, bits)
+    dev = caches[0].device
+    q = torch.empty((n, *qshape), dtype=qdtype, device=dev) if out is None else out
+    s = None
+    if sshape is not None:
+        s = torch.empty((n, *sshape), dtype=torch.float16, device=dev) if out_scale is None else out_scale
+    if q.shape != (n, *qshape) or not q.is_contiguous() or (s is not None and (s.shape != (n, *sshape) or not s.is_contiguous())):
+        raise ValueError("swap buffers must be contiguous [n, ...] of the swapped shape")
+    uni = _uniform_caches(caches, scales)
+    if uni is None:
+        for i, (c, sc) in enumerate(zip(caches, scales)):
+            swap_out_blocks(c, ids, bits, sc, out=q[i], out_scale=None if s is None else s[i])
+        return q, s
+    code, cs, ss = uni
+    if code == _lib.DT_I8 and bits != 8:
+        raise ValueError("an INT8 cache swaps at 8 bits")
+    carr, cptr = _pointer_array(caches)
+    sarr, sptr = _pointer_array(scales) if code == _lib.DT_I8 else (None, None)
+    _, bs, H, D = caches[0].shape
+    _lib.check(_lib.load().coopt_kv_swap_out_caches(
+        bits, code, n, cptr, sptr, cs[0], cs[1], cs[2], ss[0], ss[1], ss[2], _lib.ptr(ids), nb, bs,
+        H, D, caches[0].shape[0], _lib.ptr(q), _lib.ptr(s), _lib.stream_handle(dev)),
+        "coopt_kv_swap_out_caches")
+    del carr, sarr
+    return q, s
+
+
+def swap_in_caches(q, scale, bits: int, block_ids, caches, scales=None):
+    """swap_in_blocks(q[i], scale[i], ..., caches[i]) for every i, in one launch when the
+    caches share shape, dtype and strides."""
+    n = len(caches)
+    scales = list(scales) if scales is not None else [None] * n
+    _lib.require_cuda(q, caches[0], block_ids)
+    ids = block_ids.to(torch.int64).contiguous()
+    nb = ids.numel()
+    qshape, qdtype, sshape = _swap_shapes(caches[0], nb, bits)
+    if q.shape != (n, *qshape) or q.dtype != qdtype or not q.is_contiguous():
+        raise ValueError(f"q must be contiguous {qdtype} {(n, *qshape)}")
+    if sshape is not None and (scale is None or scale.shape != (n, *sshape) or not scale.is_contiguous()):
+        raise ValueError(f"scale must be contiguous fp16 {(n, *sshape)}")
+    uni = _uniform_caches(caches, scales)
+    if uni is None:
+        for i, (c, sc) in enumerate(zip(caches, scales)):
+            swap_in_blocks(q[i], None if scale is None else scale[i], bits, ids, c, sc)
+        return caches
+    code, cs, ss = uni
+    if code == _lib.DT_I8 and bits != 8:
+        raise ValueError("an INT8 cache swaps at 8 bits")
+    carr, cptr = _pointer_array(caches)
+    sarr, sptr = _pointer_array(scales) if code == _lib.DT_I8 else (None, None)
+    _, bs, H, D = caches[0].shape
+    _lib.check(_lib.load().coopt_kv_swap_in_caches(
+        bits, code, n, _lib.ptr(q), _lib.ptr(scale), _lib.ptr(ids), nb, bs, H, D,
+        caches[0].shape[0], cptr, sptr, cs[0], cs[1], cs[2], ss[0], ss[1], ss[2],
+        _lib.stream_handle(caches[0].device)), "coopt_kv_swap_in_caches")
+    del carr, sarr
+    return caches
+
+
 class KVTierManager:
     def __init__(self, engine, cpu_gb: float = 32.0, bits: int = 8):
         if bits not in (16, 8, 4):
@@ -187,10 +280,11 @@ class KVTierManager:
             # one staging buffer for the whole sequence, one PCIe copy each for codes and scales
             q = torch.empty((L, 2, *qshape), dtype=qdtype, device=dev)
             s = torch.empty((L, 2, *sshape), dtype=torch.float16, device=dev) if sshape else None
-            for li in range(L):
-                for j, (cache, cscale) in enumerate(((kcs[li], kss[li]), (vcs[li], vss[li]))):
-                    swap_out_blocks(cache, blocks, bits, cscale, out=q[li, j],
-                                    out_scale=None if s is None else s[li, j])
+            # every layer's K and V cache in one launch: cache 2 li + j is q[li, j]
+            caches = [c for li in range(L) for c in (kcs[li], vcs[li])]
+            cscales = [c for li in range(L) for c in (kss[li], vss[li])]
+            swap_out_caches(caches, blocks, bits, cscales, out=q.view(2 * L, *qshape),
+                            out_scale=None if s is None else s.view(2 * L, *sshape))
             hq = torch.empty(q.shape, dtype=q.dtype, pin_memory=True)
             hq.copy_(q, non_blocking=True)
             hs = None
@@ -225,8 +319,11 @@ class KVTierManager:
         if base_q is not None and base_q.shape[:2] == (L, 2):
             q = base_q.to(dev, non_blocking=True)
             qs = [(q[li, 0], q[li, 1]) for li in range(L)]
+            qall = q
         else:
             qs = [(sw.k[li].to(dev, non_blocking=True), sw.v[li].to(dev, non_blocking=True)) for li in range(L)]
+            qall = None
+        sall = None
         if sw.bits == 16:
             ss = [(None, None)] * L
         else:
@@ -234,12 +331,21 @@ class KVTierManager:
             if base_s is not None and base_s.shape[:2] == (L, 2):
                 s = base_s.to(dev, non_blocking=True)
                 ss = [(s[li, 0], s[li, 1]) for li in range(L)]
+                sall = s
             else:
                 ss = [(sw.k_scale[li].to(dev, non_blocking=True), sw.v_scale[li].to(dev, non_blocking=True))
                       for li in range(L)]
-        for li in range(L):
-            swap_in_blocks(qs[li][0], ss[li][0], sw.bits, blocks, kcs[li], kss[li])
-            swap_in_blocks(qs[li][1], ss[li][1], sw.bits, blocks, vcs[li], vss[li])
+        if qall is not None and (sw.bits == 16 or sall is not None):
+            # every layer's K and V cache in one launch
+            caches = [c for li in range(L) for c in (kcs[li], vcs[li])]
+            cscales = [c for li in range(L) for c in (kss[li], vss[li])]
+            swap_in_caches(qall.view(2 * L, *qall.shape[2:]),
+                           None if sw.bits == 16 else sall.view(2 * L, *sall.shape[2:]),
+                           sw.bits, blocks, caches, cscales)
+        else:
+            for li in range(L):
+                swap_in_blocks(qs[li][0], ss[li][0], sw.bits, blocks, kcs[li], kss[li])
+                swap_in_blocks(qs[li][1], ss[li][1], sw.bits, blocks, vcs[li], vss[li])
         self.used -= sw.nbytes
         self.bytes_in += sw.nbytes
         self.restores += 1

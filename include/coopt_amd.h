@@ -26,6 +26,8 @@
  *   coopt_dequantize        dequantize
  *   coopt_kv_swap_out /     quantize(cache[blocks], bits) / engine/kv_tier_manager.py:93-101
  *   coopt_kv_swap_in        cache[blocks] = dequantize(..)  engine/kv_tier_manager.py:113-119
+ *   coopt_kv_swap_*_caches  the same over every layer's K   engine/kv_tier_manager.py:93-101,
+ *                           and V cache in one launch       113-119 (the per-layer loops)
  *   coopt_qkv_epilogue      split + rotary_embedding +      engine/model.py:238-243
  *                           reshape_and_cache_flash
  *   coopt_kv_copy_blocks    buf[dst].copy_(buf[src]) per    engine/elastic.py:131 via
@@ -161,6 +163,29 @@ int coopt_kv_swap_in(int bits, int cache_dtype, const void* q, const void* scale
                      int64_t num_blocks, void* cache, int64_t c_blk_stride, int64_t c_tok_stride,
                      int64_t c_head_stride, void* cache_scale, int64_t s_blk_stride,
                      int64_t s_tok_stride, int64_t s_head_stride, coopt_stream_t stream);
+
+/*
+ * The same swap for num_caches caches of one shape, dtype and strides -- the K and V caches
+ * of every layer, which engine/kv_tier_manager.py:93-101 / 113-119 quantize / restore one
+ * tensor at a time -- in one launch per 64 caches.  caches / cache_scales are host arrays of
+ * device pointers (cache_scales NULL for bf16 caches); cache i swaps with the rows at
+ * q + i * (num_ids * block_size * Hkv * D' * code bytes) and scale + i * num_ids * block_size
+ * * Hkv, i.e. q / scale are contiguous [num_caches, num_ids, block_size, Hkv, D'] and
+ * [num_caches, num_ids, block_size, Hkv].  Results are those of num_caches single calls.
+ */
+int coopt_kv_swap_out_caches(int bits, int cache_dtype, int num_caches, const void* const* caches,
+                             const void* const* cache_scales, int64_t c_blk_stride,
+                             int64_t c_tok_stride, int64_t c_head_stride, int64_t s_blk_stride,
+                             int64_t s_tok_stride, int64_t s_head_stride,
+                             const int64_t* block_ids, int num_ids, int block_size, int Hkv,
+                             int D, int64_t num_blocks, void* q, void* scale,
+                             coopt_stream_t stream);
+int coopt_kv_swap_in_caches(int bits, int cache_dtype, int num_caches, const void* q,
+                            const void* scale, const int64_t* block_ids, int num_ids,
+                            int block_size, int Hkv, int D, int64_t num_blocks,
+                            void* const* caches, void* const* cache_scales, int64_t c_blk_stride,
+                            int64_t c_tok_stride, int64_t c_head_stride, int64_t s_blk_stride,
+                            int64_t s_tok_stride, int64_t s_head_stride, coopt_stream_t stream);
 
 /*
  * Block migration copy: for every pair i, block dst_ids[i] <- block src_ids[i] in every

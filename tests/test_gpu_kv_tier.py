@@ -165,3 +165,52 @@ def test_tier_manager_refuses_when_full_and_drops(dev):
     assert tm.swap_out(_Seq(5, 200))
     tm.drop(5)
     assert tm.used == 0 and not tm.has(5)
+
+
+@pytest.mark.parametrize("kv,bits", [("auto", 16), ("auto", 8), ("auto", 4), ("int8", 8)])
+@pytest.mark.parametrize("n", [2, 70])   # 70 caches take two launches (64 per launch)
+def test_multi_cache_swap_equals_per_cache_swaps(dev, kv, bits, n):
+    """swap_out_caches / swap_in_caches over n caches of one layout == n single-cache calls,
+    bit for bit, both directions; ids outside the pool read as zero and are skipped."""
+    NB, BS, H, D = 24, 16, 4, 64
+    caches, scales = [], []
+    for i in range(n):
+        kc, _, ks, _ = M.allocate_kv_cache(NB, BS, H, D, kv, device=dev)
+        x = kv_values((NB * BS, H, D), dev, seed=100 + i)
+        M.reshape_and_cache_flash(x, x, kc, kc.clone(), torch.arange(NB * BS, device=dev), kv, ks,
+                                  None if ks is None else ks.clone())
+        caches.append(kc)
+        scales.append(ks)
+    ids = torch.tensor([5, 0, 23, -1, 7, 40], device=dev)
+    q, s = M.swap_out_caches(caches, ids, bits, scales)
+    for i in range(n):
+        qi, si = M.swap_out_blocks(caches[i], ids, bits, scales[i])
+        assert torch.equal(q[i], qi), i
+        if si is not None:
+            assert torch.equal(s[i], si), i
+    # restore into fresh caches, then compare with single-cache restores
+    fresh = [M.allocate_kv_cache(NB, BS, H, D, kv, device=dev) for _ in range(n)]
+    tgt = [f[0] for f in fresh]
+    tsc = [f[2] for f in fresh]
+    dst = torch.tensor([1, 2, 3, -1, 4, 99], device=dev)
+    M.swap_in_caches(q, s, bits, dst, tgt, tsc)
+    for i in range(n):
+        one, _, one_s, _ = M.allocate_kv_cache(NB, BS, H, D, kv, device=dev)
+        M.swap_in_blocks(q[i], None if s is None else s[i], bits, dst, one, one_s)
+        assert torch.equal(tgt[i].view(torch.uint8), one.view(torch.uint8)), i
+        if one_s is not None:
+            assert torch.equal(tsc[i], one_s), i
+
+
+def test_multi_cache_swap_falls_back_on_mixed_layouts(dev):
+    """A token-major cache among head-major ones: one launch per cache, same results."""
+    NB, BS, H, D = 8, 16, 2, 64
+    a, _, _, _ = M.allocate_kv_cache(NB, BS, H, D, "auto", device=dev)
+    b = torch.zeros(NB, BS, H, D, dtype=torch.bfloat16, device=dev)   # token-major
+    for i, c in enumerate((a, b)):
+        c.copy_(kv_values((NB, BS, H, D), dev, seed=7 + i))
+    ids = torch.tensor([3, 1], device=dev)
+    q, s = M.swap_out_caches([a, b], ids, 8)
+    for i, c in enumerate((a, b)):
+        qi, si = M.swap_out_blocks(c, ids, 8)
+        assert torch.equal(q[i], qi) and torch.equal(s[i], si)
