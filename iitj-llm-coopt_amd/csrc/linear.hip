@@ -4,8 +4,9 @@
 // 248, 250, 253: qkv, o, gate_up, down) and the logits projection.
 //
 // At these row counts the layer is a stream over W (2 bytes per weight, read once) with
-// intensity 2M flop/byte, under the bf16 MFMA ridge (~310 flop/byte) up to M = 155; the
-// library GEMMs pick square macro tiles and leave most CUs idle on N = 4096 outputs.
+// intensity M flop per weight byte (2M per weight), under the bf16 MFMA ridge (~310 flop/byte)
+// for every M <= 256; the library GEMMs pick square macro tiles and leave most CUs idle on
+// N = 4096 outputs.
 //
 // Decomposition.  A workgroup of WAVES waves owns WAVES * NW 16-column tiles of the output
 // and a K range of `kt` elements; gridDim.y workgroups split K, and when it exceeds one they
