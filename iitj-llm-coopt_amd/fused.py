@@ -5,6 +5,7 @@ Counterparts of the vLLM ops the reference's forward calls (engine/model.py:234-
   rope_(q, k, positions, cos, sin)                     _ops.rotary_embedding (neox, in place)
   silu_and_mul(gate_up, out=None)                      torch.ops._C.silu_and_mul
   linear(x, weight, out=None)                          F.linear projections (model.py:238-253)
+  pack_linear_weight(weight)                           the weight in tile-packed form, for linear
 """
 import ctypes
 
@@ -13,7 +14,8 @@ import torch.nn.functional as F
 
 from . import _lib
 
-__all__ = ["rms_norm", "rope_", "silu_and_mul", "linear", "LinearPartials", "LINEAR_MAX_ROWS"]
+__all__ = ["rms_norm", "rope_", "silu_and_mul", "linear", "LinearPartials", "LINEAR_MAX_ROWS",
+           "PackedWeight", "pack_linear_weight", "row_major"]
 
 LINEAR_MAX_ROWS = 256
 _WS = _lib.WorkspaceCache()
@@ -127,6 +129,49 @@ def silu_and_mul(gate_up, out=None):
     return out
 
 
+class PackedWeight:
+    """A projection weight [N, K] kept twice: row-major (`weight`, for torch's GEMM at
+    prefill-sized row counts) and tile-packed (`packed`, coopt_linear_pack_weight's layout, for
+    the weight-streaming kernel).  linear() picks the copy its path reads; both give the same
+    result bit for bit on the kernel path."""
+
+    def __init__(self, weight, packed):
+        self.weight, self.packed = weight, packed
+
+    @property
+    def shape(self):
+        return self.weight.shape
+
+    @property
+    def dtype(self):
+        return self.weight.dtype
+
+    @property
+    def device(self):
+        return self.weight.device
+
+
+def row_major(weight):
+    """The row-major [N, K] tensor of a weight (a PackedWeight's first copy, else itself)."""
+    return weight.weight if isinstance(weight, PackedWeight) else weight
+
+
+def pack_linear_weight(weight):
+    """PackedWeight of a bf16 [N, K] weight on the GPU (N a multiple of 16, K of 128): one
+    coopt_linear_pack_weight launch at model load."""
+    _lib.require_cuda(weight)
+    if weight.dtype != torch.bfloat16 or weight.dim() != 2 or weight.stride(-1) != 1:
+        raise ValueError("weight must be a bf16 [N, K] matrix with contiguous rows")
+    N, K = weight.shape
+    if N % 16 or K % 128:
+        raise ValueError("packing needs N a multiple of 16 and K a multiple of 128")
+    packed = torch.empty(N * K, dtype=torch.bfloat16, device=weight.device)
+    _lib.check(_lib.load().coopt_linear_pack_weight(
+        _lib.ptr(weight), weight.stride(0), N, K, _lib.ptr(packed),
+        _lib.stream_handle(weight.device)), "coopt_linear_pack_weight")
+    return PackedWeight(weight, packed)
+
+
 def linear(x, weight, out=None, defer_reduce=False):
     """x [..., K] @ weight[N, K]^T -> [..., N], bf16 with fp32 accumulation (no bias), as the
     reference's projections (F.linear at engine/model.py:238, 248, 250, 253).
@@ -139,7 +184,13 @@ def linear(x, weight, out=None, defer_reduce=False):
 
     defer_reduce=True (no `out`): on the kernel path, return a LinearPartials instead of the
     tensor, for rms_norm() or silu_and_mul() to reduce in their own pass; other paths return
-    the tensor."""
+    the tensor.
+
+    `weight` may be a PackedWeight: the kernel path then streams its tile-packed copy
+    (coopt_linear_packed), torch's path its row-major one."""
+    packed = weight.packed if isinstance(weight, PackedWeight) else None
+    if packed is not None:
+        weight = weight.weight
     _lib.require_cuda(x, weight, out)
     K = x.shape[-1]
     N = weight.shape[0]
@@ -149,25 +200,38 @@ def linear(x, weight, out=None, defer_reduce=False):
             or weight.dtype != torch.bfloat16 or weight.dim() != 2 or weight.shape[1] != K
             or (M > 64 and N > 8192)):
         return F.linear(x, weight, out=out) if out is not None else F.linear(x, weight)
-    if x2.stride(-1) != 1 or x2.stride(0) % 8 or weight.stride(-1) != 1 or weight.stride(0) % 8:
+    if x2.stride(-1) != 1 or x2.stride(0) % 8:
         x2 = x2.contiguous()
+    if packed is None and (weight.stride(-1) != 1 or weight.stride(0) % 8):
         weight = weight.contiguous()
+    lib = _lib.load()
     if defer_reduce and out is None:
         ks, rp = ctypes.c_int(0), ctypes.c_int(0)
-        _lib.check(_lib.load().coopt_linear_split(M, N, K, ctypes.byref(ks), ctypes.byref(rp)),
+        _lib.check(lib.coopt_linear_split(M, N, K, ctypes.byref(ks), ctypes.byref(rp)),
                    "coopt_linear_split")
         ws = _WS.get(ks.value * rp.value * N * 4, x.device)
-        _lib.check(_lib.load().coopt_linear_partials(
-            _lib.ptr(x2), x2.stride(0), _lib.ptr(weight), weight.stride(0), M, N, K, _lib.ptr(ws),
-            ws.numel(), _lib.stream_handle(x.device)), "coopt_linear_partials")
+        if packed is None:
+            _lib.check(lib.coopt_linear_partials(
+                _lib.ptr(x2), x2.stride(0), _lib.ptr(weight), weight.stride(0), M, N, K,
+                _lib.ptr(ws), ws.numel(), _lib.stream_handle(x.device)), "coopt_linear_partials")
+        else:
+            _lib.check(lib.coopt_linear_partials_packed(
+                _lib.ptr(x2), x2.stride(0), _lib.ptr(packed), M, N, K, _lib.ptr(ws), ws.numel(),
+                _lib.stream_handle(x.device)), "coopt_linear_partials_packed")
         return LinearPartials(ws, ks.value, M, rp.value, N, x.shape[:-1] + (N,), x.device)
     if out is None:
         out = torch.empty(x.shape[:-1] + (N,), dtype=torch.bfloat16, device=x.device)
     y2 = out.view(-1, N)
-    need = int(_lib.load().coopt_linear_workspace(M, N, K))
+    need = int(lib.coopt_linear_workspace(M, N, K))
     ws = _WS.get(need, x.device) if need else None
-    _lib.check(_lib.load().coopt_linear(
-        _lib.ptr(x2), x2.stride(0), _lib.ptr(weight), weight.stride(0), M, N, K, _lib.ptr(y2),
-        y2.stride(0), _lib.ptr(ws), 0 if ws is None else ws.numel(),
-        _lib.stream_handle(x.device)), "coopt_linear")
+    if packed is None:
+        _lib.check(lib.coopt_linear(
+            _lib.ptr(x2), x2.stride(0), _lib.ptr(weight), weight.stride(0), M, N, K, _lib.ptr(y2),
+            y2.stride(0), _lib.ptr(ws), 0 if ws is None else ws.numel(),
+            _lib.stream_handle(x.device)), "coopt_linear")
+    else:
+        _lib.check(lib.coopt_linear_packed(
+            _lib.ptr(x2), x2.stride(0), _lib.ptr(packed), M, N, K, _lib.ptr(y2), y2.stride(0),
+            _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.stream_handle(x.device)),
+            "coopt_linear_packed")
     return out

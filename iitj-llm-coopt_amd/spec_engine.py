@@ -27,7 +27,7 @@ import torch.nn.functional as F
 
 from . import _lib
 from .attention import paged_attention, workspace_bytes
-from .fused import linear, rms_norm, rope_, silu_and_mul
+from .fused import linear, pack_linear_weight, rms_norm, rope_, row_major, silu_and_mul
 from .kv_cache import allocate_kv_cache, qkv_rope_and_cache, reshape_and_cache_flash
 from .spec_decode import AcceptResult, accept
 
@@ -87,12 +87,26 @@ class RandomLlama:
                 "gate_up": w(2 * shape.ffn, H),
                 "down": w(H, shape.ffn),
             })
+        if self.device.type == "cuda":
+            self._pack()
         inv = 1.0 / (shape.rope_theta ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
         freqs = torch.outer(torch.arange(max_pos, dtype=torch.float32), inv)
         emb = torch.cat((freqs, freqs), dim=-1)           # neox layout, as HF Llama
         self.cos = emb.cos().to(device=self.device, dtype=dtype)
         self.sin = emb.sin().to(device=self.device, dtype=dtype)
         self.scale = 1.0 / math.sqrt(D)
+
+    # Projections that stream through coopt_linear at decode / verify row counts and measured
+    # faster from tile-packed weights on MI355X (gate_up is not: the target's runs on torch's
+    # GEMM, and the draft's wide one measured slower packed).
+    PACKED = ("qkv", "o", "down")
+
+    def _pack(self):
+        for L in self.layers:
+            for k in self.PACKED:
+                N, K = L[k].shape
+                if N % 16 == 0 and K % 128 == 0:  # the packed layout's tile granularity
+                    L[k] = pack_linear_weight(L[k])
 
     def to(self, device):
         """A copy of the weights on another device (same values)."""
@@ -101,7 +115,9 @@ class RandomLlama:
         other.embed = self.embed.to(device)
         other.lm_head = other.embed if self.s.tie_embeddings else self.lm_head.to(device)
         other.norm = self.norm.to(device)
-        other.layers = [{k: v.to(device) for k, v in L.items()} for L in self.layers]
+        other.layers = [{k: row_major(v).to(device) for k, v in L.items()} for L in self.layers]
+        if other.device.type == "cuda":
+            other._pack()
         other.cos, other.sin, other.scale = self.cos.to(device), self.sin.to(device), self.scale
         return other
 
@@ -302,7 +318,7 @@ class SpecDecoder:
         d = None
         for li, L in enumerate(model.layers):
             h = self.ops.rms_norm(x if d is None else d, None if d is None else x, L["ln1"], s.eps)
-            qkv = F.linear(h, L["qkv"])
+            qkv = F.linear(h, row_major(L["qkv"]))
             q = qkv[:, : H * D].view(T, H, D)
             k = qkv[:, H * D: (H + Hkv) * D].view(T, Hkv, D)
             v = qkv[:, (H + Hkv) * D:].view(T, Hkv, D)
@@ -315,9 +331,9 @@ class SpecDecoder:
             a = F.scaled_dot_product_attention(qf.contiguous(), kf.contiguous(), vf.contiguous(),
                                                is_causal=True, scale=model.scale)
             attn = a.transpose(1, 2).reshape(T, H * D).to(x.dtype)
-            o = F.linear(attn, L["o"])
+            o = F.linear(attn, row_major(L["o"]))
             h = self.ops.rms_norm(o, x, L["ln2"], s.eps)
-            d = F.linear(self.ops.silu_mul(F.linear(h, L["gate_up"])), L["down"])
+            d = F.linear(self.ops.silu_mul(F.linear(h, L["gate_up"])), row_major(L["down"]))
         last_d = d.view(B, P, -1)[:, -1].contiguous()
         last_x = x.view(B, P, -1)[:, -1].contiguous()
         h = self.ops.rms_norm(last_d, last_x, model.norm, s.eps)

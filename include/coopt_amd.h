@@ -38,6 +38,7 @@
  *   coopt_silu_mul          vLLM silu_and_mul               engine/model.py:251-252
  *   coopt_linear            F.linear projections at decode  engine/model.py:238, 248, 250,
  *                           / verify row counts             253 (qkv, o, gate_up, down)
+ *   coopt_linear_*packed    the same, tile-packed weights   engine/model.py:238, 248, 253
  */
 #ifndef COOPT_AMD_H
 #define COOPT_AMD_H
@@ -342,6 +343,24 @@ int coopt_linear_partials(const void* x, int64_t ldx, const void* w, int64_t ldw
 int coopt_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, int N, int K,
                  void* y, int64_t ldy, void* workspace, size_t workspace_bytes,
                  coopt_stream_t stream);
+/*
+ * The same projections with the weight in tile-packed form, written once at model load by
+ * coopt_linear_pack_weight (a layout for the MI355X memory system; the reference keeps F.linear's
+ * row-major [N, K] weight, engine/model.py:238, 248, 253, which is the input here).
+ *   coopt_linear_pack_weight: out (N * K bf16, 16-byte aligned) = w [N, K] (row stride ldw)
+ *     as [N/16][K/128] tiles of 16 rows x 128 K; in tile (t, u), 16-byte chunk j * 64 + l holds
+ *     w[16 t + l % 16][128 u + 32 j + 8 (l / 16), +8).  N a multiple of 16, K of 128.
+ *   coopt_linear_packed / coopt_linear_partials_packed: coopt_linear / coopt_linear_partials
+ *     with w_packed in place of (w, ldw); same plan, workspace and split, results bit-identical.
+ */
+int coopt_linear_pack_weight(const void* w, int64_t ldw, int N, int K, void* out,
+                             coopt_stream_t stream);
+int coopt_linear_packed(const void* x, int64_t ldx, const void* w_packed, int M, int N, int K,
+                        void* y, int64_t ldy, void* workspace, size_t workspace_bytes,
+                        coopt_stream_t stream);
+int coopt_linear_partials_packed(const void* x, int64_t ldx, const void* w_packed, int M, int N,
+                                 int K, void* workspace, size_t workspace_bytes,
+                                 coopt_stream_t stream);
 
 #ifdef __cplusplus
 }

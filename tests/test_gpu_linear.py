@@ -148,3 +148,74 @@ def test_deferred_reduction_into_silu_mul_is_bit_exact(dev, M, F, K):
     part = fused.linear(x, w, defer_reduce=True)
     print(f"[defer silu] M={M} F={F} K={K}: {part.ks} slice(s)", flush=True)
     assert torch.equal(fused.silu_and_mul(part), want)
+
+
+# ---- tile-packed weights (coopt_linear_pack_weight, coopt_linear_packed) ----
+
+def packed_layout(w):
+    """The documented packed layout as torch views: tile (t, u) of 16 rows x 128 K, 16-byte
+    chunk j * 64 + l = w[16 t + l % 16][128 u + 32 j + 8 (l // 16), +8)."""
+    N, K = w.shape
+    return w.reshape(N // 16, 16, K // 128, 4, 4, 8).permute(0, 2, 3, 4, 1, 5).reshape(-1)
+
+
+@pytest.mark.parametrize("N,K,pad", [(16, 128, 0), (48, 256, 0), (4096, 4096, 0), (96, 384, 64)])
+def test_pack_weight_layout(dev, N, K, pad):
+    g = torch.Generator(device=dev).manual_seed(N + K + pad)
+    wb = torch.randn(N, K + pad, generator=g, device=dev).to(torch.bfloat16)
+    w = wb[:, :K]                                         # row stride K + pad
+    p = fused.pack_linear_weight(w)
+    torch.cuda.synchronize()
+    assert p.packed.numel() == N * K
+    assert torch.equal(p.packed.view(torch.int16), packed_layout(w.contiguous()).view(torch.int16))
+    # one spot by hand: tile (1, 0), chunk j = 2, lane 37 -> row 16 + 5, K 64 + 16
+    if N >= 32:
+        off = ((1 * (K // 128) + 0) * 256 + 2 * 64 + 37) * 8
+        assert torch.equal(p.packed[off:off + 8], w[21, 80:88])
+
+
+# shapes of every launch plan: 160 rows (10 row tiles, split K), the draft's 32 / 64 rows,
+# the 4-tile-per-wave lm_head plan, a K split 7 ways, tails in M, one row
+@pytest.mark.parametrize("M,N,K", [
+    (160, 6144, 4096), (160, 4096, 14336), (160, 4096, 4352), (32, 3072, 2048), (64, 2048, 8192),
+    (32, 128256, 2048), (1, 256, 128), (17, 96, 384), (200, 64, 640), (256, 528, 1152),
+])
+def test_packed_linear_is_bit_identical_to_row_major(dev, M, N, K):
+    g = torch.Generator(device=dev).manual_seed(M * 3 + N + K)
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    pw = fused.pack_linear_weight(w)
+    y = fused.linear(x, w)
+    yp = fused.linear(x, pw)
+    print(f"[packed] M={M} N={N} K={K}", flush=True)
+    assert torch.equal(yp.view(torch.int16), y.view(torch.int16))
+    check(yp, x, w, f"packed {M}x{N}x{K}")
+    part = fused.linear(x, w, defer_reduce=True)
+    n = part.ks * part.rows_padded * part.n * 4
+    want = part.buf[:n].clone()
+    part_p = fused.linear(x, pw, defer_reduce=True)
+    assert (part_p.ks, part_p.rows_padded) == (part.ks, part.rows_padded)
+    assert torch.equal(part_p.buf[:n], want)
+
+
+def test_packed_weight_on_the_torch_path(dev):
+    """Row counts above the kernel's range use the PackedWeight's row-major copy."""
+    g = torch.Generator(device=dev).manual_seed(9)
+    x = torch.randn(300, 256, generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn(64, 256, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    assert torch.equal(fused.linear(x, fused.pack_linear_weight(w)), F.linear(x, w))
+
+
+def test_pack_weight_errors(dev):
+    w = torch.randn(40, 128, device=dev).to(torch.bfloat16)
+    with pytest.raises(ValueError):
+        fused.pack_linear_weight(w)
+    out = torch.empty(40 * 128, device=dev, dtype=torch.bfloat16)
+    L = _lib.load()
+    assert L.coopt_linear_pack_weight(_lib.ptr(w), 128, 40, 128, _lib.ptr(out), _lib.stream_handle(dev)) != 0
+    assert "multiple of 16" in _lib.last_error()
+    x = torch.randn(4, 128, device=dev).to(torch.bfloat16)
+    y = torch.empty(4, 40, device=dev, dtype=torch.bfloat16)
+    assert L.coopt_linear_packed(_lib.ptr(x), 128, _lib.ptr(out), 4, 40, 128, _lib.ptr(y), 40, None, 0,
+                                 _lib.stream_handle(dev)) != 0
+    assert "multiple of 16" in _lib.last_error()
