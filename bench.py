@@ -303,19 +303,22 @@ def migrate_case(torch, M, dev, seed, pairs=256):
     return res
 
 
-def linear_case(torch, M, dev, rows, n, k, seed):
-    """One projection of the step through fused.linear (coopt_linear: split-K partials plus
-    the reduction launch at these shapes): x [rows, k] @ w[n, k]^T, bf16, N(0,1) x, N(0, 0.02^2)
+def linear_case(torch, M, dev, rows, n, k, seed, packed=False):
+    """One projection of the step through fused.linear (coopt_linear, or coopt_linear_packed
+    with the tile-packed weight the step's qkv / o / down use: split-K partials plus the
+    reduction launch at these shapes): x [rows, k] @ w[n, k]^T, bf16, N(0,1) x, N(0, 0.02^2)
     weights.  Algorithmic bytes: the weight, x and y once each."""
     g = torch.Generator(device=dev).manual_seed(seed)
     x = torch.randn(rows, k, generator=g, device=dev).to(torch.bfloat16)
     w = (torch.randn(n, k, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    if packed:
+        w = M.fused.pack_linear_weight(w)
     y = torch.empty(rows, n, dtype=torch.bfloat16, device=dev)
 
     def fn():
         M.fused.linear(x, w, out=y)
 
-    res = rate({"rows": rows, "n": n, "k": k, "flops": 2 * rows * n * k},
+    res = rate({"rows": rows, "n": n, "k": k, "packed_weight": packed, "flops": 2 * rows * n * k},
                n * k * 2 + rows * k * 2 + rows * n * 2, *time_launches(torch, dev, fn))
     res["TFLOP_s"] = 2 * rows * n * k / (res["avg_us"] * 1e-6) / 1e12
     return res
@@ -367,9 +370,10 @@ KERNEL_CASES = {
     "kv_tier_roundtrip": lambda t, M, d, s: kv_tier_case(t, M, d, s),
     "kv_migrate_256x2MiB": lambda t, M, d, s: migrate_case(t, M, d, s),
     # the step's weight-streaming projections: target qkv / down at the verify rows
-    # (B (gamma+1) = 160), draft lm_head at the draft rows (B = 32)
-    "linear_m160_qkv": lambda t, M, d, s: linear_case(t, M, d, 160, 6144, 4096, s),
-    "linear_m160_down": lambda t, M, d, s: linear_case(t, M, d, 160, 4096, 14336, s),
+    # (B (gamma+1) = 160, tile-packed weights as in the step), draft lm_head (row-major) at
+    # the draft rows (B = 32)
+    "linear_m160_qkv": lambda t, M, d, s: linear_case(t, M, d, 160, 6144, 4096, s, packed=True),
+    "linear_m160_down": lambda t, M, d, s: linear_case(t, M, d, 160, 4096, 14336, s, packed=True),
     "linear_m32_lm_head": lambda t, M, d, s: linear_case(t, M, d, 32, 128256, 2048, s),
     "copy": lambda t, M, d, s: copy_case(t, M, d, s),
 }
