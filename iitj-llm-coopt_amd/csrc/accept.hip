@@ -431,6 +431,42 @@ struct WeightRow {
 #pragma unroll
     for (int e = 0; e < 8; ++e) w[e] = fmaxf(p[e] - q[e], 0.0f);
   }
+
+  // at() for a full vectorised group (j + 8 <= V) in two halves: load() issues the group's
+  // loads and finish() forms w and p from them with at()'s arithmetic, so a caller can have
+  // several groups' loads in flight before the first use.
+  struct Raw {
+    float xt[8], xq[8];
+  };
+  __device__ __forceinline__ void load(int j, Raw& r) const {
+    ld8<BF16>(a->tgt, trow, a->tgt_stride, j, r.xt);
+    if (mode == kModeBonus) return;
+    if (a->draft_probs) {
+      const float4* qp = reinterpret_cast<const float4*>(static_cast<const float*>(a->drf) + drow * a->drf_stride + j);
+      const float4 q0 = qp[0], q1 = qp[1];
+      r.xq[0] = q0.x; r.xq[1] = q0.y; r.xq[2] = q0.z; r.xq[3] = q0.w;
+      r.xq[4] = q1.x; r.xq[5] = q1.y; r.xq[6] = q1.z; r.xq[7] = q1.w;
+    } else {
+      ld8<BF16>(a->drf, drow, a->drf_stride, j, r.xq);
+    }
+  }
+  __device__ __forceinline__ void finish(const Raw& r, float* w, float* p) const {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      p[e] = static_cast<float>(static_cast<double>(exp_shift(r.xt[e] * a->inv_t, mt_l2)) * inv_st);
+    if (mode == kModeBonus) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) w[e] = p[e];
+      return;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float q = a->draft_probs
+                          ? r.xq[e]
+                          : static_cast<float>(static_cast<double>(exp_shift(r.xq[e] * a->inv_t, mq_l2)) * inv_sq);
+      w[e] = fmaxf(p[e] - q, 0.0f);
+    }
+  }
 };
 
 template <bool BF16>
@@ -525,10 +561,7 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(Args a) {
   const int hi = min(a.V, lo + a.L.chunk2);
   const bool vec = a.vec_t && (dec.mode == kModeBonus || a.vec_d);
   double sw = 0.0, sp = 0.0;
-  for (int j = lo + tid * 8; j < hi; j += kThreads * 8) {
-    float w[8], p[8];
-    const int n = min(8, hi - j);
-    wr.at(j, n, vec && n == 8, w, p);
+  auto add = [&](const float* w, const float* p, int n) {
     float fw = 0.0f, fp = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -539,6 +572,35 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(Args a) {
     }
     sw += static_cast<double>(fw);
     sp += static_cast<double>(fp);
+  };
+  // Two groups per pass, in the order of a one-group loop.  When both are full the second
+  // group's loads are issued before the first group is used (its index falls back to the
+  // first group's past the chunk end, so the load is unconditional and in bounds).
+  constexpr int kStep = kThreads * 8;
+  for (int j = lo + tid * 8; j < hi; j += 2 * kStep) {
+    const int j1 = j + kStep;
+    const bool has1 = j1 < hi;
+    float w[8], p[8];
+    if (vec && hi - j >= 8 && (!has1 || hi - j1 >= 8)) {
+      typename WeightRow<BF16>::Raw r0, r1;
+      wr.load(j, r0);
+      wr.load(has1 ? j1 : j, r1);
+      wr.finish(r0, w, p);
+      add(w, p, 8);
+      if (has1) {
+        wr.finish(r1, w, p);
+        add(w, p, 8);
+      }
+    } else {
+      const int n = min(8, hi - j);
+      wr.at(j, n, vec && n == 8, w, p);
+      add(w, p, n);
+      if (has1) {
+        const int n1 = min(8, hi - j1);
+        wr.at(j1, n1, vec && n1 == 8, w, p);
+        add(w, p, n1);
+      }
+    }
   }
   sw = block_sum(sw, shd);
   sp = block_sum(sp, shd2);
@@ -630,19 +692,44 @@ __global__ __launch_bounds__(kThreads) void select_kernel(Args a) {
   constexpr int kKeep = 4;
   float keep[kKeep][8];
   double local = 0.0;
+  if (vec && ((thi - tlo) & 7) == 0 && chi - clo >= 8) {
+    // every group of the run is full: all kKeep groups' loads first (groups past the run
+    // reload the chunk's first group, in bounds and never used), then the same sums
+    typename WeightRow<BF16>::Raw r[kKeep];
 #pragma unroll
-  for (int gi = 0; gi < kKeep; ++gi) {
-    const int j = tlo + gi * 8;
+    for (int gi = 0; gi < kKeep; ++gi) {
+      const int j = tlo + gi * 8;
+      wr.load(j < thi ? j : clo, r[gi]);
+    }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) keep[gi][e] = 0.0f;
-    if (j < thi) {
-      float w[8], p[8];
-      const int n = min(8, thi - j);
-      wr.at(j, n, vec && n == 8, w, p);
+    for (int gi = 0; gi < kKeep; ++gi) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        keep[gi][e] = e < n ? (use_p ? p[e] : w[e]) : 0.0f;
-        local += static_cast<double>(keep[gi][e]);
+      for (int e = 0; e < 8; ++e) keep[gi][e] = 0.0f;
+      if (tlo + gi * 8 < thi) {
+        float w[8], p[8];
+        wr.finish(r[gi], w, p);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          keep[gi][e] = use_p ? p[e] : w[e];
+          local += static_cast<double>(keep[gi][e]);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int gi = 0; gi < kKeep; ++gi) {
+      const int j = tlo + gi * 8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) keep[gi][e] = 0.0f;
+      if (j < thi) {
+        float w[8], p[8];
+        const int n = min(8, thi - j);
+        wr.at(j, n, vec && n == 8, w, p);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          keep[gi][e] = e < n ? (use_p ? p[e] : w[e]) : 0.0f;
+          local += static_cast<double>(keep[gi][e]);
+        }
       }
     }
   }
