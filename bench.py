@@ -62,7 +62,7 @@ def parse():
 
 def head_start(torch, dev):
     """Queues ~10 ms of GPU work so the host enqueues the timed launches ahead of the GPU and
-    per-launch events bracket kernel time, not host latency."""
+    the events bracket kernel time, not host latency."""
     a = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16)
     for _ in range(8):
         a = a @ a * 1e-3
@@ -70,10 +70,22 @@ def head_start(torch, dev):
 
 
 def time_launches(torch, dev, fn, n=40):
-    """Average duration of fn() over n launches, each bracketed by HIP events."""
+    """(average, median) duration of fn().  The average is n back-to-back calls between two
+    HIP events divided by n: the sustained per-call time, launch gaps included, which is what
+    a kernel-trace average plus the gap between kernels measures.  The median is over n calls
+    each bracketed by its own pair of events (each pair's marker packets add a little)."""
     for _ in range(3):
         fn()
     torch.cuda.synchronize(dev)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    keep = head_start(torch, dev)
+    t0.record()
+    for _ in range(n):
+        fn()
+    t1.record()
+    torch.cuda.synchronize(dev)
+    del keep
+    avg = t0.elapsed_time(t1) * 1e-3 / n
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
     keep = head_start(torch, dev)
     for s, e in ev:
@@ -83,7 +95,7 @@ def time_launches(torch, dev, fn, n=40):
     torch.cuda.synchronize(dev)
     del keep
     d = sorted(s.elapsed_time(e) * 1e-3 for s, e in ev)
-    return sum(d) / n, d[n // 2]
+    return avg, d[n // 2]
 
 
 def rate(res, nbytes, avg, med):
