@@ -256,13 +256,15 @@ int m_tiles(int M) {
 }
 
 // Launch shape (measured on MI355X over the decode / verify projections of an 8B / 1B Llama
-// pair): 8 waves of one 16-column tile each, or 4 waves for N <= 4096 at M <= 64, or 4
-// column tiles per wave for very wide N (lm_head).  K is split in powers of two while the
-// grid stays within 256 workgroups and each keeps at least 4 K steps; every split adds
-// 4 * 16 * MT bytes of fp32 partials per column against 2 * kt bytes of weights.
+// pair, both weight layouts): 8 waves of one 16-column tile each, or 4 waves at M <= 64 below
+// lm_head widths (the draft's 16384-wide gate_up: 15.0 us packed / 18.6 us row-major against
+// 19.0 us with 8 waves and K split twice), or 4 column tiles per wave for very wide N
+// (lm_head).  K is split in powers of two while the grid stays within 256 workgroups and each
+// keeps at least 4 K steps; every split adds 4 * 16 * MT bytes of fp32 partials per column
+// against 2 * kt bytes of weights.
 Plan plan_for(int M, int N, int K) {
   Plan p{m_tiles(M), 1, 8, 1, K};
-  if (p.mt <= 4 && N <= 4096) p.waves = 4;
+  if (p.mt <= 4 && N < 65536) p.waves = 4;
   if (p.mt <= 4 && N >= 65536) p.nw = 4;
   const int cols = p.waves * p.nw * 16;
   const int nb = (N + cols - 1) / cols;

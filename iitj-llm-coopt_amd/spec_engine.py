@@ -65,8 +65,9 @@ class RandomLlama:
     """Llama decoder with N(0, std^2) weights (unit norms), bf16 on `device`."""
 
     def __init__(self, shape: LlamaShape, device, seed=0, std=0.02, max_pos=8192,
-                 dtype=torch.bfloat16):
+                 dtype=torch.bfloat16, packed=None):
         self.s, self.device, self.dtype = shape, torch.device(device), dtype
+        self.packed = tuple(self.PACKED if packed is None else packed)
         g = torch.Generator(device=self.device).manual_seed(seed)
 
         def w(*size):
@@ -96,14 +97,15 @@ class RandomLlama:
         self.sin = emb.sin().to(device=self.device, dtype=dtype)
         self.scale = 1.0 / math.sqrt(D)
 
-    # Projections that stream through coopt_linear at decode / verify row counts and measured
-    # faster from tile-packed weights on MI355X (gate_up is not: the target's runs on torch's
-    # GEMM, and the draft's wide one measured slower packed).
+    # Projections kept tile-packed as well on the GPU: those that stream through coopt_linear
+    # at verify row counts.  A model run only at draft row counts (<= 64) streams gate_up
+    # through it too and passes packed=("qkv", "o", "gate_up", "down"); the target's gate_up
+    # runs on torch's GEMM at 160 rows, so a packed copy would be unused.
     PACKED = ("qkv", "o", "down")
 
     def _pack(self):
         for L in self.layers:
-            for k in self.PACKED:
+            for k in self.packed:
                 N, K = L[k].shape
                 if N % 16 == 0 and K % 128 == 0:  # the packed layout's tile granularity
                     L[k] = pack_linear_weight(L[k])
@@ -112,6 +114,7 @@ class RandomLlama:
         """A copy of the weights on another device (same values)."""
         other = object.__new__(RandomLlama)
         other.s, other.device, other.dtype = self.s, torch.device(device), self.dtype
+        other.packed = self.packed
         other.embed = self.embed.to(device)
         other.lm_head = other.embed if self.s.tie_embeddings else self.lm_head.to(device)
         other.norm = self.norm.to(device)
@@ -333,7 +336,7 @@ class SpecDecoder:
             attn = a.transpose(1, 2).reshape(T, H * D).to(x.dtype)
             o = F.linear(attn, row_major(L["o"]))
             h = self.ops.rms_norm(o, x, L["ln2"], s.eps)
-            d = F.linear(self.ops.silu_mul(F.linear(h, L["gate_up"])), row_major(L["down"]))
+            d = F.linear(self.ops.silu_mul(F.linear(h, row_major(L["gate_up"]))), row_major(L["down"]))
         last_d = d.view(B, P, -1)[:, -1].contiguous()
         last_x = x.view(B, P, -1)[:, -1].contiguous()
         h = self.ops.rms_norm(last_d, last_x, model.norm, s.eps)
