@@ -608,7 +608,7 @@ def main():
     t0 = time.perf_counter()
     target = RandomLlama(TARGET_LLAMA31_8B, dev, seed=args.seed + 1)
     draft = RandomLlama(DRAFT_LLAMA32_1B, dev, seed=args.seed + 2,
-                        packed=("qkv", "o", "gate_up", "down"))   # runs at 32 / 64 rows only
+                        packed=("qkv", "o", "gate_up", "down", "lm_head"))  # 32 / 64 rows only
     log(f"weights ready in {time.perf_counter() - t0:.1f}s")
     dec = SpecDecoder(target, draft, B, g, P, max_steps=args.warmup + args.steps + 2 + args.cpu_steps,
                       temperature=args.temperature, seed=args.seed)

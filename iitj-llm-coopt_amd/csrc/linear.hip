@@ -439,6 +439,13 @@ int run_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, int M, in
                 "y rows must be 8-byte aligned with stride >= N, a multiple of 4");
   COOPT_REQUIRE(static_cast<int64_t>(N) * ldw < (int64_t(1) << 62), "w too large");
   p = plan_for(M, N, K);
+  if (packed && N >= 65536 && p.mt <= 4 && p.ks == 1) {
+    // lm_head widths from packed weights stream best with one column tile per wave (32 rows:
+    // 98.8 us, 4 waves; 64 rows: 107.1 us, 8 waves; against 107.1 / 119+ us with 4 tiles per
+    // wave).  The split (ks = 1) and so the workspace and partial layout are unchanged.
+    p.nw = 1;
+    p.waves = p.mt <= 2 ? 4 : 8;
+  }
   const size_t need = partials ? static_cast<size_t>(p.ks) * p.mt * 16 * N * sizeof(float)
                                : coopt_linear_workspace(M, N, K);
   COOPT_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr) &&

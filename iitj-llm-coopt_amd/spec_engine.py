@@ -99,16 +99,19 @@ class RandomLlama:
 
     # Projections kept tile-packed as well on the GPU: those that stream through coopt_linear
     # at verify row counts.  A model run only at draft row counts (<= 64) streams gate_up
-    # through it too and passes packed=("qkv", "o", "gate_up", "down"); the target's gate_up
-    # runs on torch's GEMM at 160 rows, so a packed copy would be unused.
+    # through it too, and its logits projection, and passes
+    # packed=("qkv", "o", "gate_up", "down", "lm_head"); the target's gate_up and lm_head run
+    # on torch's GEMM at 160 rows, so packed copies of them would be unused.
     PACKED = ("qkv", "o", "down")
 
     def _pack(self):
+        ok = lambda w: w.shape[0] % 16 == 0 and w.shape[1] % 128 == 0  # the tile granularity
         for L in self.layers:
             for k in self.packed:
-                N, K = L[k].shape
-                if N % 16 == 0 and K % 128 == 0:  # the packed layout's tile granularity
+                if k in L and ok(L[k]):
                     L[k] = pack_linear_weight(L[k])
+        if "lm_head" in self.packed and ok(self.lm_head):
+            self.lm_head = pack_linear_weight(self.lm_head)   # embed keeps the row-major copy
 
     def to(self, device):
         """A copy of the weights on another device (same values)."""
@@ -116,7 +119,7 @@ class RandomLlama:
         other.s, other.device, other.dtype = self.s, torch.device(device), self.dtype
         other.packed = self.packed
         other.embed = self.embed.to(device)
-        other.lm_head = other.embed if self.s.tie_embeddings else self.lm_head.to(device)
+        other.lm_head = other.embed if self.s.tie_embeddings else row_major(self.lm_head).to(device)
         other.norm = self.norm.to(device)
         other.layers = [{k: row_major(v).to(device) for k, v in L.items()} for L in self.layers]
         if other.device.type == "cuda":
@@ -340,7 +343,7 @@ class SpecDecoder:
         last_d = d.view(B, P, -1)[:, -1].contiguous()
         last_x = x.view(B, P, -1)[:, -1].contiguous()
         h = self.ops.rms_norm(last_d, last_x, model.norm, s.eps)
-        return F.linear(h, model.lm_head)
+        return F.linear(h, row_major(model.lm_head))
 
     # ---- one speculative step -------------------------------------------------------------
     def _rows(self, model, kv, start, S, tokens, real, logits_out=None):

@@ -175,10 +175,11 @@ def test_pack_weight_layout(dev, N, K, pad):
 
 
 # shapes of every launch plan: 160 rows (10 row tiles, split K), the draft's 32 / 64 rows,
-# the 4-tile-per-wave lm_head plan, a K split 7 ways, tails in M, one row
+# lm_head widths (4 tiles per wave row-major, 1 packed), a K split 7 ways, tails in M, one row
 @pytest.mark.parametrize("M,N,K", [
     (160, 6144, 4096), (160, 4096, 14336), (160, 4096, 4352), (32, 3072, 2048), (64, 2048, 8192),
-    (32, 128256, 2048), (1, 256, 128), (17, 96, 384), (200, 64, 640), (256, 528, 1152),
+    (32, 128256, 2048), (64, 128256, 2048), (1, 256, 128), (17, 96, 384), (200, 64, 640),
+    (256, 528, 1152),
 ])
 def test_packed_linear_is_bit_identical_to_row_major(dev, M, N, K):
     g = torch.Generator(device=dev).manual_seed(M * 3 + N + K)

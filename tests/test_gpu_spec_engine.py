@@ -27,7 +27,7 @@ def make(dev, B=4, gamma=3, P=24, steps=8, T=1.0, draft_same=False, target_kv="i
          std=0.2):
     t = RandomLlama(TINY_T, dev, seed=seed + 1, std=std)
     d = t if draft_same else RandomLlama(TINY_D, dev, seed=seed + 2, std=std,
-                                         packed=("qkv", "o", "gate_up", "down"))
+                                         packed=("qkv", "o", "gate_up", "down", "lm_head"))
     dec = SpecDecoder(t, d, B, gamma, P, steps, target_kv=target_kv,
                       draft_kv=target_kv if draft_same else "auto", temperature=T, seed=seed)
     g = torch.Generator(device=dev).manual_seed(seed + 3)
