@@ -381,12 +381,11 @@ KERNEL_CASES = {
     "kv_swap_out_4096tok_32layers": lambda t, M, d, s: kv_swap_all_case(t, M, d, s),
     "kv_tier_roundtrip": lambda t, M, d, s: kv_tier_case(t, M, d, s),
     "kv_migrate_256x2MiB": lambda t, M, d, s: migrate_case(t, M, d, s),
-    # the step's weight-streaming projections: target qkv / down at the verify rows
-    # (B (gamma+1) = 160, tile-packed weights as in the step), draft lm_head (row-major) at
-    # the draft rows (B = 32)
+    # the step's weight-streaming projections, tile-packed as in the step: target qkv / down
+    # at the verify rows (B (gamma+1) = 160), draft lm_head at the draft rows (B = 32)
     "linear_m160_qkv": lambda t, M, d, s: linear_case(t, M, d, 160, 6144, 4096, s, packed=True),
     "linear_m160_down": lambda t, M, d, s: linear_case(t, M, d, 160, 4096, 14336, s, packed=True),
-    "linear_m32_lm_head": lambda t, M, d, s: linear_case(t, M, d, 32, 128256, 2048, s),
+    "linear_m32_lm_head": lambda t, M, d, s: linear_case(t, M, d, 32, 128256, 2048, s, packed=True),
     "copy": lambda t, M, d, s: copy_case(t, M, d, s),
 }
 
