@@ -15,9 +15,10 @@ from dataclasses import dataclass
 import numpy as np
 import torch
 
+from . import _lib
 from .block_manager import BlockManager
 
-__all__ = ["WorkItem", "Batch", "build_batch", "build_padded_batch"]
+__all__ = ["WorkItem", "Batch", "build_batch", "build_padded_batch", "row_slots"]
 
 
 @dataclass
@@ -121,3 +122,29 @@ def build_padded_batch(items, bm: BlockManager, stride: int, batch_size: int, wi
         logits_indices=_to(np.arange(T, dtype=np.int64), torch.int64, device),
         max_seqlen_q=S, max_seqlen_k=int(lens.max()) if Bp else 0)
     return batch, spans
+
+
+def row_slots(block_table, start, S: int, block_size: int, n_real=None):
+    """Device-side paged addressing of S rows per sequence at positions start[b] + j
+    (coopt_row_slots): returns positions [B, S] int64, slots [B*S] int64 -- the
+    BlockManager.slot_mapping formula (engine/block_manager.py:216-220), -1 for rows
+    j >= n_real[b] and for positions past the table -- and seq_lens [B] int32 = start + S.
+    block_table [B, W] int32 and start / n_real [B] int64 on the GPU; one launch."""
+    _lib.require_cuda(block_table, start, n_real)
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.stride(-1) != 1:
+        raise ValueError("block_table must be an int32 [B, W] tensor with contiguous rows")
+    B = start.numel()
+    if start.dtype != torch.int64 or not start.is_contiguous() or block_table.shape[0] < B:
+        raise ValueError("start must be a contiguous int64 [B] tensor, B <= block_table rows")
+    if n_real is not None and (n_real.dtype != torch.int64 or not n_real.is_contiguous()
+                               or n_real.numel() != B):
+        raise ValueError("n_real must be a contiguous int64 [B] tensor")
+    dev = start.device
+    pos = torch.empty((B, S), dtype=torch.int64, device=dev)
+    slots = torch.empty(B * S, dtype=torch.int64, device=dev)
+    seq_lens = torch.empty(B, dtype=torch.int32, device=dev)
+    _lib.check(_lib.load().coopt_row_slots(
+        _lib.ptr(block_table), block_table.stride(0), block_table.shape[1], _lib.ptr(start),
+        None if n_real is None else _lib.ptr(n_real), B, S, block_size, _lib.ptr(pos),
+        _lib.ptr(slots), _lib.ptr(seq_lens), _lib.stream_handle(dev)), "coopt_row_slots")
+    return pos, slots, seq_lens

@@ -109,3 +109,53 @@ extern "C" int coopt_kv_copy_blocks(const int64_t* regions, int num_regions,
   }
   return COOPT_OK;
 }
+
+// ---------------------------------------------------------------------------------------
+// Paged addressing of a batch of row runs, on the device: sequence b owns rows
+// [b * S, (b + 1) * S) at positions start[b] + j, with cache slot
+// table[b][p / bs] * bs + p % bs (engine/block_manager.py:216-220) and seq_len start[b] + S
+// (engine/batch.py:23-55; the padded layout of engine/cuda_graphs.py:76-104).  Rows with
+// j >= n_real[b] (padding) or a block index outside [0, table_width) get slot -1: the KV
+// write skips them.
+// ---------------------------------------------------------------------------------------
+namespace {
+
+__global__ __launch_bounds__(kThreads) void row_slots_kernel(
+    const int32_t* __restrict__ table, int64_t table_stride, int width,
+    const int64_t* __restrict__ start, const int64_t* __restrict__ n_real, int B, int S, int bs,
+    int64_t* __restrict__ pos_out, int64_t* __restrict__ slot_out, int32_t* __restrict__ seq_lens) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (gid >= static_cast<int64_t>(B) * S) return;
+  const int b = static_cast<int>(gid / S), j = static_cast<int>(gid - static_cast<int64_t>(b) * S);
+  const int64_t s0 = start[b];
+  const int64_t p = s0 + j;
+  const int64_t blk = p >= 0 ? p / bs : -1;
+  const bool real = n_real == nullptr || j < n_real[b];
+  int64_t slot = -1;
+  if (real && blk >= 0 && blk < width)
+    slot = static_cast<int64_t>(table[b * table_stride + blk]) * bs + (p - blk * bs);
+  pos_out[gid] = p;
+  slot_out[gid] = slot;
+  if (j == 0 && seq_lens != nullptr) seq_lens[b] = static_cast<int32_t>(s0 + S);
+}
+
+}  // namespace
+
+extern "C" int coopt_row_slots(const int32_t* block_table, int64_t table_stride, int table_width,
+                               const int64_t* start, const int64_t* n_real, int B, int S,
+                               int block_size, int64_t* positions, int64_t* slots,
+                               int32_t* seq_lens, coopt_stream_t stream) {
+  coopt::clear_error();
+  COOPT_REQUIRE(B >= 0 && S >= 0, "negative size");
+  if (B == 0 || S == 0) return COOPT_OK;
+  COOPT_REQUIRE(block_table && start && positions && slots, "null pointer");
+  COOPT_REQUIRE(block_size > 0 && table_width > 0 && table_stride >= table_width,
+                "block_size and table_width must be positive, table_stride >= table_width");
+  const int64_t n = static_cast<int64_t>(B) * S;
+  COOPT_REQUIRE((n + kThreads - 1) / kThreads <= 0x7fffffff, "too many rows");
+  hipLaunchKernelGGL(row_slots_kernel, dim3(static_cast<unsigned>((n + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, reinterpret_cast<hipStream_t>(stream), block_table,
+                     table_stride, table_width, start, n_real, B, S, block_size, positions, slots,
+                     seq_lens);
+  return coopt::check_launch("coopt_row_slots");
+}

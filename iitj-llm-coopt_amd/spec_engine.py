@@ -27,6 +27,7 @@ import torch.nn.functional as F
 
 from . import _lib
 from .attention import paged_attention, workspace_bytes
+from .batch import row_slots
 from .fused import linear, pack_linear_weight, rms_norm, rope_, row_major, silu_and_mul
 from .kv_cache import allocate_kv_cache, qkv_rope_and_cache, reshape_and_cache_flash
 from .spec_decode import AcceptResult, accept
@@ -225,6 +226,9 @@ class HipOps:
     def silu_mul(self, gate_up):
         return silu_and_mul(gate_up)
 
+    def row_slots(self, kv: "PagedKV", start, S, n_real):
+        return row_slots(kv.block_table, start, S, kv.block_size, n_real)
+
     def linear(self, x, w, out=None, defer_reduce=False):
         return linear(x, w, out=out, defer_reduce=defer_reduce)
 
@@ -346,15 +350,11 @@ class SpecDecoder:
         return F.linear(h, row_major(model.lm_head))
 
     # ---- one speculative step -------------------------------------------------------------
-    def _rows(self, model, kv, start, S, tokens, real, logits_out=None):
-        """Forward S rows per sequence at positions start..start+S-1; rows with real=False are
-        padding (KV write skipped, seq_len = start + S as in the padded graph layout)."""
-        B = self.B
-        pos = start.unsqueeze(1) + self.ar[S]                       # [B, S]
-        slots = kv.slots(pos)
-        if real is not None:
-            slots = torch.where(real.reshape(-1), slots, torch.full_like(slots, -1))
-        seq_lens = (start + S).to(torch.int32)
+    def _rows(self, model, kv, start, S, tokens, n_real, logits_out=None):
+        """Forward S rows per sequence at positions start..start+S-1; rows j >= n_real[b] are
+        padding (KV write skipped, seq_len = start + S as in the padded graph layout).
+        Positions, slots and seq_lens come from one coopt_row_slots launch."""
+        pos, slots, seq_lens = self.ops.row_slots(kv, start, S, n_real)
         meta = (self.cu[S], seq_lens, S, self.max_len)
         return model.forward(self.ops, kv, tokens.reshape(-1), pos.reshape(-1), slots, meta,
                              logits_out=logits_out)
@@ -369,8 +369,7 @@ class SpecDecoder:
         # draft catch-up over tokens[dc:n] as a stride-2 padded batch
         idx = (dc.unsqueeze(1) + self.ar[2]).clamp(max=self.max_len - 1)
         toks2 = torch.gather(self.hist, 1, idx)
-        real = self.ar[2].unsqueeze(0) < lag.unsqueeze(1)
-        logits = self._rows(self.d, self.dkv, dc, 2, toks2, real).view(B, 2, -1)
+        logits = self._rows(self.d, self.dkv, dc, 2, toks2, lag).view(B, 2, -1)
         last = torch.gather(logits, 1, (lag - 1).view(B, 1, 1).expand(B, 1, logits.shape[-1]))
         self.draft_logits[:, 0] = last[:, 0]
         tok = self.ops.sample(self.draft_logits[:, 0], u_draft[0], T)

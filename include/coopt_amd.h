@@ -36,6 +36,8 @@
  *   coopt_rms_norm          vLLM rms_norm / fused_add_rms_norm  engine/model.py:234, 236, 249, 254
  *   coopt_rope              vLLM rotary_embedding (neox)    engine/model.py:239
  *   coopt_silu_mul          vLLM silu_and_mul               engine/model.py:251-252
+ *   coopt_row_slots         slot_mapping / positions /      engine/block_manager.py:216-220,
+ *                           seq_lens of a padded row batch  engine/batch.py:23-55
  *   coopt_linear            F.linear projections at decode  engine/model.py:238, 248, 250,
  *                           / verify row counts             253 (qkv, o, gate_up, down)
  *   coopt_linear_*packed    the same, tile-packed weights   engine/model.py:238, 248, 253
@@ -317,6 +319,20 @@ int coopt_silu_mul_partials(const float* part, int ks, int64_t slice_stride, voi
 int coopt_rms_norm_partials(const float* part, int ks, int64_t slice_stride, void* residual,
                             const void* weight, void* out, int64_t rows, int hidden, float eps,
                             coopt_stream_t stream);
+
+/*
+ * Paged addressing of a batch of row runs on the device -- BlockManager.slot_mapping
+ * (engine/block_manager.py:216-220: slot = table[p / bs] * bs + p % bs) and the positions and
+ * seq_lens of build_batch (engine/batch.py:23-55), for the padded verify layout
+ * (engine/cuda_graphs.py:76-104) where sequence b owns rows [b S, (b + 1) S).
+ *   block_table [B, table_width] int32 (row stride table_stride); start [B] int64.
+ *   positions [B S] = start[b] + j; slots [B S] int64; seq_lens [B] int32 = start[b] + S (NULL
+ *   to skip).  slots = -1 for rows with j >= n_real[b] (n_real [B] int64, NULL = all real) and
+ *   for block indices outside [0, table_width).
+ */
+int coopt_row_slots(const int32_t* block_table, int64_t table_stride, int table_width,
+                    const int64_t* start, const int64_t* n_real, int B, int S, int block_size,
+                    int64_t* positions, int64_t* slots, int32_t* seq_lens, coopt_stream_t stream);
 
 /*
  * Linear layer at decode / verify row counts: y[M, N] = x[M, K] w[N, K]^T, bf16 in and out,

@@ -7,6 +7,8 @@ reference's path restated on the CPU); the product never imports this module.
           math on the dequantised (bf16) cache       form, in fp32 torch for speed)
   sample  inverse-CDF draw from softmax(logits/T)    oracle.accept.sample
   accept  rejection sampling with explicit uniforms  oracle.accept.accept_batch
+  row_slots  positions / slots / seq_lens of a padded  oracle.paged.slot_mapping's formula
+          row batch                                  (engine/block_manager.py:216-220)
 """
 import numpy as np
 import torch
@@ -32,6 +34,21 @@ class OracleOps:
         for x in (q, k):
             x1, x2 = x.chunk(2, dim=-1)
             x.copy_(x * c + torch.cat((-x2, x1), dim=-1) * s)
+
+    def row_slots(self, kv, start, S, n_real):
+        # engine/block_manager.py:216-220 (slot = table[p // bs] * bs + p % bs) for rows
+        # start[b] + j; padding rows (j >= n_real[b]) and positions past the table get -1
+        bs = kv.block_size
+        pos = start.unsqueeze(1) + torch.arange(S, dtype=torch.int64)
+        blk = pos // bs
+        width = kv.block_table.shape[1]
+        ok = (blk >= 0) & (blk < width)
+        if n_real is not None:
+            ok &= torch.arange(S).unsqueeze(0) < n_real.unsqueeze(1)
+        table = kv.block_table.long()
+        slots = torch.gather(table, 1, blk.clamp(0, width - 1)) * bs + pos % bs
+        slots = torch.where(ok, slots, torch.full_like(slots, -1)).reshape(-1)
+        return pos, slots, (start + S).to(torch.int32)
 
     def silu_mul(self, gate_up):
         gate, up = gate_up.chunk(2, dim=-1)

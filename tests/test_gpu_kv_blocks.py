@@ -133,3 +133,36 @@ def test_unpark_migration_keeps_attention_bit_identical(dev):
     after = attend()
     for x, y in zip(before, after):
         assert torch.equal(x, y)
+
+
+# ---- device-side paged addressing of a padded row batch (coopt_row_slots) ----
+
+@pytest.mark.parametrize("B,S,W,bs", [(32, 5, 70, 16), (32, 2, 70, 16), (7, 1, 3, 32), (1, 9, 4, 16)])
+def test_row_slots_match_the_slot_mapping_oracle(dev, B, S, W, bs):
+    """positions = start + j; slots = oracle.paged.slot_mapping over the sequence's block table
+    (engine/block_manager.py:216-220); -1 for padding rows j >= n_real[b] and for positions
+    past the table; seq_lens = start + S."""
+    from iitj_llm_coopt_amd.batch import row_slots
+    from oracle import paged as OP
+    rng = np.random.default_rng(B * 100 + S)
+    table = rng.permutation(B * W + 5)[: B * W].reshape(B, W).astype(np.int32)
+    start = rng.integers(0, W * bs - S + 1, size=B).astype(np.int64)
+    start[0] = W * bs - S + (1 if S > 1 else 0)        # the last rows run past the table
+    n_real = rng.integers(0, S + 1, size=B).astype(np.int64)
+    tt = torch.from_numpy(table).to(dev)
+    st = torch.from_numpy(start).to(dev)
+    for nr in (None, n_real):
+        pos, slots, seq_lens = row_slots(tt, st, S, bs,
+                                         None if nr is None else torch.from_numpy(nr).to(dev))
+        torch.cuda.synchronize()
+        pos, slots, seq_lens = pos.cpu().numpy(), slots.cpu().numpy().reshape(B, S), seq_lens.cpu().numpy()
+        for b in range(B):
+            p = start[b] + np.arange(S)
+            assert np.array_equal(pos[b], p)
+            inside = p < W * bs
+            want = np.full(S, -1, np.int64)
+            want[inside] = OP.slot_mapping(table[b], int(start[b]), int(start[b]) + int(inside.sum()), bs)
+            if nr is not None:
+                want[np.arange(S) >= nr[b]] = -1
+            assert np.array_equal(slots[b], want), (b, slots[b], want)
+        assert np.array_equal(seq_lens, (start + S).astype(np.int32))
