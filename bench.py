@@ -13,8 +13,9 @@ and the length/history update.  value = tokens emitted by the accept step (sum o
 second over the timed steps.
 
 Printed: one JSON line (the driver's contract) with `roofline` for the verify-attention kernel
-(timed per launch with HIP events on torch's current stream, the stream the kernels run on) and
-`cpu_baseline` (the same step, from the same state, on the host cores through oracle ops).
+(40 back-to-back launches between HIP events on torch's current stream, the stream the kernels
+run on, averaged per launch) and `cpu_baseline` (the same step, from the same state, on the
+host cores through oracle ops).
 """
 import argparse
 import json
