@@ -59,9 +59,12 @@ __device__ __forceinline__ u32x4_t ldg16(const uint16_t* p) {
 }
 
 // MT: 16-row tiles of M; NW: 16-column tiles per wave; WAVES: waves per workgroup;
-// PF: K steps of W in flight per wave (even); PK: W is tile-packed.
-template <int MT, int NW, int WAVES, int PF, bool PK>
+// PF: K steps of W in flight per wave (even); PK: W is tile-packed; SILU: W is a gate_up
+// weight packed with gate and up tiles interleaved (coopt_linear_pack_gate_up), K is not
+// split, and the output is silu(gate) * up (F = N / 2 columns) instead of the projection.
+template <int MT, int NW, int WAVES, int PF, bool PK, bool SILU = false>
 __global__ __launch_bounds__(64 * WAVES) void linear_kernel(LinArgs a) {
+  static_assert(!SILU || (PK && NW == 1 && WAVES % 2 == 0), "gate / up tile pairs per wave pair");
   static_assert(PF % 2 == 0, "the step loop is unrolled by PF and alternates X buffers");
   constexpr int kThreads = 64 * WAVES;
   constexpr int kRowsPerRound = kThreads / 16;                     // X rows staged per round
@@ -189,6 +192,37 @@ __global__ __launch_bounds__(64 * WAVES) void linear_kernel(LinArgs a) {
   }
 
   // Epilogue: lane holds rows 16 mt + 4 g + i of column n0 + 16 nt + l16.
+  if constexpr (SILU) {
+    // Wave 2p holds gate tile t = blockIdx.x * WAVES / 2 + p and wave 2p + 1 the matching up
+    // tile; the up wave hands its sums over through LDS (the X staging is dead by now).  Each
+    // sum is rounded to bf16 first -- the projection's output -- then silu(gate) * up as
+    // silu_mul_kernel computes it, rounded once more.
+    __syncthreads();
+    float* xch = reinterpret_cast<float*>(&xs[0][0]);
+    const int pair = wave >> 1;
+    if (wave & 1) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xch[((pair * MT + mt) * 4 + i) * 64 + lane] = acc[mt][0][i];
+    }
+    __syncthreads();
+    if (wave & 1) return;
+    const int F = a.N / 2;
+    const int j = (blockIdx.x * (WAVES / 2) + pair) * 16 + l16;
+    if (j >= F) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = mt * 16 + 4 * g + i;
+        if (m >= a.M) continue;
+        const float gv = bf16_to_f32(f32_to_bf16(acc[mt][0][i]));
+        const float uv = bf16_to_f32(f32_to_bf16(xch[((pair * MT + mt) * 4 + i) * 64 + lane]));
+        a.y[static_cast<int64_t>(m) * a.ldy + j] = f32_to_bf16(gv / (1.0f + __expf(-gv)) * uv);
+      }
+    return;
+  }
   if (gridDim.y == 1 && !a.force_part) {
 #pragma unroll
     for (int nt = 0; nt < NW; ++nt) {
@@ -297,8 +331,10 @@ void launch_mt(const Plan& p, const LinArgs& a, bool packed, hipStream_t s) {
 
 // Tile packing: thread o writes 16-byte chunk o of the packed layout, reading it from the
 // row-major weight.  Chunk o = ((t * (K/128) + u) * 4 + j) * 64 + l.
+// With gu_half = F (a gate_up weight of 2F rows), packed tile 2s holds gate rows
+// [16 s, 16 s + 16) and tile 2s + 1 up rows [F + 16 s, F + 16 s + 16).
 __global__ __launch_bounds__(256) void pack_kernel(const uint16_t* __restrict__ w, int64_t ldw,
-                                                  int kt, int64_t chunks,
+                                                  int kt, int64_t chunks, int gu_half,
                                                   uint16_t* __restrict__ out) {
   const int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (o >= chunks) return;
@@ -306,7 +342,8 @@ __global__ __launch_bounds__(256) void pack_kernel(const uint16_t* __restrict__ 
   const int64_t tu = o >> 8;
   const int64_t t = tu / kt;
   const int u = static_cast<int>(tu - t * kt);
-  const int64_t row = 16 * t + (l & 15);
+  const int64_t src_t = gu_half ? ((t & 1) ? gu_half / 16 + (t >> 1) : (t >> 1)) : t;
+  const int64_t row = 16 * src_t + (l & 15);
   const int64_t col = static_cast<int64_t>(kKB) * u + 32 * j + 8 * (l >> 4);
   *reinterpret_cast<u32x4_t*>(out + o * 8) = ldg16(w + row * ldw + col);
 }
@@ -364,12 +401,15 @@ extern "C" int coopt_linear(const void* x, int64_t ldx, const void* w, int64_t l
   return reduce_into(p, M, N, workspace, y, ldy, s, "coopt_linear");
 }
 
-extern "C" int coopt_linear_pack_weight(const void* w, int64_t ldw, int N, int K, void* out,
-                                        coopt_stream_t stream) {
-  coopt::clear_error();
+namespace {
+
+int pack_weight(const void* w, int64_t ldw, int N, int K, int gu_half, void* out,
+                coopt_stream_t stream, const char* who) {
   COOPT_REQUIRE(N >= 0 && K >= 0, "negative size");
   if (N == 0 || K == 0) return COOPT_OK;
   COOPT_REQUIRE(N % 16 == 0 && K % kKB == 0, "N must be a multiple of 16 and K of 128");
+  COOPT_REQUIRE(gu_half == 0 || (N == 2 * gu_half && gu_half % 16 == 0),
+                "a gate_up weight has 2F rows with F a multiple of 16");
   COOPT_REQUIRE(w && out, "null pointer");
   COOPT_REQUIRE(coopt::aligned16(w) && coopt::aligned16(out), "w and out must be 16-byte aligned");
   COOPT_REQUIRE(ldw >= K && ldw % 8 == 0, "row stride of w must be >= K and a multiple of 8");
@@ -378,8 +418,64 @@ extern "C" int coopt_linear_pack_weight(const void* w, int64_t ldw, int N, int K
   COOPT_REQUIRE((chunks + 255) / 256 <= 0x7fffffff, "w too large");
   hipLaunchKernelGGL(pack_kernel, dim3(static_cast<unsigned>((chunks + 255) / 256)), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t*>(w), ldw,
-                     K / kKB, chunks, static_cast<uint16_t*>(out));
-  return coopt::check_launch("coopt_linear_pack_weight");
+                     K / kKB, chunks, gu_half, static_cast<uint16_t*>(out));
+  return coopt::check_launch(who);
+}
+
+template <int MT>
+void launch_silu(int F, const LinArgs& a, hipStream_t s) {
+  // 4 waves = 2 (gate, up) tile pairs per workgroup; a trailing half workgroup's second pair
+  // reads clamped tiles and writes nothing (its columns are >= F)
+  hipLaunchKernelGGL((linear_kernel<MT, 1, 4, 2, true, true>), dim3((2 * F + 63) / 64, 1),
+                     dim3(256), 0, s, a);
+}
+
+}  // namespace
+
+extern "C" int coopt_linear_pack_weight(const void* w, int64_t ldw, int N, int K, void* out,
+                                        coopt_stream_t stream) {
+  coopt::clear_error();
+  return pack_weight(w, ldw, N, K, 0, out, stream, "coopt_linear_pack_weight");
+}
+
+extern "C" int coopt_linear_pack_gate_up(const void* w, int64_t ldw, int F, int K, void* out,
+                                         coopt_stream_t stream) {
+  coopt::clear_error();
+  COOPT_REQUIRE(F >= 0, "negative size");
+  return pack_weight(w, ldw, 2 * F, K, F, out, stream, "coopt_linear_pack_gate_up");
+}
+
+extern "C" int coopt_linear_silu_supported(int M, int F, int K) {
+  if (M <= 0 || F <= 0 || K <= 0 || F % 16 || K % kKB || M > 256 || m_tiles(M) < 0 ||
+      2LL * F >= 65536)
+    return 0;
+  const Plan p = plan_for(M, 2 * F, K);
+  return p.ks == 1 && p.nw == 1 && p.waves == 4 && p.mt <= 4 ? 1 : 0;
+}
+
+extern "C" int coopt_linear_silu_packed(const void* x, int64_t ldx, const void* w_gu_packed,
+                                        int M, int F, int K, void* y, int64_t ldy,
+                                        coopt_stream_t stream) {
+  coopt::clear_error();
+  COOPT_REQUIRE(M >= 0 && F >= 0 && K >= 0, "negative size");
+  if (M == 0 || F == 0) return COOPT_OK;
+  COOPT_REQUIRE(coopt_linear_silu_supported(M, F, K),
+                "shape outside the fused gate_up + SiLU path (M <= 64, F a multiple of 16, "
+                "2F < 65536, K a multiple of 128 without a K split)");
+  COOPT_REQUIRE(x && w_gu_packed && y, "null pointer");
+  COOPT_REQUIRE(coopt::aligned16(x) && coopt::aligned16(w_gu_packed), "x and w must be 16-byte aligned");
+  COOPT_REQUIRE(ldx >= K && ldx % 8 == 0, "row stride of x must be >= K and a multiple of 8");
+  COOPT_REQUIRE(ldy >= F, "row stride of y must be >= F");
+  const Plan p = plan_for(M, 2 * F, K);
+  LinArgs a{static_cast<const uint16_t*>(x), ldx, static_cast<const uint16_t*>(w_gu_packed), K, M,
+            2 * F, K, p.kt, static_cast<uint16_t*>(y), ldy, nullptr, 0};
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (p.mt) {
+    case 1: launch_silu<1>(F, a, s); break;
+    case 2: launch_silu<2>(F, a, s); break;
+    default: launch_silu<4>(F, a, s); break;
+  }
+  return coopt::check_launch("coopt_linear_silu_packed");
 }
 
 extern "C" int coopt_linear_packed(const void* x, int64_t ldx, const void* w_packed, int M, int N,

@@ -15,7 +15,8 @@ import torch.nn.functional as F
 from . import _lib
 
 __all__ = ["rms_norm", "rope_", "silu_and_mul", "linear", "LinearPartials", "LINEAR_MAX_ROWS",
-           "PackedWeight", "pack_linear_weight", "row_major"]
+           "PackedWeight", "pack_linear_weight", "pack_gate_up_weight", "linear_silu",
+           "row_major"]
 
 LINEAR_MAX_ROWS = 256
 _WS = _lib.WorkspaceCache()
@@ -135,8 +136,10 @@ class PackedWeight:
     the weight-streaming kernel).  linear() picks the copy its path reads; both give the same
     result bit for bit on the kernel path."""
 
-    def __init__(self, weight, packed):
-        self.weight, self.packed = weight, packed
+    def __init__(self, weight, packed, gate_up=False):
+        # gate_up: packed by coopt_linear_pack_gate_up (gate / up tiles interleaved), read only
+        # by linear_silu; linear() then streams the row-major copy
+        self.weight, self.packed, self.gate_up = weight, packed, gate_up
 
     @property
     def shape(self):
@@ -154,6 +157,46 @@ class PackedWeight:
 def row_major(weight):
     """The row-major [N, K] tensor of a weight (a PackedWeight's first copy, else itself)."""
     return weight.weight if isinstance(weight, PackedWeight) else weight
+
+
+def pack_gate_up_weight(weight):
+    """PackedWeight of a bf16 [2F, K] gate_up weight for linear_silu (F a multiple of 16, K of
+    128): one coopt_linear_pack_gate_up launch at model load."""
+    _lib.require_cuda(weight)
+    if weight.dtype != torch.bfloat16 or weight.dim() != 2 or weight.stride(-1) != 1:
+        raise ValueError("weight must be a bf16 [2F, K] matrix with contiguous rows")
+    N2, K = weight.shape
+    if N2 % 32 or K % 128:
+        raise ValueError("packing needs 2F a multiple of 32 and K a multiple of 128")
+    packed = torch.empty(N2 * K, dtype=torch.bfloat16, device=weight.device)
+    _lib.check(_lib.load().coopt_linear_pack_gate_up(
+        _lib.ptr(weight), weight.stride(0), N2 // 2, K, _lib.ptr(packed),
+        _lib.stream_handle(weight.device)), "coopt_linear_pack_gate_up")
+    return PackedWeight(weight, packed, gate_up=True)
+
+
+def linear_silu(x, weight, out=None):
+    """silu_and_mul(linear(x, weight)) (engine/model.py:250-252).  With a gate_up PackedWeight
+    and a shape the fused kernel takes (coopt_linear_silu_supported: draft row counts), one
+    coopt_linear_silu_packed launch, bit-identical to the two-step path; otherwise the two
+    steps."""
+    if isinstance(weight, PackedWeight) and weight.gate_up:
+        K = x.shape[-1]
+        x2 = x.reshape(-1, K)
+        M, F = x2.shape[0], weight.shape[0] // 2
+        lib = _lib.load()
+        if (x.dtype == torch.bfloat16 and x.is_cuda and lib.coopt_linear_silu_supported(M, F, K)):
+            _lib.require_cuda(x, out)
+            if x2.stride(-1) != 1 or x2.stride(0) % 8:
+                x2 = x2.contiguous()
+            if out is None:
+                out = torch.empty(x.shape[:-1] + (F,), dtype=torch.bfloat16, device=x.device)
+            y2 = out.view(-1, F)
+            _lib.check(lib.coopt_linear_silu_packed(
+                _lib.ptr(x2), x2.stride(0), _lib.ptr(weight.packed), M, F, K, _lib.ptr(y2),
+                y2.stride(0), _lib.stream_handle(x.device)), "coopt_linear_silu_packed")
+            return out
+    return silu_and_mul(linear(x, weight, defer_reduce=True), out=out)
 
 
 def pack_linear_weight(weight):
@@ -188,8 +231,8 @@ def linear(x, weight, out=None, defer_reduce=False):
 
     `weight` may be a PackedWeight: the kernel path then streams its tile-packed copy
     (coopt_linear_packed), torch's path its row-major one."""
-    packed = weight.packed if isinstance(weight, PackedWeight) else None
-    if packed is not None:
+    packed = weight.packed if isinstance(weight, PackedWeight) and not weight.gate_up else None
+    if isinstance(weight, PackedWeight):
         weight = weight.weight
     _lib.require_cuda(x, weight, out)
     K = x.shape[-1]

@@ -28,7 +28,8 @@ import torch.nn.functional as F
 from . import _lib
 from .attention import paged_attention, workspace_bytes
 from .batch import row_slots
-from .fused import linear, pack_linear_weight, rms_norm, rope_, row_major, silu_and_mul
+from .fused import (linear, linear_silu, pack_gate_up_weight, pack_linear_weight, rms_norm, rope_,
+                    row_major, silu_and_mul)
 from .kv_cache import allocate_kv_cache, qkv_rope_and_cache, reshape_and_cache_flash
 from .spec_decode import AcceptResult, accept
 
@@ -106,11 +107,12 @@ class RandomLlama:
     PACKED = ("qkv", "o", "down")
 
     def _pack(self):
-        ok = lambda w: w.shape[0] % 16 == 0 and w.shape[1] % 128 == 0  # the tile granularity
+        ok = lambda w, r=16: w.shape[0] % r == 0 and w.shape[1] % 128 == 0  # tile granularity
         for L in self.layers:
             for k in self.packed:
-                if k in L and ok(L[k]):
-                    L[k] = pack_linear_weight(L[k])
+                if k in L and ok(L[k], 32 if k == "gate_up" else 16):
+                    # gate_up: gate / up tiles interleaved, for the fused SiLU epilogue
+                    L[k] = pack_gate_up_weight(L[k]) if k == "gate_up" else pack_linear_weight(L[k])
         if "lm_head" in self.packed and ok(self.lm_head):
             self.lm_head = pack_linear_weight(self.lm_head)   # embed keeps the row-major copy
 
@@ -147,12 +149,12 @@ class RandomLlama:
             qkv = ops.linear(h, L["qkv"], defer_reduce=True)
             q = ops.qkv_epilogue(kv, li, qkv, pos, self.cos, self.sin, slots, H, Hkv, D)
             attn = ops.attend(kv, li, q, meta, self.scale)
-            # o, gate_up and down feed only the fused add + norm or SiLU, which reduce their
+            # gate_up + SiLU·mul is one launch at draft row counts (linear_silu); o, down and
+            # otherwise gate_up feed only the fused add + norm or SiLU, which reduce their
             # split-K partials as they read them
             o = ops.linear(attn.reshape(T, H * D), L["o"], defer_reduce=True)
             h = ops.rms_norm(o, x, L["ln2"], s.eps)
-            gu = ops.linear(h, L["gate_up"], defer_reduce=True)
-            d = ops.linear(ops.silu_mul(gu), L["down"], defer_reduce=True)
+            d = ops.linear(ops.linear_silu(h, L["gate_up"]), L["down"], defer_reduce=True)
         h = ops.rms_norm(d, x, self.norm, s.eps)
         return ops.linear(h, self.lm_head, out=logits_out)
 
@@ -228,6 +230,9 @@ class HipOps:
 
     def row_slots(self, kv: "PagedKV", start, S, n_real):
         return row_slots(kv.block_table, start, S, kv.block_size, n_real)
+
+    def linear_silu(self, x, w):
+        return linear_silu(x, w)
 
     def linear(self, x, w, out=None, defer_reduce=False):
         return linear(x, w, out=out, defer_reduce=defer_reduce)

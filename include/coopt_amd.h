@@ -41,6 +41,7 @@
  *   coopt_linear            F.linear projections at decode  engine/model.py:238, 248, 250,
  *                           / verify row counts             253 (qkv, o, gate_up, down)
  *   coopt_linear_*packed    the same, tile-packed weights   engine/model.py:238, 248, 253
+ *   coopt_linear_silu_packed  gate_up + silu_and_mul        engine/model.py:250-252
  */
 #ifndef COOPT_AMD_H
 #define COOPT_AMD_H
@@ -377,6 +378,23 @@ int coopt_linear_packed(const void* x, int64_t ldx, const void* w_packed, int M,
 int coopt_linear_partials_packed(const void* x, int64_t ldx, const void* w_packed, int M, int N,
                                  int K, void* workspace, size_t workspace_bytes,
                                  coopt_stream_t stream);
+/*
+ * The gate_up projection fused with SiLU-and-mul, engine/model.py:250-252
+ * (silu_and_mul(F.linear(h, gate_up))), for draft row counts:
+ *   coopt_linear_pack_gate_up: out (2F * K bf16) = the [2F, K] gate_up weight packed as
+ *     coopt_linear_pack_weight does, with gate and up tiles interleaved: packed tile 2s holds
+ *     gate rows [16 s, +16), tile 2s + 1 up rows [F + 16 s, +16).  F a multiple of 16.
+ *   coopt_linear_silu_supported(M, F, K): 1 when the fused path takes the shape (M <= 64,
+ *     2F < 65536 and K not split by coopt_linear's plan), else 0.
+ *   coopt_linear_silu_packed: y [M, F] (row stride ldy) = bf16(silu(g) * u) with
+ *     g = bf16(x w_gate^T), u = bf16(x w_up^T) -- bit for bit what coopt_linear followed by
+ *     coopt_silu_mul gives -- in one launch, no workspace.
+ */
+int coopt_linear_pack_gate_up(const void* w, int64_t ldw, int F, int K, void* out,
+                              coopt_stream_t stream);
+int coopt_linear_silu_supported(int M, int F, int K);
+int coopt_linear_silu_packed(const void* x, int64_t ldx, const void* w_gu_packed, int M, int F,
+                             int K, void* y, int64_t ldy, coopt_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -50,6 +50,10 @@ class OracleOps:
         slots = torch.where(ok, slots, torch.full_like(slots, -1)).reshape(-1)
         return pos, slots, (start + S).to(torch.int32)
 
+    def linear_silu(self, x, w):
+        # engine/model.py:250-252: silu_and_mul(F.linear(h, gate_up))
+        return self.silu_mul(self.linear(x, w))
+
     def silu_mul(self, gate_up):
         gate, up = gate_up.chunk(2, dim=-1)
         return torch.nn.functional.silu(gate) * up

@@ -220,3 +220,39 @@ def test_pack_weight_errors(dev):
     assert L.coopt_linear_packed(_lib.ptr(x), 128, _lib.ptr(out), 4, 40, 128, _lib.ptr(y), 40, None, 0,
                                  _lib.stream_handle(dev)) != 0
     assert "multiple of 16" in _lib.last_error()
+
+
+# ---- gate_up fused with SiLU-and-mul (coopt_linear_pack_gate_up, coopt_linear_silu_packed) ----
+
+def test_pack_gate_up_interleaves_gate_and_up_tiles(dev):
+    F, K = 48, 256
+    g = torch.Generator(device=dev).manual_seed(5)
+    w = torch.randn(2 * F, K, generator=g, device=dev).to(torch.bfloat16)
+    p = fused.pack_gate_up_weight(w)
+    order = torch.cat([torch.stack([w[16 * s:16 * s + 16], w[F + 16 * s:F + 16 * s + 16]])
+                       for s in range(F // 16)]).reshape(2 * F, K)     # gate 0, up 0, gate 1, ...
+    assert torch.equal(p.packed.view(torch.int16), packed_layout(order).view(torch.int16))
+
+
+@pytest.mark.parametrize("M,F,K", [(32, 8192, 2048), (64, 8192, 2048), (1, 512, 256), (17, 48, 384),
+                                   (64, 16, 128)])
+def test_linear_silu_is_bit_identical_to_linear_then_silu(dev, M, F, K):
+    g = torch.Generator(device=dev).manual_seed(M + F + K)
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn(2 * F, K, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    assert _lib.load().coopt_linear_silu_supported(M, F, K) == 1    # the fused launch runs
+    want = fused.silu_and_mul(fused.linear(x, w))
+    got = fused.linear_silu(x, fused.pack_gate_up_weight(w))
+    print(f"[linear_silu] M={M} F={F} K={K}", flush=True)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def test_linear_silu_falls_back_outside_the_fused_shapes(dev):
+    """160 rows (a split K and 8 waves) and torch-sized row counts take the two-step path."""
+    g = torch.Generator(device=dev).manual_seed(2)
+    for M, F, K in [(160, 2048, 2048), (300, 64, 256)]:
+        x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+        w = (torch.randn(2 * F, K, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+        assert _lib.load().coopt_linear_silu_supported(M, F, K) == 0
+        want = fused.silu_and_mul(fused.linear(x, w))
+        assert torch.equal(fused.linear_silu(x, fused.pack_gate_up_weight(w)), want)
