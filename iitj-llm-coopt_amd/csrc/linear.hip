@@ -422,12 +422,13 @@ int pack_weight(const void* w, int64_t ldw, int N, int K, int gu_half, void* out
   return coopt::check_launch(who);
 }
 
-template <int MT>
+template <int MT, int WAVES>
 void launch_silu(int F, const LinArgs& a, hipStream_t s) {
-  // 4 waves = 2 (gate, up) tile pairs per workgroup; a trailing half workgroup's second pair
-  // reads clamped tiles and writes nothing (its columns are >= F)
-  hipLaunchKernelGGL((linear_kernel<MT, 1, 4, 2, true, true>), dim3((2 * F + 63) / 64, 1),
-                     dim3(256), 0, s, a);
+  // WAVES / 2 (gate, up) tile pairs per workgroup; pairs of a trailing partial workgroup past
+  // the weight read clamped tiles and write nothing (their columns are >= F)
+  const int rows = 16 * WAVES;
+  hipLaunchKernelGGL((linear_kernel<MT, 1, WAVES, 2, true, true>), dim3((2 * F + rows - 1) / rows, 1),
+                     dim3(64 * WAVES), 0, s, a);
 }
 
 }  // namespace
@@ -450,7 +451,7 @@ extern "C" int coopt_linear_silu_supported(int M, int F, int K) {
       2LL * F >= 65536)
     return 0;
   const Plan p = plan_for(M, 2 * F, K);
-  return p.ks == 1 && p.nw == 1 && p.waves == 4 && p.mt <= 4 ? 1 : 0;
+  return p.ks == 1 && p.nw == 1 && (p.waves == 4 ? p.mt <= 4 : p.mt == 10) ? 1 : 0;
 }
 
 extern "C" int coopt_linear_silu_packed(const void* x, int64_t ldx, const void* w_gu_packed,
@@ -460,8 +461,8 @@ extern "C" int coopt_linear_silu_packed(const void* x, int64_t ldx, const void* 
   COOPT_REQUIRE(M >= 0 && F >= 0 && K >= 0, "negative size");
   if (M == 0 || F == 0) return COOPT_OK;
   COOPT_REQUIRE(coopt_linear_silu_supported(M, F, K),
-                "shape outside the fused gate_up + SiLU path (M <= 64, F a multiple of 16, "
-                "2F < 65536, K a multiple of 128 without a K split)");
+                "shape outside the fused gate_up + SiLU path (M <= 64 or 129-160, F a multiple "
+                "of 16, 2F < 65536, K a multiple of 128 without a K split)");
   COOPT_REQUIRE(x && w_gu_packed && y, "null pointer");
   COOPT_REQUIRE(coopt::aligned16(x) && coopt::aligned16(w_gu_packed), "x and w must be 16-byte aligned");
   COOPT_REQUIRE(ldx >= K && ldx % 8 == 0, "row stride of x must be >= K and a multiple of 8");
@@ -471,9 +472,10 @@ extern "C" int coopt_linear_silu_packed(const void* x, int64_t ldx, const void* 
             2 * F, K, p.kt, static_cast<uint16_t*>(y), ldy, nullptr, 0};
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (p.mt) {
-    case 1: launch_silu<1>(F, a, s); break;
-    case 2: launch_silu<2>(F, a, s); break;
-    default: launch_silu<4>(F, a, s); break;
+    case 1: launch_silu<1, 4>(F, a, s); break;
+    case 2: launch_silu<2, 4>(F, a, s); break;
+    case 4: launch_silu<4, 4>(F, a, s); break;
+    default: launch_silu<10, 8>(F, a, s); break;   // the verify rows (129-160), 8 waves
   }
   return coopt::check_launch("coopt_linear_silu_packed");
 }

@@ -235,7 +235,7 @@ def test_pack_gate_up_interleaves_gate_and_up_tiles(dev):
 
 
 @pytest.mark.parametrize("M,F,K", [(32, 8192, 2048), (64, 8192, 2048), (1, 512, 256), (17, 48, 384),
-                                   (64, 16, 128)])
+                                   (64, 16, 128), (160, 14336, 4096), (131, 14336, 4096)])
 def test_linear_silu_is_bit_identical_to_linear_then_silu(dev, M, F, K):
     g = torch.Generator(device=dev).manual_seed(M + F + K)
     x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
