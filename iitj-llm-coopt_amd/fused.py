@@ -177,7 +177,8 @@ def pack_gate_up_weight(weight):
 
 def linear_silu(x, weight, out=None):
     """silu_and_mul(linear(x, weight)) (engine/model.py:250-252).  With a gate_up PackedWeight
-    and a shape the fused kernel takes (coopt_linear_silu_supported: draft row counts), one
+    and a shape the fused kernel takes (coopt_linear_silu_supported: draft or verify row counts
+    with K unsplit), one
     coopt_linear_silu_packed launch, bit-identical to the two-step path; otherwise the two
     steps."""
     if isinstance(weight, PackedWeight) and weight.gate_up:

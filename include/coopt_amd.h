@@ -380,12 +380,12 @@ int coopt_linear_partials_packed(const void* x, int64_t ldx, const void* w_packe
                                  coopt_stream_t stream);
 /*
  * The gate_up projection fused with SiLU-and-mul, engine/model.py:250-252
- * (silu_and_mul(F.linear(h, gate_up))), for draft row counts:
+ * (silu_and_mul(F.linear(h, gate_up))), at draft and verify row counts:
  *   coopt_linear_pack_gate_up: out (2F * K bf16) = the [2F, K] gate_up weight packed as
  *     coopt_linear_pack_weight does, with gate and up tiles interleaved: packed tile 2s holds
  *     gate rows [16 s, +16), tile 2s + 1 up rows [F + 16 s, +16).  F a multiple of 16.
- *   coopt_linear_silu_supported(M, F, K): 1 when the fused path takes the shape (M <= 64,
- *     2F < 65536 and K not split by coopt_linear's plan), else 0.
+ *   coopt_linear_silu_supported(M, F, K): 1 when the fused path takes the shape (M <= 64 or
+ *     129 <= M <= 160, 2F < 65536 and K not split by coopt_linear's plan), else 0.
  *   coopt_linear_silu_packed: y [M, F] (row stride ldy) = bf16(silu(g) * u) with
  *     g = bf16(x w_gate^T), u = bf16(x w_up^T) -- bit for bit what coopt_linear followed by
  *     coopt_silu_mul gives -- in one launch, no workspace.
