@@ -34,9 +34,13 @@
 // score MFMAs see the reference's operands.  V: the codes enter the PV MFMAs
 // (v_mfma_f32_16x16x32_f16) as exact fp16 integers -- two byte selects place (code + 128)
 // under a 0x64 exponent byte, giving 1024 + code + 128 exactly, and one packed fp16 add
-// removes the 1152 -- and each key's V scale is folded into its probability, fp16(p * s_v).
-// That replaces bf16(p) * bf16(code * s_v) by one fp16 rounding of the product (11 bits
-// against two 8-bit roundings) at a third of the VALU work per V element.
+// removes the 1152 -- and each key's V scale is folded into its probability,
+// fp16(p * s_v * 2^-e_v).  That replaces bf16(p) * bf16(code * s_v) by one fp16 rounding of
+// the product (11 bits against two 8-bit roundings) at a third of the VALU work per V
+// element.  e_v is a per-wave power-of-two reference that keeps the fp16 product inside
+// [2^-14, 2^15] for every scale the fp16 scale cache can hold (up to 65504, i.e. |V| up to
+// 8.3e6): it is set from the largest V scale seen so far and enters the softmax exponent, so
+// it cancels in o / l like the running max does.
 #include <math.h>
 
 #include "common.h"
@@ -114,6 +118,14 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 }
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+
+// Per-half unsigned max of two words of two u16 each (v_pk_max_u16).
+__device__ __forceinline__ uint32_t max_u16x2(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2_t, a),
+                                                                __builtin_bit_cast(u16x2_t, b)));
+}
 
 __device__ __forceinline__ int64_t clamp_page(int32_t page, int64_t num_blocks) {
   return page < 0 ? 0 : (page >= num_blocks ? num_blocks - 1 : page);
@@ -244,6 +256,11 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
 #pragma unroll
     for (int dt = 0; dt < kDt; ++dt) o[rt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
+  // INT8: the wave's V-scale reference exponent e_v (wave-uniform).  The PV operand is
+  // fp16(p * s_v * 2^-e_v); o and l are kept relative to 2^(m_run + e_v), so e_v enters the
+  // exponent of p and the row maxima the merge sees, and cancels in o / l.
+  int e_v = 0;
+  bool ev_set = false;
 
   const int ntiles = (k_end - k_begin + kTileKeys - 1) / kTileKeys;
   const unsigned char* kbase = static_cast<const unsigned char*>(a.kc);
@@ -349,6 +366,37 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
     auto scale_of = [&](const u32x2_t& w, int i) {
       return f16_to_f32(static_cast<uint16_t>(w[i >> 1] >> (16 * (i & 1))));
     };
+
+    // INT8: keep fp16(p * s_v * 2^-e_v) in range.  p <= 2^kSlack = 2^8, so every V scale must
+    // stay at or below 2^(e_v + 7) (products <= 2^15 < 65504).  The first positive scale, or
+    // one above that bound, moves e_v so that the tile's largest scale lands in [2^6, 2^7),
+    // and o and l are rescaled by the change (one uniform branch, taken O(log range) times
+    // per wave).  Scales are non-negative fp16, so their bit patterns order them; non-finite
+    // patterns count as the largest finite scale.
+    if constexpr (INT8) {
+      const uint32_t wv = max_u16x2(max_u16x2(raw.vs[0][0], raw.vs[0][1]),
+                                    max_u16x2(raw.vs[1][0], raw.vs[1][1]));
+      const uint32_t smax = min(max(wv & 0xffffu, wv >> 16), 0x7bffu);
+      const uint32_t thr = !ev_set ? 0u
+                           : (e_v + 7 >= 16 ? 0x7c00u : static_cast<uint32_t>(e_v + 7 + 15) << 10);
+      if (__builtin_amdgcn_ballot_w64(smax > thr)) {
+        uint32_t wm = smax;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1)
+          wm = max(wm, static_cast<uint32_t>(__shfl_xor(static_cast<int>(wm), off, 64)));
+        // fp16 exponent of the largest scale (subnormals count as 2^-15), minus 6
+        const int e_new = __builtin_amdgcn_readfirstlane(static_cast<int>(wm >> 10) - 21);
+        const float f = exp2_fast(static_cast<float>(e_v - e_new));
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          l_run[rt] *= f;
+#pragma unroll
+          for (int dt = 0; dt < kDt; ++dt) o[rt][dt] *= f;
+        }
+        e_v = e_new;
+        ev_set = true;
+      }
+    }
 
     // ---- V^T operands, built first: they do not depend on the scores, so their VALU work
     // is scheduled alongside the score MFMAs in one basic block ----
@@ -470,7 +518,8 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
     uint32_t pb[RT][4];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      const float m_use = m_run[rt] == -INFINITY ? 0.0f : m_run[rt];
+      const float m_use = (m_run[rt] == -INFINITY ? 0.0f : m_run[rt]) +
+                          (INT8 ? static_cast<float>(e_v) : 0.0f);
       float p[2][4], psum = 0.0f;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
@@ -560,8 +609,11 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
   __syncthreads();  // Q in LDS is dead; the merge below reuses the space
 
   // ---- merge the waves ----
+  // the wave's o and l are relative to 2^(m_run + e_v) (e_v = 0 for bf16 KV)
+  const float ev_f = INT8 ? static_cast<float>(e_v) : 0.0f;
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
+    m_run[rt] += ev_f;
     l_run[rt] += __shfl_xor(l_run[rt], 16, 64);
     l_run[rt] += __shfl_xor(l_run[rt], 32, 64);
     if (grp == 0) {

@@ -256,12 +256,13 @@ class HipOps:
         return res.tokens[:, 0]
 
     def accept(self, target_logits, draft_logits, draft_tokens, temperature, u_acc, u_res,
-               out=None):
+               out=None, gamma_per_seq=None, target_row0=None, draft_row0=None):
         B, g = draft_tokens.shape
         V = target_logits.shape[-1]
         ws = self.workspace(("acc", 1), _lib.load().coopt_accept_sample_workspace(B, g, V))
         return accept(target_logits, draft_logits, draft_tokens, temperature, u_acc, u_res,
-                      workspace=ws, out=out)
+                      gamma_per_seq=gamma_per_seq, target_row0=target_row0,
+                      draft_row0=draft_row0, workspace=ws, out=out)
 
     def _empty_tokens(self, n):
         key = ("empty", n)
@@ -272,38 +273,154 @@ class HipOps:
         return t
 
 
+
+def target_strides(gamma_max: int):
+    """Verify strides the step is bucketed by: {1} and gamma + 1 for gamma in
+    (1, 2, 3, 4, 6, 8) up to gamma_max, plus gamma_max + 1 (engine/engine.py:221-225)."""
+    return sorted({1} | {g + 1 for g in (1, 2, 3, 4, 6, 8) if g <= gamma_max}
+                  | ({gamma_max + 1} if gamma_max else set()))
+
+
+BATCH_BUCKETS = (1, 2, 4, 8, 16, 32, 64, 96, 128, 160, 192, 224, 256)  # engine/engine.py:161
+
+
 class SpecDecoder:
-    """Batch of B sequences decoding speculatively with gamma drafts per step."""
+    """A batch of sequences decoding speculatively, every step device-resident.
+
+    Per sequence b (its slot) and step, with gamma[b] the caller's draft length
+    (engine/engine.py:325-470 for a batch in which every sequence decodes):
+      lag = len(tokens) - draft_computed
+      gamma[b] > 0 and lag <= 2   speculate: the draft catches up over tokens[dc:] and
+                                  proposes gamma[b] tokens; the target verifies
+                                  [last] + drafts; rejection sampling keeps a prefix + 1
+      gamma[b] > 0 and lag > 2    lagging: the draft catches up over min(lag - 1, S_c) tokens
+                                  and proposes nothing; the target decodes one token
+      gamma[b] == 0               plain decode: one target token, the draft is not run
+    followed by the rollback of engine/engine.py:463-470 (num_computed = len - 1,
+    draft_computed clamped to it).  Rollback needs no cache writes: KV beyond a sequence's
+    length is overwritten by its next step (slots are a function of position and table).
+
+    Shapes are bucketed as the reference's graph runner buckets them (engine/cuda_graphs.py:
+    7-16, 68-104): the first Bc slots of the state are one step's batch, Bc the smallest batch
+    bucket >= the live sequences, and the slots past the live ones are dummy sequences (all
+    rows padding: no KV write, seq_len = S, outputs discarded).  G = max gamma[b] drafting
+    rounds run; the target verify has stride S_t = the smallest stride >= G + 1, and a
+    sequence's rows past its own gamma + 1 are padding (slot -1, seq_len = start + S_t, so
+    the bottom-right causal mask keeps real rows exact).  The draft catch-up has stride
+    S_c = 2, or more when a lagging sequence needs it.  One HIP graph is captured per
+    (Bc, G) bucket with S_c = 2; a step that needs a longer catch-up runs eagerly, as the
+    reference runs such draft batches outside its graphs.
+
+    Random draws come from a uniform table (set_uniforms): step i reads row i of it.  Row
+    layout, for the Bcap = max bucket slots and gamma_max:
+      [0, gmax*Bcap)                   u_draft[i, b] at i*Bcap + b  (inverse-CDF draw of draft i)
+      [gmax*Bcap, 2*gmax*Bcap)         u_acc[b, i] at b*gmax + i    (accept test of draft i)
+      [2*gmax*Bcap, (2*gmax+1)*Bcap)   u_res[b]                     (emitted token's draw)
+    so a step's decisions are a pure function of the state, the logits and its row.
+    """
 
     def __init__(self, target: RandomLlama, draft: RandomLlama, batch: int, gamma: int,
                  prompt_len: int, max_steps: int, ops=None, target_kv="int8", draft_kv="auto",
-                 temperature=1.0, block_size=16, seed=0):
+                 temperature=1.0, block_size=16, seed=0, batch_buckets=None, max_catchup=64):
         dev = target.device
-        self.t, self.d, self.B, self.g = target, draft, batch, gamma
-        self.P, self.T = prompt_len, temperature
+        self.t, self.d = target, draft
+        self.P, self.T, self.gmax = prompt_len, temperature, gamma
         self.ops = ops or HipOps(dev)
-        self.max_len = prompt_len + 1 + max_steps * (gamma + 1) + gamma + 2
-        self.tkv = PagedKV(target.s, batch, self.max_len, target_kv, dev, block_size, seed)
-        self.dkv = PagedKV(draft.s, batch, self.max_len, draft_kv, dev, block_size, seed + 1)
-        self.hist = torch.zeros((batch, self.max_len), dtype=torch.int64, device=dev)
-        self.n = torch.zeros(batch, dtype=torch.int64, device=dev)    # tokens so far
-        self.dc = torch.zeros(batch, dtype=torch.int64, device=dev)   # draft KV length
-        self.emitted = torch.zeros((), dtype=torch.int64, device=dev)
-        self.drafted = torch.zeros((), dtype=torch.int64, device=dev)
-        self.accepted = torch.zeros((), dtype=torch.int64, device=dev)
+        self.strides = target_strides(gamma)
+        self.smax = self.strides[-1]
+        buckets = tuple(sorted(BATCH_BUCKETS if batch_buckets is None else batch_buckets))
+        self.buckets = tuple(b for b in buckets if b < batch) + (min([b for b in buckets if b >= batch] or [batch]),)
+        self.Bcap = self.buckets[-1]
+        self.max_catchup = max_catchup
+        # positions reach n - 1 + S_t - 1 (verify) and dc + S_c - 1 (catch-up) past the tokens
+        self.max_len = prompt_len + 1 + max_steps * (gamma + 1) + self.smax + max_catchup + 2
+        Bc = self.Bcap
+        self.tkv = PagedKV(target.s, Bc, self.max_len, target_kv, dev, block_size, seed)
+        self.dkv = PagedKV(draft.s, Bc, self.max_len, draft_kv, dev, block_size, seed + 1)
+        i64 = dict(dtype=torch.int64, device=dev)
+        self.hist = torch.zeros((Bc, self.max_len), **i64)
+        self.n = torch.zeros(Bc, **i64)          # tokens so far
+        self.dc = torch.zeros(Bc, **i64)         # draft KV length (draft_computed)
+        self.gamma_dev = torch.zeros(Bc, **i64)  # the caller's gamma per slot (0: dummy)
+        self.live_dev = torch.zeros(Bc, dtype=torch.bool, device=dev)
+        self.gamma_eff = torch.zeros(Bc, dtype=torch.int32, device=dev)  # drafts verified
+        self.emitted = torch.zeros((), **i64)
+        self.drafted = torch.zeros((), **i64)
+        self.accepted = torch.zeros((), **i64)
         V = target.s.vocab
-        self.draft_logits = torch.empty((batch, gamma, V), dtype=torch.bfloat16, device=dev)
-        self.target_logits = torch.empty((batch * (gamma + 1), V), dtype=torch.bfloat16,
-                                         device=dev)
-        self.draft_tok = torch.zeros((batch, gamma), dtype=torch.int32, device=dev)
-        self.u = torch.zeros(batch * (2 * gamma + 1), dtype=torch.float32, device=dev)
-        self.res = AcceptResult(torch.empty(batch, dtype=torch.int32, device=dev),
-                                torch.empty((batch, gamma + 1), dtype=torch.int32, device=dev),
-                                torch.empty(batch, dtype=torch.float32, device=dev))
-        self.cu = {S: torch.arange(batch + 1, dtype=torch.int32, device=dev) * S
-                   for S in (1, 2, gamma + 1)}
-        self.ar = {S: torch.arange(S, dtype=torch.int64, device=dev) for S in (1, 2, gamma + 1)}
-        self.graph = None
+        self.draft_logits = torch.empty((Bc, self.smax - 1, V), dtype=torch.bfloat16, device=dev)
+        self.target_logits = torch.empty((Bc * self.smax, V), dtype=torch.bfloat16, device=dev)
+        self.draft_tok = torch.zeros((Bc, self.smax - 1), dtype=torch.int32, device=dev)
+        self.nu = Bc * (2 * gamma + 1)
+        self.u = torch.zeros(self.nu, dtype=torch.float32, device=dev)
+        self.u_ctr = torch.zeros((), **i64)
+        g = torch.Generator().manual_seed(seed + 17)
+        self.set_uniforms(torch.rand((max_steps + 8, self.nu), generator=g))
+        # accept outputs; the token rows are [Bc, S_t] per verify stride (contiguous)
+        self._acc_len = torch.zeros(Bc, dtype=torch.int32, device=dev)
+        self._margin = torch.zeros(Bc, dtype=torch.float32, device=dev)
+        self._acc_tok = {S: torch.zeros((Bc, S), dtype=torch.int32, device=dev) for S in self.strides}
+        self.res = AcceptResult(self._acc_len, self._acc_tok[self.smax], self._margin)
+        self.ar = {S: torch.arange(S, **i64) for S in range(1, max(self.smax, max_catchup) + 1)}
+        self._cu = {}
+        self._row0 = {}
+        self.graphs = {}
+        self.pool = None
+        self.last_key = None
+        self.B = batch                      # live sequences: slots [0, B)
+        self.seq_ids = list(range(batch))   # the caller's id of the sequence in each slot
+        self.gamma = [gamma] * batch        # the caller's draft lengths
+        self.lag_lo = [1] * batch           # host bounds on len(tokens) - draft_computed
+        self.lag_hi = [1] * batch
+        self._sync_live()
+
+    # ---- caller inputs ----------------------------------------------------------------
+    @property
+    def g(self):
+        return self.gmax
+
+    def set_uniforms(self, table):
+        """table [rows, (2*gamma_max + 1) * Bcap] fp32 (layout in the class docstring); the next
+        step reads row 0 (graph replays included: the row index lives on the device)."""
+        table = torch.as_tensor(table, dtype=torch.float32)
+        if table.dim() != 2 or table.shape[1] != self.nu:
+            raise ValueError(f"uniform table must be [rows, {self.nu}]")
+        self.u_table = table.to(self.hist.device).contiguous()
+        self.u_ctr.zero_()
+
+    def set_gamma(self, gamma):
+        """Draft length per live sequence (int or one per slot); 0 = plain decoding."""
+        g = [int(gamma)] * self.B if isinstance(gamma, int) else [int(x) for x in gamma]
+        if len(g) != self.B or any(x < 0 or x > self.gmax for x in g):
+            raise ValueError(f"gamma must be {self.B} values in [0, {self.gmax}]")
+        self.gamma = g
+        self._sync_live()
+
+    def retire(self, slot):
+        """Drops the sequence in `slot`: the last live sequence moves into it (its history,
+        lengths and both block-table rows, so its KV stays where it is)."""
+        if not 0 <= slot < self.B:
+            raise ValueError("no live sequence in that slot")
+        last = self.B - 1
+        if slot != last:
+            for t in (self.hist, self.n, self.dc, self.tkv.block_table, self.dkv.block_table):
+                a, b = t[slot].clone(), t[last].clone()
+                t[slot].copy_(b)
+                t[last].copy_(a)
+            for lst in (self.gamma, self.lag_lo, self.lag_hi, self.seq_ids):
+                lst[slot] = lst[last]
+        for lst in (self.gamma, self.lag_lo, self.lag_hi, self.seq_ids):
+            lst.pop()
+        self.B -= 1
+        self._sync_live()
+
+    def _sync_live(self):
+        live = torch.zeros(self.Bcap, dtype=torch.bool)
+        live[: self.B] = True
+        gam = torch.zeros(self.Bcap, dtype=torch.int64)
+        gam[: self.B] = torch.tensor(self.gamma, dtype=torch.int64)
+        self.live_dev.copy_(live)
+        self.gamma_dev.copy_(gam)
 
     # ---- prefill (not part of the timed step) -------------------------------------------
     @torch.inference_mode()
@@ -312,16 +429,20 @@ class SpecDecoder:
         in fp32 SDPA, KV written through the paged write kernel), samples the first token
         from the target and sets num_computed = P (engine/engine.py:427-436)."""
         B, P = prompts.shape
-        self.hist[:, :P] = prompts
+        if B != self.B:
+            raise ValueError(f"{self.B} prompts expected")
+        self.hist[:B, :P] = prompts
         pos = torch.arange(P, device=self.hist.device).expand(B, P)
         for model, kv in ((self.t, self.tkv), (self.d, self.dkv)):
             logits = self._prefill_model(model, kv, prompts, pos)
             if model is self.t:
                 first = self.ops.sample(logits, u_first, self.T)
-        self.hist[:, P] = first.long()
-        self.n.fill_(P + 1)
-        self.dc.fill_(P)
-        torch.cuda.synchronize(self.hist.device)
+        self.hist[:B, P] = first.long()
+        self.n[:B] = P + 1
+        self.dc[:B] = P
+        self.lag_lo, self.lag_hi = [1] * B, [1] * B
+        if self.hist.is_cuda:
+            torch.cuda.synchronize(self.hist.device)
 
     def _prefill_model(self, model, kv, ids, pos):
         s = model.s
@@ -329,7 +450,8 @@ class SpecDecoder:
         H, Hkv, D = s.heads, s.kv_heads, s.head_dim
         T = B * P
         flat_pos = pos.reshape(-1).contiguous()
-        slots = kv.slots(pos)
+        blk = torch.gather(kv.block_table[:B].long(), 1, pos // kv.block_size)
+        slots = (blk * kv.block_size + pos % kv.block_size).reshape(-1)
         x = F.embedding(ids.reshape(-1), model.embed)
         d = None
         for li, L in enumerate(model.layers):
@@ -355,82 +477,163 @@ class SpecDecoder:
         h = self.ops.rms_norm(last_d, last_x, model.norm, s.eps)
         return F.linear(h, row_major(model.lm_head))
 
+    # ---- buckets ----------------------------------------------------------------------
+    def bucket(self):
+        """(Bc, G, S_t, S_c) of the next step, from the host's gamma and lag bounds."""
+        Bc = next(b for b in self.buckets if b >= self.B)
+        G = max(self.gamma, default=0)
+        S_t = next(S for S in self.strides if S >= G + 1)
+        need = max([self.lag_hi[b] - 1 for b in range(self.B) if self.gamma[b] > 0] + [2])
+        S_c = 2 if need <= 2 else min(self.max_catchup, 1 << (need - 1).bit_length())
+        return Bc, G, S_t, S_c
+
+    def _advance_host(self, S_c):
+        for b in range(self.B):
+            lo, hi, g = self.lag_lo[b], self.lag_hi[b], self.gamma[b]
+            if g == 0:
+                lo, hi = lo + 1, hi + 1
+            elif hi <= 2 or lo <= 2:
+                lo, hi = 1, 2      # speculated (lag 1 or 2 after), or caught up from lag 3
+            else:
+                lo, hi = max(2, lo - S_c + 1), max(2, hi - S_c + 1)
+            self.lag_lo[b], self.lag_hi[b] = lo, hi
+
+    def _meta(self, Bc, S):
+        key = (Bc, S)
+        if key not in self._cu:
+            self._cu[key] = torch.arange(Bc + 1, dtype=torch.int32, device=self.hist.device) * S
+        return self._cu[key]
+
+    def _rows0(self, Bc, S):
+        key = (Bc, S)
+        if key not in self._row0:
+            self._row0[key] = torch.arange(Bc, dtype=torch.int32, device=self.hist.device) * S
+        return self._row0[key]
+
     # ---- one speculative step -------------------------------------------------------------
-    def _rows(self, model, kv, start, S, tokens, n_real, logits_out=None):
-        """Forward S rows per sequence at positions start..start+S-1; rows j >= n_real[b] are
-        padding (KV write skipped, seq_len = start + S as in the padded graph layout).
-        Positions, slots and seq_lens come from one coopt_row_slots launch."""
+    def _rows(self, model, kv, Bc, start, S, tokens, n_real, logits_out=None):
+        """Forward S rows per sequence at positions start..start+S-1 over slots [0, Bc); rows
+        j >= n_real[b] are padding (KV write skipped, seq_len = start + S as in the padded
+        graph layout).  Positions, slots and seq_lens come from one coopt_row_slots launch."""
         pos, slots, seq_lens = self.ops.row_slots(kv, start, S, n_real)
-        meta = (self.cu[S], seq_lens, S, self.max_len)
+        meta = (self._meta(Bc, S), seq_lens, S, self.max_len)
         return model.forward(self.ops, kv, tokens.reshape(-1), pos.reshape(-1), slots, meta,
                              logits_out=logits_out)
 
     @torch.inference_mode()
-    def step(self):
-        B, g, T = self.B, self.g, self.T
-        u = torch.rand(self.u.shape, device=self.u.device, out=self.u)
-        u_draft, u_acc, u_res = u[: B * g].view(g, B), u[B * g: 2 * B * g].view(B, g), u[2 * B * g:]
-        n, dc = self.n, self.dc
-        lag = n - dc                                                 # 1 or 2
-        # draft catch-up over tokens[dc:n] as a stride-2 padded batch
-        idx = (dc.unsqueeze(1) + self.ar[2]).clamp(max=self.max_len - 1)
-        toks2 = torch.gather(self.hist, 1, idx)
-        logits = self._rows(self.d, self.dkv, dc, 2, toks2, lag).view(B, 2, -1)
-        last = torch.gather(logits, 1, (lag - 1).view(B, 1, 1).expand(B, 1, logits.shape[-1]))
-        self.draft_logits[:, 0] = last[:, 0]
-        tok = self.ops.sample(self.draft_logits[:, 0], u_draft[0], T)
-        self.draft_tok[:, 0] = tok
-        for i in range(1, g):
-            start = n - 1 + i
-            self._rows(self.d, self.dkv, start, 1, self.draft_tok[:, i - 1].long(), None,
-                       logits_out=self.draft_logits[:, i])
-            self.draft_tok[:, i] = self.ops.sample(self.draft_logits[:, i], u_draft[i], T)
-        # target verify over [last token] + drafts
-        vt = torch.cat([torch.gather(self.hist, 1, (n - 1).unsqueeze(1)), self.draft_tok.long()], 1)
-        self._rows(self.t, self.tkv, n - 1, g + 1, vt, None, logits_out=self.target_logits)
-        res = self.ops.accept(self.target_logits.view(B, g + 1, -1), self.draft_logits,
-                              self.draft_tok, T, u_acc, u_res, out=self.res)
-        acc = res.accepted_len.long()
-        # append drafts[:k] + [token] to the history; rollback is the length update
-        pos = (n.unsqueeze(1) + self.ar[g + 1]).clamp(max=self.max_len - 1)
-        keep = self.ar[g + 1].unsqueeze(0) <= acc.unsqueeze(1)
-        old = torch.gather(self.hist, 1, pos)
-        self.hist.scatter_(1, pos, torch.where(keep, res.tokens.long(), old))
-        new_n = n + acc + 1
-        self.dc.copy_(torch.minimum(n + g - 1, new_n - 1))
-        self.n.copy_(new_n)
-        self.emitted += (acc + 1).sum()
-        self.drafted += B * g
+    def _step(self, Bc, G, S_t, S_c):
+        T, V = self.T, self.t.s.vocab
+        gm, Bcap = self.gmax, self.Bcap
+        u = torch.index_select(self.u_table, 0, torch.remainder(self.u_ctr, self.u_table.shape[0]).view(1))
+        self.u.copy_(u.view(-1))
+        self.u_ctr += 1
+        u_draft = self.u[: gm * Bcap].view(gm, Bcap)
+        u_acc = self.u[gm * Bcap: 2 * gm * Bcap].view(Bcap, gm)
+        u_res = self.u[2 * gm * Bcap:]
+        live, greq = self.live_dev[:Bc], self.gamma_dev[:Bc]
+        n, dc = self.n[:Bc], self.dc[:Bc]
+        zero = torch.zeros_like(n)
+        lag = n - dc
+        want = live & (greq > 0)
+        spec = want & (lag <= 2)
+        lagging = want & (lag > 2)
+        geff = torch.where(spec, greq, zero)
+        m = torch.where(spec, lag, torch.where(lagging, torch.clamp(lag - 1, max=S_c), zero))
+        # draft: catch-up over tokens[dc : dc + m] (stride S_c) and the first proposal
+        dc1 = dc.clone()
+        if G > 0:
+            start = torch.where(live, dc, zero)
+            idx = (start.unsqueeze(1) + self.ar[S_c]).clamp(max=self.max_len - 1)
+            toks = torch.gather(self.hist[:Bc], 1, idx)
+            logits = self._rows(self.d, self.dkv, Bc, start, S_c, toks, m).view(Bc, S_c, V)
+            last = torch.gather(logits, 1, (m - 1).clamp(min=0).view(Bc, 1, 1).expand(Bc, 1, V))
+            self.draft_logits[:Bc, 0] = last[:, 0]
+            self.draft_tok[:Bc, 0] = self.ops.sample(self.draft_logits[:Bc, 0], u_draft[0, :Bc], T)
+            dc1 = dc1 + m
+            for i in range(1, G):
+                active = (spec & (geff > i)).long()
+                start = torch.where(live, dc1, zero)
+                self._rows(self.d, self.dkv, Bc, start, 1, self.draft_tok[:Bc, i - 1].long(), active,
+                           logits_out=self.draft_logits[:Bc, i])
+                dc1 = dc1 + active
+                self.draft_tok[:Bc, i] = self.ops.sample(self.draft_logits[:Bc, i], u_draft[i, :Bc], T)
+        # target verify over [last token] + drafts (stride S_t; rows past gamma_eff + 1 padding)
+        start = torch.where(live, n - 1, zero)
+        last_tok = torch.gather(self.hist[:Bc], 1, start.unsqueeze(1))
+        vt = torch.cat([last_tok, self.draft_tok[:Bc, : S_t - 1].long()], 1)
+        self._rows(self.t, self.tkv, Bc, start, S_t, vt, torch.where(live, geff + 1, zero),
+                   logits_out=self.target_logits[: Bc * S_t])
+        self.gamma_eff[:Bc] = geff.to(torch.int32)
+        res = AcceptResult(self._acc_len[:Bc], self._acc_tok[S_t][:Bc], self._margin[:Bc])
+        res = self.ops.accept(self.target_logits[: Bc * S_t], self.draft_logits.view(Bcap * (self.smax - 1), V),
+                              self.draft_tok[:Bc, : S_t - 1], T, u_acc[:Bc, : S_t - 1], u_res[:Bc],
+                              out=res, gamma_per_seq=self.gamma_eff[:Bc],
+                              target_row0=self._rows0(Bc, S_t), draft_row0=self._rows0(Bc, self.smax - 1))
+        acc = torch.where(live, res.accepted_len.long(), zero)
+        # append drafts[:k] + [token] to live histories; rollback is the length update
+        pos = (n.unsqueeze(1) + self.ar[S_t]).clamp(max=self.max_len - 1)
+        keep = (self.ar[S_t].unsqueeze(0) <= acc.unsqueeze(1)) & live.unsqueeze(1)
+        old = torch.gather(self.hist[:Bc], 1, pos)
+        self.hist[:Bc].scatter_(1, pos, torch.where(keep, res.tokens.long(), old))
+        new_n = torch.where(live, n + acc + 1, n)
+        self.dc[:Bc] = torch.where(live, torch.minimum(dc1, new_n - 1), dc)
+        self.n[:Bc] = new_n
+        self.emitted += torch.where(live, acc + 1, zero).sum()
+        self.drafted += geff.sum()
         self.accepted += acc.sum()
 
-    def to(self, device, ops):
-        """A copy of the decoder's full state (weights, caches, history) on another device,
-        stepping through `ops` -- e.g. to time the same step on the host cores."""
-        other = object.__new__(SpecDecoder)
-        other.__dict__.update(self.__dict__)
-        other.t, other.d = self.t.to(device), self.d.to(device)
-        other.tkv, other.dkv = self.tkv.to(device), self.dkv.to(device)
-        other.ops = ops
-        for name in ("hist", "n", "dc", "emitted", "drafted", "accepted", "draft_logits",
-                     "target_logits", "draft_tok", "u"):
-            setattr(other, name, getattr(self, name).to(device))
-        other.res = AcceptResult(*(t.to(device) for t in (self.res.accepted_len,
-                                                            self.res.tokens, self.res.margin)))
-        other.cu = {k: v.to(device) for k, v in self.cu.items()}
-        other.ar = {k: v.to(device) for k, v in self.ar.items()}
-        other.graph = None
-        return other
+    def step(self):
+        """One eager step (same device work as a graph replay, launched from the host)."""
+        key = self.bucket()
+        self._step(*key)
+        self._finish(key)
 
-    def capture(self):
-        """Records one step into a HIP graph (call after a warm-up step)."""
-        s = torch.cuda.Stream(device=self.hist.device)
-        s.wait_stream(torch.cuda.current_stream(self.hist.device))
+    def _finish(self, key):
+        Bc, S_t = key[0], key[2]
+        self.res = AcceptResult(self._acc_len[:Bc], self._acc_tok[S_t][:Bc], self._margin[:Bc])
+        self.last_key = key
+        self._advance_host(key[3])
+
+    def capture(self, key=None):
+        """Records the step of bucket `key` = (Bc, G, S_t, 2) (default: the next step's) into
+        a HIP graph.  Side-effect free: the warm-up pass and the recording run with every
+        slot a dummy, and the uniform row counter is restored."""
+        key = self.bucket() if key is None else key
+        if key[3] != 2:
+            raise ValueError("graphs are captured with the stride-2 draft catch-up")
+        dev = self.hist.device
+        ctr = self.u_ctr.clone()
+        self.live_dev.zero_()
+        self.gamma_dev.zero_()
+        if self.pool is None:
+            self.pool = torch.cuda.graph_pool_handle()
+        s = torch.cuda.Stream(device=dev)
+        s.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(s):
-            self.step()
-        torch.cuda.current_stream(self.hist.device).wait_stream(s)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self.step()
+            self._step(*key)
+        torch.cuda.current_stream(dev).wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, pool=self.pool):
+            self._step(*key)
+        self.graphs[key] = g
+        self.u_ctr.copy_(ctr)
+        self._sync_live()
+        torch.cuda.synchronize(dev)
+        return key
 
     def replay(self):
-        self.graph.replay()
+        """One step through the captured graph of its bucket (captured on first use); steps
+        whose draft catch-up needs more than 2 rows run eagerly."""
+        key = self.bucket()
+        if key[3] != 2:
+            return self.step()
+        if key not in self.graphs:
+            self.capture(key)
+        self.graphs[key].replay()
+        self._finish(key)
+
+    # ---- views for inspection ------------------------------------------------------------
+    def state(self):
+        """Host copy of the live sequences' (tokens, num_computed = len - 1, draft_computed)."""
+        n, dc, hist = self.n.cpu().tolist(), self.dc.cpu().tolist(), self.hist.cpu()
+        return [(hist[b, : n[b]].tolist(), n[b] - 1, dc[b]) for b in range(self.B)]

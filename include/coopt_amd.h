@@ -220,10 +220,16 @@ int coopt_kv_copy_blocks(const int64_t* regions, int num_regions, const int64_t*
  *
  *   q      [T, Hq, D] bf16 (q_tok_stride, q_head_stride, 1);  out likewise (o_tok_stride, ...)
  *   kv_dtype COOPT_DT_BF16: caches bf16 [NB, block_size, Hkv, D], k_scale/v_scale unused
- *            COOPT_DT_I8:   caches int8 codes, k_scale/v_scale fp16 [NB, block_size, Hkv];
- *                           every element is dequantised in the kernel to
+ *            COOPT_DT_I8:   caches int8 codes, k_scale/v_scale fp16 [NB, block_size, Hkv].
+ *                           K: every code is dequantised in the kernel to
  *                           bf16(float(code) * float(scale)), the value dequantize() gives,
- *                           so the result equals the bf16 path on the dequantised cache.
+ *                           so the scores use the reference's operands.  V: the codes enter
+ *                           the PV product as exact fp16 integers and each key's V scale is
+ *                           folded into its probability, rounded once to fp16 as
+ *                           p * s_v * 2^-e (e a per-wave power of two that keeps the product
+ *                           in fp16's normal range for every fp16 scale).  The output is
+ *                           therefore not bit-equal to the bf16 path on the dequantised
+ *                           cache; it stays within the INT8 tolerance of attention over it.
  *   block_table [B, bt_stride] int32; entries past ceil(L/block_size) are never read.
  *   Supported: D in {64, 128}; (Hq/Hkv) * max_seqlen_q <= 64; block_size a power of two >= 16;
  *   B * Hkv <= 131072.  Callers must keep seq_lens <= max_seqlen_k, q rows per sequence

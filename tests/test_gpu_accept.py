@@ -191,7 +191,20 @@ def test_sample_and_softmax(dev):
     u = torch.rand(N, generator=gen, device=dev)
     tok, probs = M.sample(x, 0.7, uniforms=u)
     ref_tok, ref_p = OA.sample(x.cpu().numpy(), 0.7, u.cpu().numpy())
-    assert (tok.cpu().numpy() == ref_tok).sum() >= N - 1
+    # bit-exact tokens, except rows whose inverse-CDF boundary lies within 1e-6 (a tie by
+    # either side's margin), which are reported
+    res = M.accept(x, None, torch.empty((N, 0), dtype=torch.int32, device=dev), 0.7,
+                   u_resample=u)
+    assert torch.equal(res.tokens[:, 0].long(), tok)
+    _, _, ref_m = OA.accept_batch(x.cpu().numpy()[:, None], None, np.zeros((N, 0), np.int32),
+                                  0.7, None, u.cpu().numpy())
+    got_m = res.margin.cpu().numpy()
+    t = tok.cpu().numpy()
+    for i in range(N):
+        if t[i] != ref_tok[i]:
+            report(f"[sample] row {i}: kernel {t[i]} oracle {ref_tok[i]} margins "
+                   f"{got_m[i]:.3g} / {ref_m[i]:.3g}")
+            assert min(got_m[i], ref_m[i]) < TIE, f"row {i} differs outside a tie"
     assert torch.allclose(probs.cpu(), torch.from_numpy(ref_p), rtol=1e-5, atol=1e-12)
     tok_g, _ = M.sample(x, 1.0, generator=torch.Generator(device=dev).manual_seed(1))
     assert tok_g.shape == (N,) and int(tok_g.min()) >= 0 and int(tok_g.max()) < V

@@ -1,0 +1,122 @@
+"""GPU parity of the whole speculative step (config 5's step) against the oracle step.
+
+Each GPU step -- eager or a HIP-graph replay -- starts from a state the oracle copies
+(caches, histories, lengths, the step's row of the uniform table); oracle.spec_step then
+restates engine/engine.py:338-470 on the CPU, teacher-forced on the GPU step's logits, and
+oracle.step_check compares:
+  * decisions bit-exact (which sequences speculate, every draft token, accepted lengths,
+    emitted tokens), a decision within 1e-6 of its boundary reported as a tie and its
+    sequence no longer compared;
+  * histories, num_computed, draft_computed and the step counters exactly;
+  * the oracle's own logits within LOGIT_TOL (relative to the largest logit) of the GPU's,
+    and every cache entry the step wrote within KV_TOL, every other entry unchanged.
+Cases: tiny models with ragged gamma (0 .. gamma_max), a sequence made to lag by gamma 0 and
+then caught up (a stride-4 eager step), batch padding with dummy sequences, a retired
+sequence, greedy and sampled; and the config-5 widths (hidden 4096 / 2048, 32/8 heads, head
+dim 128 / 64, FFN 14336 / 8192, vocab 128256, INT8 target KV) at B=16, gamma 4, with two
+layers per model, through graph replays.
+"""
+import pytest
+import torch
+
+from iitj_llm_coopt_amd.spec_engine import (DRAFT_LLAMA32_1B, TARGET_LLAMA31_8B, LlamaShape,
+                                            RandomLlama, SpecDecoder)
+from oracle.step_check import StepChecker
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL, KV_TOL = 5e-2, 5e-2
+
+TINY_T = LlamaShape(hidden=256, ffn=512, layers=2, heads=4, kv_heads=2, head_dim=64, vocab=1000)
+TINY_D = LlamaShape(hidden=128, ffn=256, layers=1, heads=4, kv_heads=2, head_dim=64, vocab=1000,
+                    tie_embeddings=True)
+
+
+def report(msg):
+    print(msg, flush=True)
+
+
+def make(dev, tshape, dshape, B, gamma, P, steps, T, seed=0, std=0.02):
+    t = RandomLlama(tshape, dev, seed=seed + 1, std=std)
+    d = RandomLlama(dshape, dev, seed=seed + 2, std=std,
+                    packed=("qkv", "o", "gate_up", "down", "lm_head"))
+    dec = SpecDecoder(t, d, B, gamma, P, steps, temperature=T, seed=seed, max_catchup=16)
+    g = torch.Generator(device=dev).manual_seed(seed + 3)
+    prompts = torch.randint(0, tshape.vocab, (B, P), generator=g, device=dev)
+    dec.prefill(prompts, torch.rand(B, generator=g, device=dev))
+    return dec
+
+
+def checked_steps(dec, chk, schedule, graph):
+    """schedule: per step a gamma list (or int), or ("retire", slot)."""
+    for i, item in enumerate(schedule):
+        if isinstance(item, tuple) and item[0] == "retire":
+            dec.retire(item[1])
+            continue
+        dec.set_gamma(item)
+        chk.before()
+        report(f"[step {i}] bucket {dec.bucket()} gamma {dec.gamma} "
+               f"{'graph' if graph else 'eager'}")
+        dec.replay() if graph else dec.step()
+        torch.cuda.synchronize()
+        chk.after()
+    return chk.summary()
+
+
+RAGGED = [[4, 3, 0, 1, 4, 2], [4, 3, 0, 1, 4, 2], [2, 4, 0, 3, 1, 4],
+          [4, 4, 3, 4, 4, 4],            # slot 2 now lags by 3-4: catch-up of 2-3 tokens (S_c 4)
+          [1, 2, 3, 4, 0, 1], ("retire", 1), [3, 0, 4, 2, 4], [4, 4, 4, 4, 4],
+          ("retire", 0), [2, 3, 1, 4], [4, 4, 4, 4]]
+
+
+@pytest.mark.parametrize("T", [1.0, 0.0])
+@pytest.mark.parametrize("graph", [False, True])
+def test_ragged_bucketed_steps_match_the_oracle_step(dev, T, graph):
+    """B=6 in the 8-slot bucket (2 dummy sequences), then 5, then 4 (bucket 4, no dummies);
+    per-sequence gamma in 0..4, verify strides {1, 2, 3, 4, 5}; one sequence lags."""
+    dec = make(dev, TINY_T, TINY_D, B=6, gamma=4, P=24, steps=16, T=T, seed=3)
+    chk = StepChecker(dec, logit_tol=LOGIT_TOL, kv_tol=KV_TOL)
+    s = checked_steps(dec, chk, RAGGED, graph)
+    report(f"[ragged T={T} graph={graph}] {s}")
+    for line in chk.log:
+        report(f"  tie: {line}")
+    assert s["draft_tokens"] > 20 and s["accept_decisions"] > 40
+    assert s["diverged_sequences"] <= 1
+    if graph:
+        assert len(dec.graphs) >= 4, dec.graphs.keys()   # several (Bc, G) buckets replayed
+
+
+def test_graph_replay_equals_eager_step_bit_for_bit(dev):
+    """The same ragged schedule through graph replays and eager steps: identical histories,
+    lengths and logits (same kernels, same launch parameters)."""
+    a = make(dev, TINY_T, TINY_D, B=6, gamma=4, P=24, steps=16, T=1.0, seed=5)
+    b = make(dev, TINY_T, TINY_D, B=6, gamma=4, P=24, steps=16, T=1.0, seed=5)
+    for i, item in enumerate(RAGGED):
+        if isinstance(item, tuple):
+            a.retire(item[1])
+            b.retire(item[1])
+            continue
+        a.set_gamma(item)
+        b.set_gamma(item)
+        a.step()
+        b.replay()
+        torch.cuda.synchronize()
+        _ = torch.randn(1000, device=dev).sum().item()  # unrelated eager work between replays
+        Bc, G, S_t, _ = a.last_key
+        assert torch.equal(a.n, b.n) and torch.equal(a.dc, b.dc) and torch.equal(a.hist, b.hist), i
+        assert torch.equal(a.target_logits[: Bc * S_t], b.target_logits[: Bc * S_t]), i
+
+
+def test_config5_widths_match_the_oracle_step(dev):
+    """Config 5's model widths and vocabulary (2 layers each), B=16, gamma 4, T=1.0, INT8
+    target KV, bf16 draft KV; three graph-replayed steps and one ragged eager step."""
+    tshape = LlamaShape(**{**TARGET_LLAMA31_8B.__dict__, "layers": 2})
+    dshape = LlamaShape(**{**DRAFT_LLAMA32_1B.__dict__, "layers": 2})
+    dec = make(dev, tshape, dshape, B=16, gamma=4, P=64, steps=8, T=1.0, seed=11)
+    chk = StepChecker(dec, logit_tol=LOGIT_TOL, kv_tol=KV_TOL)
+    s = checked_steps(dec, chk, [4, 4, 4], graph=True)
+    s = checked_steps(dec, chk, [[4, 0, 2, 3] * 4], graph=False)
+    report(f"[config5 widths] {s}")
+    for line in chk.log:
+        report(f"  tie: {line}")
+    assert s["accept_decisions"] >= 60 and s["diverged_sequences"] <= 1
