@@ -244,8 +244,8 @@ class HipOps:
         B = seq_lens.numel()
         nb = workspace_bytes(B, q.shape[1], kc.shape[2], q.shape[2], S, max_k)
         ws = self.workspace(("attn", q.shape[2]), nb)
-        return paged_attention(q, kc, vc, cu, seq_lens, kv.block_table, S, max_k, scale, ks, vs,
-                               workspace=ws)
+        return paged_attention(q, kc, vc, cu, seq_lens, kv.block_table[:B], S, max_k, scale, ks,
+                               vs, workspace=ws)
 
     def sample(self, logits, u, temperature, out=None):
         """One token per row: inverse-CDF draw from softmax(logits / T) (argmax if T <= 0)."""

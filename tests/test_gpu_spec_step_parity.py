@@ -47,8 +47,9 @@ def make(dev, tshape, dshape, B, gamma, P, steps, T, seed=0, std=0.02):
     return dec
 
 
-def checked_steps(dec, chk, schedule, graph):
-    """schedule: per step a gamma list (or int), or ("retire", slot)."""
+def checked_steps(dec, chk, schedule, graph, keys=None):
+    """schedule: per step a gamma list (or int), or ("retire", slot).  Appends each step's
+    bucket to `keys`."""
     for i, item in enumerate(schedule):
         if isinstance(item, tuple) and item[0] == "retire":
             dec.retire(item[1])
@@ -60,13 +61,17 @@ def checked_steps(dec, chk, schedule, graph):
         dec.replay() if graph else dec.step()
         torch.cuda.synchronize()
         chk.after()
+        if keys is not None:
+            keys.append(dec.last_key)
     return chk.summary()
 
 
-RAGGED = [[4, 3, 0, 1, 4, 2], [4, 3, 0, 1, 4, 2], [2, 4, 0, 3, 1, 4],
+# per-step gamma of each live slot (G = the largest: verify stride S_t = G + 1 here)
+RAGGED = [[4, 3, 0, 1, 4, 2], [4, 3, 0, 1, 4, 2], [2, 1, 0, 2, 1, 2],
           [4, 4, 3, 4, 4, 4],            # slot 2 now lags by 3-4: catch-up of 2-3 tokens (S_c 4)
-          [1, 2, 3, 4, 0, 1], ("retire", 1), [3, 0, 4, 2, 4], [4, 4, 4, 4, 4],
-          ("retire", 0), [2, 3, 1, 4], [4, 4, 4, 4]]
+          [1, 1, 1, 1, 0, 1], ("retire", 1),
+          [0, 0, 0, 0, 0],               # plain decoding (S_t 1); every lag grows by one
+          [3, 0, 3, 2, 3], [4, 4, 4, 4, 4], ("retire", 0), [2, 3, 1, 4], [4, 4, 4, 4]]
 
 
 @pytest.mark.parametrize("T", [1.0, 0.0])
@@ -76,14 +81,18 @@ def test_ragged_bucketed_steps_match_the_oracle_step(dev, T, graph):
     per-sequence gamma in 0..4, verify strides {1, 2, 3, 4, 5}; one sequence lags."""
     dec = make(dev, TINY_T, TINY_D, B=6, gamma=4, P=24, steps=16, T=T, seed=3)
     chk = StepChecker(dec, logit_tol=LOGIT_TOL, kv_tol=KV_TOL)
-    s = checked_steps(dec, chk, RAGGED, graph)
-    report(f"[ragged T={T} graph={graph}] {s}")
+    keys = []
+    s = checked_steps(dec, chk, RAGGED, graph, keys)
+    report(f"[ragged T={T} graph={graph}] {s}; buckets {keys}")
     for line in chk.log:
         report(f"  tie: {line}")
     assert s["draft_tokens"] > 20 and s["accept_decisions"] > 40
     assert s["diverged_sequences"] <= 1
+    assert {k[2] for k in keys} == {1, 2, 3, 4, 5} and {k[0] for k in keys} == {4, 8}
+    assert sum(k[3] > 2 for k in keys) >= 2          # lagging catch-ups ran eagerly
     if graph:
-        assert len(dec.graphs) >= 4, dec.graphs.keys()   # several (Bc, G) buckets replayed
+        # one graph per bucket with the stride-2 catch-up, replayed
+        assert set(dec.graphs) == {k for k in keys if k[3] == 2}, dec.graphs.keys()
 
 
 def test_graph_replay_equals_eager_step_bit_for_bit(dev):
