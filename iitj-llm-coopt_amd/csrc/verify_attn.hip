@@ -304,15 +304,15 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
     }
   };
   // a full tile: every key < L
+  // INT8: the scales are issued first, so the V-scale check of a loaded tile (vcheck) waits
+  // only for them and leaves the tile's K/V loads in flight.
   auto load_full = [&](Raw& raw, int t, int64_t pg0, int64_t pg1) {
     const int kb = k_begin + t * kTileKeys;
+    if constexpr (INT8) {
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      const int64_t pg = kt ? pg1 : pg0;
-      const int tok0 = (kb + kt * 16) & bs_mask;
-      const int64_t r = pg * a.c_bs + head_off + static_cast<int64_t>(tok0) * c_ts;
-      issue(raw, kt, kbase + kElt * r, vbase + kElt * r, k_lane, v_lane);
-      if constexpr (INT8) {
+      for (int kt = 0; kt < 2; ++kt) {
+        const int64_t pg = kt ? pg1 : pg0;
+        const int tok0 = (kb + kt * 16) & bs_mask;
         const uint16_t* ksp = a.ks + pg * a.s_bs + shead_off;
         const uint16_t* vsp = a.vs + pg * a.s_bs + shead_off;
         if constexpr (SC) {
@@ -328,6 +328,13 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
           raw.vs[kt] = u32x2_t{vh[0] | (vh[1] << 16), vh[2] | (vh[3] << 16)};
         }
       }
+    }
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const int64_t pg = kt ? pg1 : pg0;
+      const int tok0 = (kb + kt * 16) & bs_mask;
+      const int64_t r = pg * a.c_bs + head_off + static_cast<int64_t>(tok0) * c_ts;
+      issue(raw, kt, kbase + kElt * r, vbase + kElt * r, k_lane, v_lane);
     }
   };
   // the split's last tile when it ends inside a tile: keys clamped to L - 1
@@ -359,20 +366,14 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
     }
   };
 
-  auto compute_tile = [&](const Raw& raw, int t) {
-    const int kb = k_begin + t * kTileKeys;
-    // every key of the tile inside the split and visible to every row: no masking
-    const bool open = kb + kTileKeys <= k_end && kb + kTileKeys - 1 <= min_lim;
-    auto scale_of = [&](const u32x2_t& w, int i) {
-      return f16_to_f32(static_cast<uint16_t>(w[i >> 1] >> (16 * (i & 1))));
-    };
-
-    // INT8: keep fp16(p * s_v * 2^-e_v) in range.  p <= 2^kSlack = 2^8, so every V scale must
-    // stay at or below 2^(e_v + 7) (products <= 2^15 < 65504).  The first positive scale, or
-    // one above that bound, moves e_v so that the tile's largest scale lands in [2^6, 2^7),
-    // and o and l are rescaled by the change (one uniform branch, taken O(log range) times
-    // per wave).  Scales are non-negative fp16, so their bit patterns order them; non-finite
-    // patterns count as the largest finite scale.
+  // INT8: keep fp16(p * s_v * 2^-e_v) in range.  p <= 2^kSlack = 2^8, so every V scale must
+  // stay at or below 2^(e_v + 7) (products <= 2^15 < 65504).  The first positive scale, or
+  // one above that bound, moves e_v so that the tile's largest scale lands in [2^6, 2^7),
+  // and o and l are rescaled by the change (one uniform branch, taken O(log range) times
+  // per wave).  Scales are non-negative fp16, so their bit patterns order them; non-finite
+  // patterns count as the largest finite scale.  Run on a tile before it is computed, at the
+  // end of the previous tile's compute, where that tile's registers are free.
+  auto vcheck = [&](const Raw& raw) {
     if constexpr (INT8) {
       const uint32_t wv = max_u16x2(max_u16x2(raw.vs[0][0], raw.vs[0][1]),
                                     max_u16x2(raw.vs[1][0], raw.vs[1][1]));
@@ -397,11 +398,22 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
         ev_set = true;
       }
     }
+  };
 
-    // ---- V^T operands, built first: they do not depend on the scores, so their VALU work
-    // is scheduled alongside the score MFMAs in one basic block ----
+  auto compute_tile = [&](const Raw& raw, int t) {
+    const int kb = k_begin + t * kTileKeys;
+    // every key of the tile inside the split and visible to every row: no masking
+    const bool open = kb + kTileKeys <= k_end && kb + kTileKeys - 1 <= min_lim;
+    auto scale_of = [&](const u32x2_t& w, int i) {
+      return f16_to_f32(static_cast<uint16_t>(w[i >> 1] >> (16 * (i & 1))));
+    };
+
+    // ---- V^T operands.  They do not depend on the scores: up to 32 rows they are built
+    // first, so their VALU work is scheduled alongside the score MFMAs in one basic block;
+    // at 48 rows and more they are built after the softmax, which keeps them out of the
+    // score phase's registers ----
     u32x4_t va[kDt];
-    {
+    auto build_va = [&]() {
       uint32_t vx[8][Raw::kVWords];
 #pragma unroll
       for (int j = 0; j < 8; ++j)
@@ -433,7 +445,9 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
             va[dt][e2] = __builtin_amdgcn_perm(vx[j1][w], vx[j0][w], (dt & 1) ? 0x07060302u : 0x05040100u);
           }
       }
-    }
+    };
+    constexpr bool kVFirst = RT <= 2;
+    if constexpr (kVFirst) build_va();
 
     // ---- scores: S^T = K . Q^T, K operands built per k-step ----
     f32x4_t acc[RT][2];
@@ -547,6 +561,8 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
       }
     }
 
+    if constexpr (!kVFirst) build_va();
+
     // ---- O^T += V^T . P^T ----
 #pragma unroll
     for (int dt = 0; dt < kDt; ++dt)
@@ -578,16 +594,19 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
       pages(t, p0, p1);
       load_full(bufA, t, p0, p1);
       pages(min(t + kWaves, tlast), nx0, nx1);
+      vcheck(bufA);
     }
     for (; t < nfull; t += 2 * kWaves) {
       const int t1 = t + kWaves, t2 = t1 + kWaves;
       load_full(bufB, min(t1, tlast), nx0, nx1);
       pages(min(t2, tlast), nx0, nx1);
       compute_tile(bufA, t);
+      vcheck(bufB);
       if (t1 >= nfull) break;
       load_full(bufA, min(t2, tlast), nx0, nx1);
       pages(min(t2 + kWaves, tlast), nx0, nx1);
       compute_tile(bufB, t1);
+      vcheck(bufA);
     }
   } else {
     Raw buf;
@@ -596,6 +615,7 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
     for (int t = wave; t < nfull; t += kWaves) {
       load_full(buf, t, nx0, nx1);
       if (t + kWaves < nfull) pages(t + kWaves, nx0, nx1);
+      vcheck(buf);
       compute_tile(buf, t);
     }
   }
@@ -604,6 +624,7 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
     int64_t p0, p1;
     pages(nfull, p0, p1);
     load_partial(buf, nfull, p0, p1);
+    vcheck(buf);
     compute_tile(buf, nfull);
   }
   __syncthreads();  // Q in LDS is dead; the merge below reuses the space
