@@ -8,14 +8,17 @@ Workload (BASELINE.json config 5 at the metric's B=32): random-init Llama-3.1-8B
 paged INT8 KV cache, Llama-3.2-1B-shaped draft (16 layers, hidden 2048, head_dim 64, FFN 8192,
 tied embeddings) with a paged bf16 KV cache; B prompts of 1024 seeded uniform-random ids are
 prefilled, then each timed step is one HIP-graph replay of: draft catch-up + gamma draft
-proposals (temperature 1.0), one (gamma+1)-row target verify forward, the fused accept kernel
-and the length/history update.  value = tokens emitted by the accept step (sum of k_b + 1) per
-second over the timed steps.
+proposals (temperature 1.0, draws from the decoder's seeded uniform table), one (gamma+1)-row
+target verify forward, the fused accept kernel and the length/history update.  value = tokens
+emitted by the accept step (sum of k_b + 1) per second over the timed steps; also reported:
+scored positions/s (B (gamma+1) per step) and config 5's stated B=16.
 
 Printed: one JSON line (the driver's contract) with `roofline` for the verify-attention kernel
 (40 back-to-back launches between HIP events on torch's current stream, the stream the kernels
-run on, averaged per launch) and `cpu_baseline` (the same step, from the same state, on the
-host cores through oracle ops).
+run on, averaged per launch) and `cpu_baseline`: the reference's step restated on the host
+(oracle.spec_step) from the GPU run's state, at every core and at 8 threads, each step checked
+against the GPU step it shadows.  The kernel cases of configs 1-4 carry `cpu` legs: the
+reference's verify loop, quantize + index_put and textbook paged attention on the host.
 """
 import argparse
 import json
@@ -45,8 +48,12 @@ def parse():
     ap.add_argument("--gamma", type=int, default=4)
     ap.add_argument("--prompt", type=int, default=1024)
     ap.add_argument("--temperature", type=float, default=1.0)
-    ap.add_argument("--cpu-steps", type=int, default=5)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-steps", type=int, default=4,
+                    help="steps of the CPU baseline (half at all threads, half at 8)")
+    ap.add_argument("--b16-steps", type=int, default=20,
+                    help="timed steps of config 5's stated B=16 (0: skip)")
+    ap.add_argument("--no-cpu", action="store_true",
+                    help="skip the CPU baseline leg and the configs' CPU legs")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-tune-gemm", action="store_true",
                     help="skip PyTorch TunableOp selection of the decode-shape GEMMs")
@@ -105,7 +112,57 @@ def rate(res, nbytes, avg, med):
     return res
 
 
-def attention_case(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128):
+CPU_LEGS = {"on": True}   # main() turns the configs' CPU legs off with --no-cpu
+
+
+def cpu_legs(torch, fn, reps=3):
+    """Median wall time of fn() on the host cores, at torch's default thread count (every
+    core this process may use) and at 8 threads (the reference's OMP_NUM_THREADS,
+    runpod/setup.sh:23).  One untimed call first."""
+    out = {}
+    n_all = torch.get_num_threads()
+    for label, n in (("all_cores", n_all), ("threads_8", 8)):
+        torch.set_num_threads(n)
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        out[label] = {"seconds": sorted(ts)[len(ts) // 2], "threads": n}
+    torch.set_num_threads(n_all)
+    out["affinity_cores"] = len(os.sched_getaffinity(0))
+    return out
+
+
+def cpu_attention(torch, q, kc, vc, ks, vs, table, seq, qlen, seqs, D):
+    """Textbook paged attention on the host (FlashAttention has no CPU path): per sequence,
+    gather its pages, dequantise INT8 to bf16 (dequantize(), engine/kv_tier_manager.py:34-41),
+    softmax(scale * q K^T + bottom-right causal mask) V in fp32."""
+    import math
+
+    out = torch.empty(len(seqs) * qlen, q.shape[1], D, dtype=torch.bfloat16)
+    Hkv = kc.shape[2]
+    G = q.shape[1] // Hkv
+    for i, b in enumerate(seqs):
+        L = int(seq[b])
+        pos = torch.arange(L)
+        blk, off = table[b].long()[pos // 16], pos % 16
+        if ks is None:
+            K, V = kc[blk, off].float(), vc[blk, off].float()
+        else:
+            K = (kc[blk, off].float() * ks[blk, off].float().unsqueeze(-1)).to(torch.bfloat16).float()
+            V = (vc[blk, off].float() * vs[blk, off].float().unsqueeze(-1)).to(torch.bfloat16).float()
+        Q = q[b * qlen:(b + 1) * qlen].float().view(qlen, Hkv, G, D).permute(1, 0, 2, 3).reshape(Hkv, qlen * G, D)
+        sc = torch.matmul(Q, K.permute(1, 2, 0)) / math.sqrt(D)
+        lim = torch.repeat_interleave(L - qlen + torch.arange(qlen), G)
+        sc = sc.masked_fill(torch.arange(L)[None, None, :] > lim[None, :, None], float("-inf"))
+        o = torch.matmul(torch.softmax(sc, -1), V.permute(1, 0, 2))
+        out[i * qlen:(i + 1) * qlen] = o.view(Hkv, qlen, G, D).permute(1, 0, 2, 3).reshape(qlen, -1, D)
+    return out
+
+
+def attention_case(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128, cpu_sample=0):
     """Verify attention over len(ctx) sequences with ctx[b] cached tokens and q_len new rows
     each (seq_len = ctx + q_len), Hq 32 / Hkv 8, head size D (128: the target; 64: the draft),
     block size 16, block tables a seeded permutation of a shared pool.  K/V are N(0,1) with 1%
@@ -148,9 +205,26 @@ def attention_case(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128):
     def fn():
         M.paged_attention(q, kc, vc, cu, sl, table, qlen, max_k, D ** -0.5, ks, vs, out, ws)
 
+    cpu_sample = cpu_sample if CPU_LEGS["on"] else 0
+
     res = {"kv": kv_dtype, "head_dim": D, "batch": B, "q_len": qlen, "ctx_min": int(ctx.min()),
            "ctx_max": int(ctx.max()), "ctx_mean": float(ctx.mean())}
-    return rate(res, nbytes, *time_launches(torch, dev, fn))
+    res = rate(res, nbytes, *time_launches(torch, dev, fn))
+    if cpu_sample:
+        # the same call on the host cores over the first cpu_sample sequences, scaled to the
+        # batch by their share of the keys
+        seqs = list(range(min(cpu_sample, B)))
+        hc = [None if t is None else t.cpu() for t in (kc, vc, ks, vs)]
+        hq, ht = q.cpu(), table.cpu()
+        legs = cpu_legs(torch, lambda: cpu_attention(torch, hq, *hc, ht, seq, qlen, seqs, D), reps=1)
+        share = float(seq[seqs].sum()) / float(seq.sum())
+        for k in ("all_cores", "threads_8"):
+            legs[k]["us_per_call"] = legs[k]["seconds"] / share * 1e6
+        got = cpu_attention(torch, hq, *hc, ht, seq, qlen, seqs[:2], D).float()
+        legs["max_abs_vs_gpu_first_2_seqs"] = float((got - out[: 2 * qlen].float().cpu()).abs().max())
+        legs["sample"] = f"{len(seqs)} of {B} sequences ({share:.1%} of the keys), fp32 torch on the host"
+        res["cpu"] = legs
+    return res
 
 
 def accept_case(torch, M, dev, B, gamma, V, seed):
@@ -170,7 +244,26 @@ def accept_case(torch, M, dev, B, gamma, V, seed):
         M.accept(tl, dl, dt32, 1.0, ua, ur, out=res, workspace=ws)
 
     nbytes = B * (2 * gamma + 1) * V * 4 + B * 2 * V * 4
-    return rate({"batch": B, "gamma": gamma, "vocab": V}, nbytes, *time_launches(torch, dev, fn))
+    res = rate({"batch": B, "gamma": gamma, "vocab": V}, nbytes, *time_launches(torch, dev, fn))
+    if CPU_LEGS["on"]:
+        # engine/engine.py:437-446 on the host: per sequence, the draft softmax the engine
+        # keeps from sample() and the reference's verify lines (engine/spec_decode.py:37-49)
+        # executed by torch-CPU with the same uniforms
+        from oracle import accept as OA
+        htl, hdl, hdt, hua, hur = (t.cpu() for t in (tl, dl, dt, ua, ur))
+
+        def loop():
+            return [OA.verify_torch(htl[b], hdt[b].tolist(), torch.softmax(hdl[b], -1), 1.0,
+                                    hua[b], float(hur[b])) for b in range(B)]
+        legs = cpu_legs(torch, loop)
+        for k in ("all_cores", "threads_8"):
+            legs[k]["us_per_call"] = legs[k]["seconds"] * 1e6
+        got = M.accept(tl, dl, dt32, 1.0, ua, ur).to_lists()
+        ref = loop()
+        legs["sequences_equal_to_gpu"] = sum(a == b for a, b in zip(got, ref))
+        legs["sample"] = f"the whole batch: {B} sequences, torch-CPU"
+        res["cpu"] = legs
+    return res
 
 
 def kv_write_case(torch, M, dev, T, seed):
@@ -191,7 +284,31 @@ def kv_write_case(torch, M, dev, T, seed):
         M.reshape_and_cache_flash(k, v, kc, vc, slots, "int8", ks, vs)
 
     nbytes = T * Hkv * D * (2 * 2 + 2 * 1) + T * Hkv * 2 * 2 + T * 8
-    return rate({"tokens": T}, nbytes, *time_launches(torch, dev, fn))
+    res = rate({"tokens": T}, nbytes, *time_launches(torch, dev, fn))
+    if CPU_LEGS["on"] and T <= 4096:
+        # the reference's quantize lines (engine/kv_tier_manager.py:21-31) on torch-CPU and
+        # the index_put write (engine/model.py:201-203) into host caches of the same pool
+        from oracle import codec as OC
+        hk, hv, hs = k.cpu(), v.cpu(), slots.cpu()
+        ck = torch.zeros(NB, bs, Hkv, D, dtype=torch.int8)
+        cv = torch.zeros_like(ck)
+        sk = torch.zeros(NB, bs, Hkv, dtype=torch.float16)
+        sv = torch.zeros_like(sk)
+        blk, off = hs // bs, hs % bs
+
+        def write():
+            for x, c, sc in ((hk, ck, sk), (hv, cv, sv)):
+                qx, s_ = OC.quantize_torch_cpu(x, 8)
+                c[blk, off] = qx
+                sc[blk, off] = s_
+        legs = cpu_legs(torch, write)
+        for kk in ("all_cores", "threads_8"):
+            legs[kk]["us_per_call"] = legs[kk]["seconds"] * 1e6
+        write()
+        legs["codes_equal_to_gpu"] = bool(torch.equal(ck[blk, off], kc[slots // bs, slots % bs].cpu()))
+        legs["sample"] = f"the whole call: {T} tokens, torch-CPU"
+        res["cpu"] = legs
+    return res
 
 
 def kv_swap_case(torch, M, dev, seed, tokens=4096, bits=8):
@@ -362,11 +479,11 @@ KERNEL_CASES = {
     "attention_int8": lambda t, M, d, s: attention_case(t, M, d, [8192] * 32, 5, "int8", s),
     "attention_bf16": lambda t, M, d, s: attention_case(t, M, d, [8192] * 32, 5, "auto", s),
     # config 3: bf16, B=32, ctx U[512, 4096], q_len 5
-    "attention_config3": lambda t, M, d, s: attention_case(t, M, d, config_ctx(s, 32, 512, 4096), 5, "auto", s),
+    "attention_config3": lambda t, M, d, s: attention_case(t, M, d, config_ctx(s, 32, 512, 4096), 5, "auto", s, cpu_sample=32),
     # config 4: INT8, B=64, ctx U[4096, 16384], gamma 2 / 4 / 8
-    "attention_config4_g2": lambda t, M, d, s: attention_case(t, M, d, config_ctx(s, 64, 4096, 16384), 3, "int8", s),
-    "attention_config4_g4": lambda t, M, d, s: attention_case(t, M, d, config_ctx(s, 64, 4096, 16384), 5, "int8", s),
-    "attention_config4_g8": lambda t, M, d, s: attention_case(t, M, d, config_ctx(s, 64, 4096, 16384), 9, "int8", s),
+    "attention_config4_g2": lambda t, M, d, s: attention_case(t, M, d, config_ctx(s, 64, 4096, 16384), 3, "int8", s, cpu_sample=8),
+    "attention_config4_g4": lambda t, M, d, s: attention_case(t, M, d, config_ctx(s, 64, 4096, 16384), 5, "int8", s, cpu_sample=8),
+    "attention_config4_g8": lambda t, M, d, s: attention_case(t, M, d, config_ctx(s, 64, 4096, 16384), 9, "int8", s, cpu_sample=8),
     # the bench step's own attention launches (prompt 1024 + the tokens of the timed steps):
     # target verify (INT8, q_len 5), draft proposals (bf16, D 64, 1 row) and catch-up (2 rows)
     "attention_step_target": lambda t, M, d, s: attention_case(t, M, d, [1100] * 32, 5, "int8", s),
@@ -559,27 +676,80 @@ def summarize(paths):
 
 
 def cpu_baseline(torch, dec, steps):
-    """The same speculative step from the same state, on the host cores, through oracle ops
-    (the reference's algorithm restated on the CPU).  Bounded sample: `steps` steps."""
-    from oracle.step_ops import OracleOps
+    """The reference's step on the host cores, checked against the GPU step it shadows.
+
+    For each of `steps` steps (the first half at torch's default thread count, i.e. every core
+    this process may use, the rest at 8 threads, the reference's OMP_NUM_THREADS), the GPU runs
+    one eager step from the decoder's state and oracle.spec_step runs the same step on the
+    host from a copy of that state and the same row of the uniform table: the reference's
+    engine step (engine/engine.py:338-470) with a bf16 torch-CPU Llama, INT8 KV quantised on
+    write, fp32 paged attention and explicit-uniform sampling, teacher-forced on the GPU's
+    logits so that every decision is compared (oracle.step_check).  Reported: tokens emitted
+    per second of oracle step time at each thread count, and the agreement counts."""
+    from oracle.step_check import StepChecker
 
     t0 = time.perf_counter()
-    cpu = dec.to("cpu", OracleOps())
-    log(f"cpu baseline: state copied to host in {time.perf_counter() - t0:.1f}s")
-    e0 = int(cpu.emitted)
-    t0 = time.perf_counter()
+    chk = StepChecker(dec, logit_tol=None, kv_tol=None)   # differences reported
+    log(f"cpu baseline: weights copied to host in {time.perf_counter() - t0:.1f}s")
+    n_all = torch.get_num_threads()
+    legs = {"all_cores": [0, 0.0, n_all], "threads_8": [0, 0.0, 8]}
+    for i in range(steps):
+        leg = "all_cores" if i < (steps + 1) // 2 else "threads_8"
+        torch.set_num_threads(legs[leg][2])
+        chk.before()
+        dec.step()
+        torch.cuda.synchronize()
+        e0 = sum(len(s.tokens) for s in chk.seqs)
+        secs = chk.after()
+        legs[leg][0] += sum(len(s.tokens) for s in chk.seqs) - e0
+        legs[leg][1] += secs
+        log(f"cpu baseline step {i} ({legs[leg][2]} threads): {secs:.2f}s")
+    torch.set_num_threads(n_all)
+    agree = chk.summary()
+    v = {k: (toks / secs if secs else None) for k, (toks, secs, _) in legs.items()}
+    return {"value": v["all_cores"], "unit": "tokens/s", "cores": n_all, "kind": "port",
+            "sample": f"{steps} speculative steps of the same B={dec.B}, gamma={dec.g} batch "
+                      f"from the GPU run's state ({(steps + 1) // 2} at {n_all} threads, the rest "
+                      f"at 8): oracle.spec_step on the host (bf16 torch-CPU Llama, INT8 KV "
+                      f"quantised on write, fp32 paged attention, explicit-uniform sampling), "
+                      f"each step checked against the GPU step from the same state",
+            "seconds": legs["all_cores"][1], "affinity_cores": len(os.sched_getaffinity(0)),
+            "threads_8": {"value": v["threads_8"], "seconds": legs["threads_8"][1]},
+            "agreement": agree}
+
+
+def run_step_bench(torch, dec, steps, warmup, tune):
+    """Prefilled decoder -> (seconds over `steps` graph replays, emitted, drafted, accepted)."""
+    dev = dec.hist.device
+    if tune:
+        # Pick the hipBLASLt/rocBLAS solution of each decode-shape GEMM by timing (PyTorch
+        # TunableOp), during an eager step, i.e. after prefill and before capture.
+        t0 = time.perf_counter()
+        torch.cuda.tunable.enable(True)
+        torch.cuda.tunable.tuning_enable(True)
+        torch.cuda.tunable.set_max_tuning_duration(50)
+        torch.cuda.tunable.set_filename(os.path.join(os.environ.get("TMPDIR", "/tmp"),
+                                                     "coopt_tunableop_%d.csv"))
+        dec.step()
+        torch.cuda.synchronize(dev)
+        torch.cuda.tunable.tuning_enable(False)
+        log(f"GEMM tuning step in {time.perf_counter() - t0:.1f}s")
+    dec.step()                       # eager warm-up (allocates workspaces)
+    dec.capture()                    # one HIP graph for the step's bucket
+    for _ in range(warmup):
+        dec.replay()
+    torch.cuda.synchronize(dev)
+    e0, d0, a0 = int(dec.emitted), int(dec.drafted), int(dec.accepted)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(1)  # marker kernel (spin_kernel) bracketing the timed steps in traces
+    start.record()
     for _ in range(steps):
-        cpu.step()
-    dt = time.perf_counter() - t0
-    toks = int(cpu.emitted) - e0
-    return {"value": toks / dt, "unit": "tokens/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"{steps} speculative step(s) of the same B={dec.B}, gamma={dec.g} batch "
-                      f"from the GPU run's prefilled state: torch-CPU bf16 model, oracle INT8 "
-                      f"KV write, fp32 paged attention over the dequantised cache, oracle "
-                      f"inverse-CDF sampling and rejection sampling; {toks} tokens in "
-                      f"{dt:.1f}s", "seconds": dt,
-            "affinity_cores": len(os.sched_getaffinity(0))}
+        dec.replay()
+    end.record()
+    torch.cuda._sleep(1)
+    torch.cuda.synchronize(dev)
+    secs = start.elapsed_time(end) * 1e-3
+    return secs, int(dec.emitted) - e0, int(dec.drafted) - d0, int(dec.accepted) - a0
 
 
 def main():
@@ -600,6 +770,7 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.manual_seed(args.seed)
+    CPU_LEGS["on"] = not args.no_cpu
     if args.kernels_only:
         names = args.case or sorted(KERNEL_CASES)
         print(json.dumps(run_kernel_cases(torch, M, dev, names, args.seed)), flush=True)
@@ -618,40 +789,24 @@ def main():
     dec.prefill(prompts, torch.rand(B, generator=gen, device=dev))
     log(f"prefill of {B}x{P} tokens in {time.perf_counter() - t0:.1f}s")
 
-    tuned = False
-    if not args.no_tune_gemm:
-        # Pick the hipBLASLt/rocBLAS solution of each decode-shape GEMM by timing (PyTorch
-        # TunableOp), during the eager warm-up step, i.e. after prefill and before capture.
-        t0 = time.perf_counter()
-        torch.cuda.tunable.enable(True)
-        torch.cuda.tunable.tuning_enable(True)
-        torch.cuda.tunable.set_max_tuning_duration(50)
-        torch.cuda.tunable.set_filename(os.path.join(os.environ.get("TMPDIR", "/tmp"),
-                                                     "coopt_tunableop_%d.csv"))
-        dec.step()
-        torch.cuda.synchronize(dev)
-        torch.cuda.tunable.tuning_enable(False)
-        tuned = True
-        log(f"GEMM tuning step in {time.perf_counter() - t0:.1f}s")
-    dec.step()                       # eager warm-up (allocates workspaces)
-    dec.capture()                    # then one HIP graph per step
-    for _ in range(args.warmup):
-        dec.replay()
-    torch.cuda.synchronize(dev)
-    e0, d0, a0 = int(dec.emitted), int(dec.drafted), int(dec.accepted)
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize(dev)
-    torch.cuda._sleep(1)  # marker kernel (spin_kernel) bracketing the timed steps in traces
-    start.record()
-    for _ in range(args.steps):
-        dec.replay()
-    end.record()
-    torch.cuda._sleep(1)
-    torch.cuda.synchronize(dev)
-    secs = start.elapsed_time(end) * 1e-3
-    emitted = int(dec.emitted) - e0
-    acc_rate = (int(dec.accepted) - a0) / max(1, int(dec.drafted) - d0)
+    tuned = not args.no_tune_gemm
+    secs, emitted, drafted, accepted = run_step_bench(torch, dec, args.steps, args.warmup, tuned)
+    acc_rate = accepted / max(1, drafted)
     log(f"{args.steps} steps in {secs * 1e3:.1f} ms: {emitted} tokens, acceptance {acc_rate:.3f}")
+
+    b16 = None
+    if args.b16_steps and B != 16:
+        # config 5 as stated (B=16): a second decoder over the same weights
+        d16 = SpecDecoder(target, draft, 16, g, P, max_steps=args.warmup + args.b16_steps + 2,
+                          temperature=args.temperature, seed=args.seed)
+        d16.prefill(prompts[:16], torch.rand(16, generator=gen, device=dev))
+        s16, e16, dr16, a16 = run_step_bench(torch, d16, args.b16_steps, args.warmup, False)
+        b16 = {"batch": 16, "steps": args.b16_steps, "ms_per_step": s16 / args.b16_steps * 1e3,
+               "tokens_per_s": e16 / s16, "scored_positions_per_s": 16 * (g + 1) * args.b16_steps / s16,
+               "acceptance_rate": a16 / max(1, dr16)}
+        log(f"B=16: {b16['ms_per_step']:.2f} ms/step, {b16['tokens_per_s']:.0f} tokens/s")
+        del d16
+        torch.cuda.empty_cache()
 
     # kernel-level measurements (HIP events per call, torch's current stream)
     kern, att_i8 = {}, None
@@ -662,7 +817,8 @@ def main():
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(torch, dec, args.cpu_steps)
-        log(f"cpu baseline {cpu['value']:.2f} tokens/s on {cpu['cores']} threads")
+        log(f"cpu baseline {cpu['value']:.2f} tokens/s on {cpu['cores']} threads, "
+            f"{cpu['threads_8']['value']:.2f} on 8; agreement {cpu['agreement']}")
 
     out = {
         "metric": METRIC,
@@ -696,6 +852,8 @@ def main():
         "cpu_baseline": cpu,
         "acceptance_rate": acc_rate,
         "tokens_per_step": emitted / args.steps,
+        "scored_positions_per_s": B * (g + 1) * args.steps / secs,
+        "config5_b16": b16,
         "kernels": kern,
     }
     print(json.dumps(out), flush=True)

@@ -12,8 +12,11 @@ step's row of the uniform table, copied to the host):
   logits      the oracle's own logits (its bf16 torch-CPU forward) against the GPU's: the
               largest difference, relative to the largest logit, within `logit_tol`;
   KV cache    the GPU step changed no cache entry outside the slots the oracle wrote, and
-              the written entries are within `kv_tol` of the oracle's (bf16: relative;
-              INT8: dequantised values within kv_tol * 127 scales... see _kv_error).
+              the written entries are within `kv_tol` of the oracle's (bf16: relative to
+              max(1, |value|); INT8: dequantised values relative to the vector's range,
+              127 * scale).
+A tolerance of None reports the largest difference without asserting on it (a deep model's
+bf16 rounding differences grow with depth; decisions are compared either way).
 The forward is not bit-reproducible across GEMM implementations (MFMA partial sums against a
 CPU GEMM), so logits and caches are compared with a tolerance and the decisions are compared
 bit-exactly from the same logits.
@@ -174,7 +177,8 @@ class StepChecker:
             err = float((mine - ref).abs().max() / max(1.0, float(ref.abs().max())))
             key = "logit_err_draft" if stage == "draft" else "logit_err_target"
             self.worst[key] = max(self.worst[key], err)
-            assert err <= self.logit_tol, f"{stage} {i}: logits differ by {err:.3g} (relative)"
+            assert self.logit_tol is None or err <= self.logit_tol, \
+                f"{stage} {i}: logits differ by {err:.3g} (relative)"
             agree = (mine.argmax(-1) == ref.argmax(-1)).float().mean().item()
             st[key.replace("err", "argmax_rows")] += mine.shape[0]
             st[key.replace("err", "argmax_agree")] += round(agree * mine.shape[0])
@@ -202,7 +206,7 @@ class StepChecker:
                 o, g = flat(orc[j])[w].float(), flat(post[j])[w].float()
                 err = float(((o - g).abs() / o.abs().clamp(min=1.0)).max()) if o.numel() else 0.0
                 self.worst[f"kv_err_{name}"] = max(self.worst[f"kv_err_{name}"], err)
-                assert err <= self.kv_tol, f"{name} layer {li}: KV differs by {err:.3g}"
+                assert self.kv_tol is None or err <= self.kv_tol, f"{name} layer {li}: KV differs by {err:.3g}"
         else:                    # INT8: dequantised values, relative to each vector's range
             for j in range(2):
                 oq, os_ = flat(orc[j])[w].float(), flat(orc[j + 2])[w].float()
@@ -211,7 +215,8 @@ class StepChecker:
                 rng = (os_ * 127).clamp(min=1e-6).unsqueeze(-1)
                 err = float(((od - gd).abs() / rng).max()) if od.numel() else 0.0
                 self.worst[f"kv_err_{name}"] = max(self.worst[f"kv_err_{name}"], err)
-                assert err <= self.kv_tol, f"{name} layer {li}: INT8 KV differs by {err:.3g}"
+                assert self.kv_tol is None or err <= self.kv_tol, \
+                    f"{name} layer {li}: INT8 KV differs by {err:.3g}"
         self.stats[f"kv_layers_{name}"] += 1
 
     def summary(self):
