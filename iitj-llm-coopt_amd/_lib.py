@@ -61,6 +61,9 @@ SIGNATURES = {
     "coopt_accept_sample_workspace": (_sz, [_i, _i, _i]),
     "coopt_accept_sample": (_i, [_i, _p, _i64, _p, _i, _p, _i64, _p, _p, _p, _p, _p, _f, _i, _i,
                                  _i, _p, _p, _p, _p, _sz, _p]),
+    "coopt_accept_sample_noalloc_max_bytes": (_sz, []),
+    "coopt_accept_sample_noalloc": (_i, [_i, _p, _i64, _p, _i, _p, _i64, _p, _p, _p, _p, _p, _f,
+                                         _i, _i, _i, _p, _p, _p, _p]),
     "coopt_softmax": (_i, [_i, _p, _i64, _i64, _i, _f, _p, _i64, _p]),
     "coopt_rms_norm": (_i, [_p, _p, _p, _p, _i64, _i, _f, _p]),
     "coopt_rope": (_i, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _i, _i, _i, _i, _i, _p]),

@@ -23,6 +23,9 @@
 // (relative error < 1e-6); cumulative weights are fp64 sums of fp32 w_j.
 #include <math.h>
 
+#include <mutex>
+#include <string>
+
 #include "common.h"
 
 namespace {
@@ -921,6 +924,74 @@ extern "C" int coopt_accept_sample(int logits_dtype, const void* target, int64_t
   carve(&a.ws, reinterpret_cast<uintptr_t>(workspace), B, gamma_max, a.L);
   auto s = static_cast<hipStream_t>(stream);
   return bf16 ? launch_all<true>(a, greedy, s) : launch_all<false>(a, greedy, s);
+}
+
+// ---- the entry point that allocates nothing ----------------------------------------------
+// Its workspace is this file-scope device array: each GPU the library runs on holds its own
+// copy (kAcceptScratchBytes) until the process ends.  Host code never passes the array's name
+// to a kernel -- on the host that name is a stand-in, not a device address -- but the address
+// hipGetSymbolAddress returns for the current device, looked up once per device.
+namespace {
+
+constexpr size_t kAcceptScratchBytes = size_t{2} << 20;
+__device__ __align__(256) unsigned char scratch[kAcceptScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch` (nullptr with the error recorded on failure).
+void* scratch_ptr() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    coopt::set_error("coopt_accept_sample_noalloc: no current HIP device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t rc = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (rc != hipSuccess || p == nullptr) {
+      coopt::set_error(std::string("coopt_accept_sample_noalloc: hipGetSymbolAddress: ") +
+                       hipGetErrorString(rc));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" size_t coopt_accept_sample_noalloc_max_bytes(void) { return kAcceptScratchBytes; }
+
+extern "C" int coopt_accept_sample_noalloc(int logits_dtype, const void* target,
+                                           int64_t target_row_stride, const int32_t* target_row0,
+                                           int draft_kind, const void* draft,
+                                           int64_t draft_row_stride, const int32_t* draft_row0,
+                                           const int32_t* draft_tokens,
+                                           const int32_t* gamma_per_seq, const float* u_accept,
+                                           const float* u_resample, float temperature, int B,
+                                           int gamma_max, int V, int32_t* accepted_len,
+                                           int32_t* out_tokens, float* margin,
+                                           coopt_stream_t stream) {
+  COOPT_REQUIRE(B >= 0 && gamma_max >= 0 && gamma_max <= 64 && V > 0, "bad sizes");
+  if (B == 0) return COOPT_OK;
+  const size_t need = coopt_accept_sample_workspace(B, gamma_max, V);
+  if (need > kAcceptScratchBytes) {
+    coopt::set_error("coopt_accept_sample_noalloc: B=" + std::to_string(B) + ", gamma_max=" +
+                     std::to_string(gamma_max) + ", V=" + std::to_string(V) + " need " +
+                     std::to_string(need) + " bytes of scratch, more than its " +
+                     std::to_string(kAcceptScratchBytes) + "; use coopt_accept_sample with a "
+                     "caller workspace");
+    return COOPT_EWORKSPACE;
+  }
+  void* ws = scratch_ptr();
+  if (ws == nullptr) return COOPT_EHIP;
+  return coopt_accept_sample(logits_dtype, target, target_row_stride, target_row0, draft_kind,
+                             draft, draft_row_stride, draft_row0, draft_tokens, gamma_per_seq,
+                             u_accept, u_resample, temperature, B, gamma_max, V, accepted_len,
+                             out_tokens, margin, ws, kAcceptScratchBytes, stream);
 }
 
 extern "C" int coopt_softmax(int logits_dtype, const void* logits, int64_t in_stride, int64_t rows,

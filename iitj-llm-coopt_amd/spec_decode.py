@@ -59,7 +59,9 @@ def accept(target_logits, draft, draft_tokens, temperature, u_accept=None, u_res
     kernel) or, with draft_is_probs, fp32 draft probabilities; draft_tokens [B, gamma_max].
     temperature <= 0 selects the greedy rule (argmax, accept while equal).
     out / workspace: optional preallocated AcceptResult and uint8 scratch buffer (neither
-    allocates then, so the call can be recorded into a HIP graph).
+    allocates then, so the call can be recorded into a HIP graph).  workspace="static" runs
+    coopt_accept_sample_noalloc, whose workspace is the library's own per-GPU device array
+    (sizes up to coopt_accept_sample_noalloc_max_bytes(); overlapping calls on one GPU race).
     """
     tgt, tstride = _rows(target_logits)
     _lib.require_cuda(tgt, draft_tokens)
@@ -119,6 +121,16 @@ def accept(target_logits, draft, draft_tokens, temperature, u_accept=None, u_res
                            torch.empty((B, gmax + 1), dtype=torch.int32, device=dev),
                            torch.empty(B, dtype=torch.float32, device=dev))
     lib = _lib.load()
+    if isinstance(workspace, str):
+        if workspace != "static":
+            raise ValueError('workspace must be a tensor, None or "static"')
+        _lib.check(lib.coopt_accept_sample_noalloc(
+            _lib.dt_code(tgt.dtype), _lib.ptr(tgt), tstride, _lib.ptr(t0),
+            1 if draft_is_probs else 0, _lib.ptr(drf), dstride, _lib.ptr(d0),
+            _lib.ptr(dtok), _lib.ptr(gam), _lib.ptr(ua), _lib.ptr(ur), float(temperature),
+            B, gmax, V, _lib.ptr(out.accepted_len), _lib.ptr(out.tokens), _lib.ptr(out.margin),
+            _lib.stream_handle(dev)), "coopt_accept_sample_noalloc")
+        return out
     need = int(lib.coopt_accept_sample_workspace(B, gmax, V))
     if workspace is None:
         ws = _WS.get(need, dev)

@@ -284,6 +284,29 @@ int coopt_accept_sample(int logits_dtype,
                         void* workspace, size_t workspace_bytes, coopt_stream_t stream);
 
 /*
+ * coopt_accept_sample without a workspace argument: no counterpart in the reference.  For
+ * callers that cannot allocate device memory -- code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc.  Same arguments, kernels and results as
+ * coopt_accept_sample; its workspace is a file-scope device array of
+ * coopt_accept_sample_noalloc_max_bytes() bytes (2 MiB: B <= 512 at gamma_max 8 and V 128256,
+ * or B <= 256 at V 262144), which each GPU holds until the process ends.  Sizes whose
+ * coopt_accept_sample_workspace() exceeds it return COOPT_EWORKSPACE with a message.  It
+ * allocates nothing and needs no clearing (the kernels initialise what they read); every call
+ * on one GPU shares that GPU's array, so calls that overlap on one GPU (different streams or
+ * host threads without ordering) race.
+ */
+size_t coopt_accept_sample_noalloc_max_bytes(void);
+int coopt_accept_sample_noalloc(int logits_dtype,
+                                const void* target, int64_t target_row_stride,
+                                const int32_t* target_row0, int draft_kind, const void* draft,
+                                int64_t draft_row_stride, const int32_t* draft_row0,
+                                const int32_t* draft_tokens, const int32_t* gamma_per_seq,
+                                const float* u_accept, const float* u_resample, float temperature,
+                                int B, int gamma_max, int V,
+                                int32_t* accepted_len, int32_t* out_tokens, float* margin,
+                                coopt_stream_t stream);
+
+/*
  * probs[r, :] = softmax(logits[r, :] * (1/T)) in fp32 (engine/spec_decode.py:16), for the
  * probabilities sample() returns.  logits F32 or BF16 with row stride in_stride.
  */

@@ -135,3 +135,19 @@ def test_python_wrappers_refuse_cpu_tensors():
         M.quantize(x, 8)
     with pytest.raises(_lib.CooptError, match="no CPU fallback"):
         M.sample(torch.zeros(2, 10), 1.0)
+
+
+def test_accept_noalloc_rejects_sizes_beyond_its_scratch(lib):
+    """The static-scratch accept entry point checks its size before touching the device."""
+    cap = lib.coopt_accept_sample_noalloc_max_bytes()
+    assert cap == 2 << 20
+    assert lib.coopt_accept_sample_workspace(512, 8, 128256) <= cap
+    need = lib.coopt_accept_sample_workspace(4096, 8, 262144)
+    assert need > cap
+    rc = lib.coopt_accept_sample_noalloc(_lib.DT_F32, 16, 262144, None, 0, 16, 262144, None, 16,
+                                         None, 16, 16, 1.0, 4096, 8, 262144, 16, 16, 16, None)
+    assert rc == _lib.COOPT_EWORKSPACE
+    msg = _lib.last_error()
+    assert "scratch" in msg and str(need) in msg and str(cap) in msg, msg
+    assert lib.coopt_accept_sample_noalloc(_lib.DT_F32, 0, 1, None, 0, 0, 1, None, 0, None, 0, 0,
+                                           1.0, 0, 4, 100, 0, 0, 0, None) == _lib.COOPT_OK
