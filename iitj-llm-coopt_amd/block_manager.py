@@ -63,7 +63,7 @@ class BlockManager:
         """Grows seq_id's table to hold total_tokens tokens (all or nothing)."""
         need = self.extra_blocks_needed(seq_id, total_tokens)
         if need > self.num_free:
-            raise OutOfBlocks(f"seq {seq_id} needs {need} blocks, {self.num_free} free")
+            raise OutOfBlocks(f"cannot grow sequence {seq_id} by {need} blocks: only {self.num_free} are free")
         table = self.tables.setdefault(seq_id, [])
         table.extend(self._free.popleft() for _ in range(need))
 
@@ -95,7 +95,7 @@ class BlockManager:
             if b not in excluded:
                 del self._free[i]
                 return b
-        raise OutOfBlocks("no free block outside the excluded range")
+        raise OutOfBlocks("every free block lies inside the excluded id range")
 
     def migrate_out_of(self, ids, copy_fn) -> int:
         """Moves every in-use block in `ids` to a free block outside `ids`, in ascending id
@@ -127,7 +127,7 @@ class BlockManager:
         ids = set(int(b) for b in ids)
         remaining = deque(b for b in self._free if b not in ids)
         if len(self._free) - len(remaining) != len(ids):
-            raise OutOfBlocks("withdraw_free: some blocks are still in use")
+            raise OutOfBlocks("withdraw_free: not every requested block is free")
         self._free = remaining
         self.num_blocks -= len(ids)
 

@@ -214,7 +214,7 @@ class KVTierManager:
             raise ValueError("bits must be 16, 8 or 4")
         self.e = engine
         self.capacity = int(cpu_gb * 2**30)
-        self.bits = bits                 # current quantization level (set by a co-optimizer)
+        self.bits = bits                 # codec width of the next swap_out (a policy may change it)
         self.store: dict = {}
         self.used = 0
         self._stream = None              # side stream for swap_out, created on first use
@@ -258,7 +258,8 @@ class KVTierManager:
 
     # ---- swap out / in ---------------------------------------------------------------------
     def swap_out(self, seq) -> bool:
-        """Copy seq's target KV (num_computed tokens) to the CPU tier. False if it does not fit."""
+        """Moves the target KV of seq's first num_computed tokens to host memory (quantised to
+        self.bits); returns False, moving nothing, when the tier lacks the room."""
         n = seq.num_computed
         if n == 0:
             return False
@@ -304,7 +305,8 @@ class KVTierManager:
         return True
 
     def swap_in(self, seq) -> None:
-        """Restore seq's KV into newly allocated GPU blocks (caller has checked capacity)."""
+        """Brings seq's swapped KV back into blocks ensure() hands out now (the caller has
+        made sure they are available), dequantised into the caches."""
         sw = self.store.pop(seq.seq_id)
         e, bm = self.e, self.e.bm
         kcs, vcs = e.target.k_cache, e.target.v_cache
