@@ -59,6 +59,28 @@ __device__ __forceinline__ uint16_t f32_to_f16(float f) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 
+// The value lane l ^ 16 (lane l ^ 32) holds, for a symmetric combination: v_permlane16_swap
+// (v_permlane32_swap) run on two copies of v leaves every lane's own value in one result and
+// its partner's in the other, so op(first, second) = op(v, partner).  A VALU exchange, unlike
+// __shfl_xor's ds_bpermute round trip through the LDS crossbar.
+typedef unsigned int u32x2_pl_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float max_xor16(float v) {
+  const u32x2_pl_t r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  const u32x2_pl_t r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float add_xor16(float v) {
+  const u32x2_pl_t r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor32(float v) {
+  const u32x2_pl_t r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 template <typename T>
 __device__ __forceinline__ T wave_shfl_xor(T v, int mask) {
   return __shfl_xor(v, mask, COOPT_WAVE);

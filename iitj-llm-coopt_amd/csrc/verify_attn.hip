@@ -512,8 +512,7 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
     for (int rt = 0; rt < RT; ++rt) {
       float tmax = fmaxf(fmaxf(fmaxf(sv[rt][0][0], sv[rt][0][1]), fmaxf(sv[rt][0][2], sv[rt][0][3])),
                          fmaxf(fmaxf(sv[rt][1][0], sv[rt][1][1]), fmaxf(sv[rt][1][2], sv[rt][1][3])));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      tmax = max_xor32(max_xor16(tmax));
       m_tile[rt] = tmax * score_scale;
       raise_any |= m_tile[rt] > m_run[rt] + kSlack;
     }
@@ -635,8 +634,7 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     m_run[rt] += ev_f;
-    l_run[rt] += __shfl_xor(l_run[rt], 16, 64);
-    l_run[rt] += __shfl_xor(l_run[rt], 32, 64);
+    l_run[rt] = add_xor32(add_xor16(l_run[rt]));
     if (grp == 0) {
       sm_m[wave][rt * 16 + l16] = m_run[rt];
       sm_l[wave][rt * 16 + l16] = l_run[rt];
