@@ -6,12 +6,16 @@
 // packed into R = G*n "rows" (row r = head_local * n + j), so each K/V byte is read once per
 // KV head.  A block covers `split` keys of one (sequence, KV head); its waves take 32-key
 // tiles in turn, each with its own online softmax, and double-buffer them: the loads of a
-// wave's next tile are in flight while it computes the current one.  The waves merge through
-// LDS, each into its own region in one round, summed while the output is written.  With
-// one split the block writes the bf16 output; otherwise it writes its (max, sum) and
-// unnormalised fp32 rows to the workspace and a second launch (merge_kernel, one block per
-// (KV head, sequence)) combines the splits -- the kernel boundary orders the two, so no block
-// waits on another and no cross-workgroup fence is needed.
+// wave's next tile are in flight while it computes the current one.  The first tile's loads
+// are issued before Q is staged in LDS, and its page lookups before seq_lens is known, so
+// the block's start-up round trips overlap.  The waves merge through LDS, each into its own
+// region in one round, summed while the output is written.  With one split the block writes
+// the bf16 output; otherwise it writes its (max, sum) and unnormalised fp32 rows to the
+// workspace and a second launch (merge_kernel, one block per (KV head, sequence)) combines
+// the splits -- the kernel boundary orders the two, so no block waits on another and no
+// cross-workgroup fence is needed.  A ragged batch with more (sequence, KV head) items than
+// one round of blocks holds runs on a 1-D grid whose blocks rank the sequences by length and
+// take the items longest first (plan_item), so its long sequences do not start last.
 //
 // MFMA layout (v_mfma_f32_16x16x32_{bf16,f16}; lane l, g = l/16, m = l%16):
 //   scores  S^T[key][row] = sum_d K[key][d] Q[row][d]     A = K, B = Q^T
@@ -82,7 +86,13 @@ struct AttnArgs {
   int split, max_splits, rmax;
   float2* part_ml;
   float* part_o;
+  int B;
+  int plan;  // blocks order the items longest first (plan_item)
 };
+
+// Batches of up to kPlanSeqs sequences can be ordered by the blocks themselves (one wave,
+// one lane per sequence); larger ones run in grid order.
+constexpr int kPlanSeqs = 64;
 
 __device__ __forceinline__ f32x4_t mfma_bf16(u32x4_t a, u32x4_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
@@ -127,13 +137,13 @@ __device__ __forceinline__ uint32_t max_u16x2(uint32_t a, uint32_t b) {
                                                                 __builtin_bit_cast(u16x2_t, b)));
 }
 
-__device__ __forceinline__ int64_t clamp_page(int32_t page, int64_t num_blocks) {
-  return page < 0 ? 0 : (page >= num_blocks ? num_blocks - 1 : page);
-}
-
 // Byte `i` of a dword holding (code + 128) bytes -> float(code) * s, exact: u * s - 128 * s.
 __device__ __forceinline__ float dequant_byte(uint32_t ux, int i, float s, float sb) {
   return fmaf(static_cast<float>((ux >> (8 * i)) & 0xffu), s, sb);
+}
+
+__device__ __forceinline__ int64_t clamp_page(int32_t page, int64_t num_blocks) {
+  return page < 0 ? 0 : (page >= num_blocks ? num_blocks - 1 : page);
 }
 
 // Raw data of one wave's 32-key tile (see the layout notes at the top of the file).
@@ -158,6 +168,36 @@ __device__ __forceinline__ void load_words(const unsigned char* p, uint32_t* dst
     dst[0] = x[0]; dst[1] = x[1];
   } else {
     dst[0] = *reinterpret_cast<const uint32_t*>(p);
+  }
+}
+
+// The item of block blockIdx.x in an ordered launch (one wave, lane t = sequence t, B <=
+// kPlanSeqs): sequences are ranked by key count, longest first (ties by index, sequences
+// without query rows last), and block k takes KV head k % Hkv of the sequence of rank
+// k / Hkv.  With more items than one round of blocks holds, the dispatcher then starts the
+// longest and gives CUs that free up the next longest: longest-processing-time-first list
+// scheduling, instead of whatever order the batch came in.  out = {sequence, q0, n, L}, the
+// values the lane loaded, so the block does not load them again.
+__device__ void plan_item(const AttnArgs& a, int lane, int* out) {
+  const int t = lane;
+  int q0 = 0, n = 0, L = 0, key = -2;
+  if (t < a.B) {
+    q0 = a.cu[t];
+    n = a.cu[t + 1] - q0;
+    L = min(a.seq_lens[t], a.max_seqlen_k);
+    key = n > 0 ? max(L, 0) : -1;
+  }
+  // rank by lane reads into scalar registers: B short scalar steps, no LDS round trips
+  int rank = 0;
+  for (int j = 0; j < a.B; ++j) {
+    const int kj = __builtin_amdgcn_readlane(key, j);
+    rank += (kj > key || (kj == key && j < t)) ? 1 : 0;
+  }
+  if (t < a.B && rank == static_cast<int>(blockIdx.x) / a.Hkv) {
+    out[0] = t;
+    out[1] = q0;
+    out[2] = n;
+    out[3] = L;
   }
 }
 
@@ -190,49 +230,61 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
   __shared__ float sm_l[kWaves][kRows];
   __shared__ float sm_M[kRows];
   __shared__ float sm_L[kRows];
+  __shared__ int sm_plan[4];
   float* osh = reinterpret_cast<float*>(lds);
-
-  const int b = blockIdx.z, hkv = blockIdx.y, sidx = blockIdx.x;
-  const int q0 = a.cu[b];
-  const int n = a.cu[b + 1] - q0;
-  // Clamps keep a malformed call (seq_len > max_seqlen_k, q_len > max_seqlen_q, block ids
-  // outside the pool) inside its buffers: such calls give wrong rows, never stray accesses.
-  const int L = min(a.seq_lens[b], a.max_seqlen_k);
-  if (n <= 0) return;
-  const int nsplit = L > 0 ? (L + a.split - 1) / a.split : 1;
-  if (sidx >= nsplit) return;
-  const int R = min(min(a.G * n, kRows), a.rmax);
-  const int k_begin = sidx * a.split;
-  const int k_end = min(L, k_begin + a.split);
-
   const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, l16 = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int bs_mask = (1 << a.bs_shift) - 1;
+
+  // One piece: keys [sidx * split, min(L, (sidx + 1) * split)) of (sequence b, KV head hkv)
+  // with query rows [q0, q0 + n); L = min(seq_lens[b], max_seqlen_k).
+  auto run_piece = [&](const int b, const int hkv, const int sidx, const int q0, const int n,
+                       const int L) {
   // The block table is read-only here: reading it through the constant address space lets
   // the wave-uniform page lookups be scalar loads, which do not wait behind (or drain) the
   // wave's outstanding K/V vector loads.
   typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
   const const_i32_ptr table = (const_i32_ptr)(a.bt + static_cast<int64_t>(b) * a.bt_stride);
+  const int k_begin = sidx * a.split;
+  // The pages of the wave's first tile, looked up before L is tested: they are used only if
+  // that tile is full, i.e. all its keys are < L, where no clamp to L - 1 applies (the index
+  // is kept inside the table row regardless).
+  const int64_t bt_last = a.bt_stride - 1;
+  const int kb_first = k_begin + wave * kTileKeys;
+  const int64_t first_pg0 = clamp_page(table[min<int64_t>(kb_first >> a.bs_shift, bt_last)], a.num_blocks);
+  const int64_t first_pg1 = clamp_page(table[min<int64_t>((kb_first + 16) >> a.bs_shift, bt_last)], a.num_blocks);
+  if (n <= 0) return;
+  const int nsplit = L > 0 ? (L + a.split - 1) / a.split : 1;
+  if (sidx >= nsplit) return;
+  const int R = min(min(a.G * n, kRows), a.rmax);
+  const int k_end = min(L, k_begin + a.split);
 
-  // ---- Q rows into LDS, causal limits ----
+  const int bs_mask = (1 << a.bs_shift) - 1;
+
+  // ---- Q rows (into LDS by stage_q, once the first tile's loads are issued), causal limits ----
   // Row r of the block is query head hkv*G + r/n at query row j = r % n; rows >= R are 0.
   constexpr int kQCh = D / 8;  // 16-byte chunks per row
   constexpr int kQIter = (kRows * kQCh + kBlock - 1) / kBlock;
+  u32x4_t qreg[kQIter];
 #pragma unroll
   for (int it = 0; it < kQIter; ++it) {
     const int idx = it * kBlock + tid;
     const int r = idx / kQCh, c = idx % kQCh;
-    if (r < kRows) {
-      u32x4_t qv = {0, 0, 0, 0};
-      if (r < R) {
-        const int hl = r / n, j = r - hl * n;
-        qv = *reinterpret_cast<const u32x4_t*>(a.q + static_cast<int64_t>(q0 + j) * a.q_ts +
-                                               static_cast<int64_t>(hkv * a.G + hl) * a.q_hs + c * 8);
-      }
-      *reinterpret_cast<u32x4_t*>(lds + r * kQPitch + c * 16) = qv;
+    qreg[it] = u32x4_t{0, 0, 0, 0};
+    if (r < R) {
+      const int hl = r / n, j = r - hl * n;
+      qreg[it] = *reinterpret_cast<const u32x4_t*>(a.q + static_cast<int64_t>(q0 + j) * a.q_ts +
+                                                   static_cast<int64_t>(hkv * a.G + hl) * a.q_hs + c * 8);
     }
   }
-  __syncthreads();
+  auto stage_q = [&]() {
+#pragma unroll
+    for (int it = 0; it < kQIter; ++it) {
+      const int idx = it * kBlock + tid;
+      const int r = idx / kQCh, c = idx % kQCh;
+      if (r < kRows) *reinterpret_cast<u32x4_t*>(lds + r * kQPitch + c * 16) = qreg[it];
+    }
+    __syncthreads();
+  };
   const float score_scale = a.scale_log2;
   int lim[RT];
 #pragma unroll
@@ -574,11 +626,22 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
 
   // ---- the wave's tiles: double-buffered (the next tile's loads in flight while the current
   // one is computed) or, for large row counts, one at a time; then the partial tile ----
+  // Wave w takes tiles w, w + kWaves, w + 2 kWaves, ... (a fixed assignment keeps the result
+  // bit-reproducible: each wave's sum covers the same keys on every call); the wave whose
+  // sequence reaches nfull also takes the split's partial tile.
   const int nfull = (k_end - k_begin) / kTileKeys;
   auto pages = [&](int t, int64_t& p0, int64_t& p1) {
     const int kb = k_begin + t * kTileKeys;
     p0 = page_of(kb);
     p1 = page_of(kb + 16);
+  };
+  bool own_partial = wave == nfull;
+  int next_t = wave + kWaves;
+  auto grab = [&]() {
+    const int v = next_t;
+    next_t += kWaves;
+    own_partial |= v == nfull;
+    return v;
   };
   if constexpr (DB) {
     // Loads inside the loop are unconditional (an index past the last full tile repeats it,
@@ -586,39 +649,50 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
     // buffer's loads and the other buffer's stay in flight.
     Raw bufA, bufB;
     const int tlast = nfull - 1;
-    int t = wave;
+    int tA = wave;
     int64_t nx0 = 0, nx1 = 0;  // pages of the wave's next tile to load
-    if (t < nfull) {
-      int64_t p0, p1;
-      pages(t, p0, p1);
-      load_full(bufA, t, p0, p1);
-      pages(min(t + kWaves, tlast), nx0, nx1);
+    if (tA < nfull) load_full(bufA, tA, first_pg0, first_pg1);
+    stage_q();  // the Q loads complete while the first tile's are in flight
+    if (tA < nfull) {
       vcheck(bufA);
-    }
-    for (; t < nfull; t += 2 * kWaves) {
-      const int t1 = t + kWaves, t2 = t1 + kWaves;
-      load_full(bufB, min(t1, tlast), nx0, nx1);
-      pages(min(t2, tlast), nx0, nx1);
-      compute_tile(bufA, t);
-      vcheck(bufB);
-      if (t1 >= nfull) break;
-      load_full(bufA, min(t2, tlast), nx0, nx1);
-      pages(min(t2 + kWaves, tlast), nx0, nx1);
-      compute_tile(bufB, t1);
-      vcheck(bufA);
+      int tB = grab();
+      pages(min(tB, tlast), nx0, nx1);
+      for (;;) {
+        load_full(bufB, min(tB, tlast), nx0, nx1);
+        const int tA2 = tB < nfull ? grab() : nfull;
+        pages(min(tA2, tlast), nx0, nx1);
+        compute_tile(bufA, tA);
+        vcheck(bufB);
+        if (tB >= nfull) break;
+        load_full(bufA, min(tA2, tlast), nx0, nx1);
+        const int tB2 = tA2 < nfull ? grab() : nfull;
+        pages(min(tB2, tlast), nx0, nx1);
+        compute_tile(bufB, tB);
+        vcheck(bufA);
+        if (tA2 >= nfull) break;
+        tA = tA2;
+        tB = tB2;
+      }
     }
   } else {
     Raw buf;
     int64_t nx0 = 0, nx1 = 0;
-    if (wave < nfull) pages(wave, nx0, nx1);
-    for (int t = wave; t < nfull; t += kWaves) {
+    int t = wave;
+    if (t < nfull) {
+      nx0 = first_pg0;
+      nx1 = first_pg1;
+    }
+    stage_q();
+    while (t < nfull) {
       load_full(buf, t, nx0, nx1);
-      if (t + kWaves < nfull) pages(t + kWaves, nx0, nx1);
+      const int tn = grab();
+      if (tn < nfull) pages(tn, nx0, nx1);
       vcheck(buf);
       compute_tile(buf, t);
+      t = tn;
     }
   }
-  if (nfull < ntiles && wave == nfull % kWaves) {
+  if (nfull < ntiles && own_partial) {
     Raw buf;
     int64_t p0, p1;
     pages(nfull, p0, p1);
@@ -669,6 +743,7 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
         const int r = rt * 16 + l16;
+        if (rt * 16 >= R) break;  // row tiles of padding only (uniform)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           float* dst = region + r * kOPitch + (grp * 4 + i) * kDt;
@@ -698,7 +773,6 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
   };
 
   constexpr int kCh = D / 8;  // 8-element chunks per row
-  const int64_t item = static_cast<int64_t>(b) * a.Hkv + hkv;
   if (nsplit == 1) {
     for (int idx = tid; idx < R * kCh; idx += kBlock) {
       const int r = idx / kCh, c = idx % kCh;
@@ -720,7 +794,7 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
   }
 
   // ---- several splits: publish this split's partial; merge_kernel combines them ----
-  const int64_t pbase = (item * a.max_splits + sidx) * a.rmax;
+  const int64_t pbase = ((static_cast<int64_t>(b) * a.Hkv + hkv) * a.max_splits + sidx) * a.rmax;
   for (int idx = tid; idx < R * kCh; idx += kBlock) {
     const int r = idx / kCh, c = idx % kCh;
     f32x4_t lo, hi;
@@ -730,6 +804,29 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
     reinterpret_cast<f32x4_t*>(dst)[1] = hi;
   }
   if (tid < R) a.part_ml[pbase + tid] = make_float2(sm_M[tid], sm_L[tid]);
+  };  // run_piece
+
+  // Clamps keep a malformed call (seq_len > max_seqlen_k, q_len > max_seqlen_q, block ids
+  // outside the pool) inside its buffers: such calls give wrong rows, never stray accesses.
+  int b, hkv, sidx, q0, n, L;
+  if (a.plan) {
+    if (wave == 0) plan_item(a, lane, sm_plan);
+    __syncthreads();
+    b = __builtin_amdgcn_readfirstlane(sm_plan[0]);
+    q0 = __builtin_amdgcn_readfirstlane(sm_plan[1]);
+    n = __builtin_amdgcn_readfirstlane(sm_plan[2]);
+    L = __builtin_amdgcn_readfirstlane(sm_plan[3]);
+    hkv = static_cast<int>(blockIdx.x) % a.Hkv;
+    sidx = 0;
+  } else {
+    b = blockIdx.z;
+    hkv = blockIdx.y;
+    sidx = blockIdx.x;
+    q0 = a.cu[b];
+    n = a.cu[b + 1] - q0;
+    L = min(a.seq_lens[b], a.max_seqlen_k);
+  }
+  run_piece(b, hkv, sidx, q0, n, L);
 }
 
 // Second launch: combines the split partials of every (sequence, KV head) that needed more
@@ -747,19 +844,20 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(AttnArgs a) {
   if (nsplit <= 1) return;
   const int R = min(a.G * n, a.rmax);
   constexpr int kCh = D / 8;
-  const int64_t ibase = (static_cast<int64_t>(b) * a.Hkv + hkv) * a.max_splits * a.rmax;
+  const int64_t first = (static_cast<int64_t>(b) * a.Hkv + hkv) * a.max_splits;
+  auto slot = [&](int s) { return (first + s) * a.rmax; };
   for (int idx = threadIdx.x; idx < R * kCh; idx += kThreads) {
     const int r = idx / kCh, c = idx % kCh;
     float M = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, a.part_ml[ibase + s * a.rmax + r].x);
+    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, a.part_ml[slot(s) + r].x);
     f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
     float Lsum = 0.0f;
     for (int s = 0; s < nsplit; ++s) {
-      const float2 ml = a.part_ml[ibase + s * a.rmax + r];
+      const float2 ml = a.part_ml[slot(s) + r];
       if (!(ml.x > -INFINITY)) continue;
       const float w = exp2_fast(ml.x - M);
       Lsum += ml.y * w;
-      const f32x4_t* src = reinterpret_cast<const f32x4_t*>(a.part_o + (ibase + s * a.rmax + r) * D + c * 8);
+      const f32x4_t* src = reinterpret_cast<const f32x4_t*>(a.part_o + (slot(s) + r) * D + c * 8);
       acc0 += src[0] * w;
       acc1 += src[1] * w;
     }
@@ -777,15 +875,36 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(AttnArgs a) {
 // reading seq_lens.  Aims at one block per CU (8-wave blocks) or two (4-wave blocks) for the
 // longest context, in whole rounds of 32-key tiles over the block's waves; a sequence longer
 // than one split is split, so shorter ones run whole.
+int target_blocks(int waves) { return waves == 8 ? 256 : 512; }
+
 int choose_split(int B, int Hkv, int max_seqlen_k, int waves) {
   const int64_t items = static_cast<int64_t>(B) * Hkv;
-  const int64_t target = waves == 8 ? 256 : 512;
+  const int64_t target = target_blocks(waves);
   const int64_t gran = 32 * waves;
   int64_t per = (static_cast<int64_t>(max_seqlen_k) * items + target - 1) / target;
   per = ((per + gran - 1) / gran) * gran;
   if (per < 2 * gran) per = 2 * gran;
   if (per > 65536) per = 65536;
   return static_cast<int>(per);
+}
+
+// How one call is laid out: `split`-key pieces, max_splits per (sequence, KV head).  plan:
+// more (sequence, KV head) items than one round of blocks holds, none split, B <= kPlanSeqs --
+// a 1-D grid of B * Hkv blocks that order the items themselves (plan_item); otherwise the
+// grid (max_splits, Hkv, B) in order, where one round holds every item and order is moot.
+struct AttnShape {
+  bool plan;
+  int split, max_splits;
+};
+
+AttnShape attn_shape(int B, int Hkv, int rmax, int max_seqlen_k) {
+  const int waves = waves_for((rmax + 15) / 16);
+  AttnShape s{};
+  s.split = choose_split(B, Hkv, max_seqlen_k, waves);
+  s.max_splits = (max_seqlen_k + s.split - 1) / s.split;
+  s.plan = B <= kPlanSeqs && static_cast<int64_t>(B) * Hkv > target_blocks(waves) &&
+           s.max_splits == 1;
+  return s;
 }
 
 struct AttnWs {
@@ -813,7 +932,7 @@ int launch_rt(int RT, const AttnArgs& a, dim3 grid, hipStream_t s) {
   }
   int rc = coopt::check_launch("coopt_verify_attention");
   if (rc != COOPT_OK || a.max_splits <= 1) return rc;
-  hipLaunchKernelGGL((merge_kernel<D>), dim3(grid.y, grid.z), dim3(kThreads), 0, s, a);
+  hipLaunchKernelGGL((merge_kernel<D>), dim3(a.Hkv, a.B), dim3(kThreads), 0, s, a);
   return coopt::check_launch("coopt_verify_attention/merge");
 }
 
@@ -829,9 +948,8 @@ extern "C" size_t coopt_verify_attention_workspace(int B, int Hq, int Hkv, int D
                                                    int max_seqlen_k) {
   if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv || max_seqlen_q <= 0 || max_seqlen_k <= 0) return 0;
   const int rmax = (Hq / Hkv) * max_seqlen_q;
-  const int split = choose_split(B, Hkv, max_seqlen_k, waves_for((rmax + 15) / 16));
-  const int max_splits = (max_seqlen_k + split - 1) / split;
-  return attn_ws_layout(B, Hkv, D, rmax, max_splits).total;
+  const AttnShape sh = attn_shape(B, Hkv, rmax, max_seqlen_k);
+  return attn_ws_layout(B, Hkv, D, rmax, sh.max_splits).total;
 }
 
 extern "C" int coopt_verify_attention(int kv_dtype, const void* q, int64_t q_tok_stride,
@@ -918,15 +1036,18 @@ extern "C" int coopt_verify_attention(int kv_dtype, const void* q, int64_t q_tok
   a.o_ts = o_tok_stride;
   a.o_hs = o_head_stride;
   a.rmax = G * max_seqlen_q;
-  a.split = choose_split(B, Hkv, max_seqlen_k, waves_for((a.rmax + 15) / 16));
-  a.max_splits = (max_seqlen_k + a.split - 1) / a.split;
+  const AttnShape shape = attn_shape(B, Hkv, a.rmax, max_seqlen_k);
+  a.split = shape.split;
+  a.max_splits = shape.max_splits;
+  a.B = B;
+  a.plan = shape.plan;
   const AttnWs w = attn_ws_layout(B, Hkv, D, a.rmax, a.max_splits);
   char* base = static_cast<char*>(workspace);
   a.part_ml = reinterpret_cast<float2*>(base + w.ml_off);
   a.part_o = reinterpret_cast<float*>(base + w.o_off);
 
   const int RT = (a.rmax + 15) / 16;
-  const dim3 grid(a.max_splits, Hkv, B);
+  const dim3 grid = shape.plan ? dim3(B * Hkv) : dim3(a.max_splits, Hkv, B);
   auto s = static_cast<hipStream_t>(stream);
   // scale caches with consecutive tokens adjacent and 8-byte aligned groups of four
   const bool sc = int8 && s_tok_stride == 1 && s_blk_stride % 4 == 0 && s_head_stride % 4 == 0 &&

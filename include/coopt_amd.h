@@ -236,6 +236,9 @@ int coopt_kv_copy_blocks(const int64_t* regions, int num_regions, const int64_t*
  *   <= max_seqlen_q and block ids in [0, num_blocks); the kernel clamps all three so a
  *   malformed call yields wrong rows but never an access outside its buffers.
  *   workspace: coopt_verify_attention_workspace() bytes (see above).
+ *   Scheduling: when a batch of B <= 64 sequences has more (sequence, KV head) items than the
+ *   GPU runs at once, the blocks take them longest first (whatever order the batch lists
+ *   them in), so the long sequences start early instead of being left for last.
  */
 size_t coopt_verify_attention_workspace(int B, int Hq, int Hkv, int D, int max_seqlen_q,
                                         int max_seqlen_k);

@@ -313,3 +313,40 @@ def test_int8_v_scales_across_the_fp16_scale_range(dev, q_len):
         assert rel <= 2e-2, name
         if name != "mixed":
             assert mabs / c <= TOL_INT8, name
+
+
+def _ragged(rng, B, lo, hi):
+    return [int(x) for x in rng.integers(lo, hi + 1, B)]
+
+
+# (name, ctx, q_lens, D, kv): batches of more than 32 sequences hold more (sequence, KV head)
+# items than the 256 CUs run at once, so the blocks order them longest first themselves
+_r = np.random.default_rng(31)
+RAGGED = [
+    ("40 sequences, int8", _ragged(_r, 40, 16, 6000), [5] * 40, 128, "int8"),
+    ("48 sequences, one long", [9000] + _ragged(_r, 47, 20, 300), [5] * 48, 128, "auto"),
+    ("64 with idle ones", _ragged(_r, 64, 0, 3000), [5, 0, 3, 5] * 16, 128, "auto"),
+    ("48, gamma 8, int8", _ragged(_r, 48, 30, 4000), [9] * 48, 128, "int8"),
+    ("48, head dim 64, 2 rows", _ragged(_r, 48, 0, 5000), [2] * 48, 64, "int8"),
+    ("32 sequences (one round)", _ragged(_r, 32, 512, 4096), [5] * 32, 128, "auto"),
+    ("6 sequences, 64 rows", [3000, 40, 900, 6000, 10, 2500], [16] * 6, 128, "auto"),
+    ("65 sequences (grid order)", _ragged(_r, 65, 16, 3000), [5] * 65, 128, "int8"),
+]
+
+
+@pytest.mark.parametrize("case", RAGGED, ids=[c[0] for c in RAGGED])
+def test_ragged_batches_match_the_oracle(dev, case):
+    """Ragged batches, idle sequences (no query rows) and sequences of their new tokens only
+    (ctx 0), in both launch orders: against the oracle, and bit-identical on a second call."""
+    name, ctx, q_lens, D, kv = case
+    pool = Pool(ctx, q_lens, 32, 8, D, dev, kv, seed=32)
+    report(f"[ragged {name}] B {len(ctx)} keys {int(pool.seq_lens.sum())}")
+    out = pool.run()
+    again = pool.run()
+    assert bool(torch.isfinite(out.float()).all())
+    assert torch.equal(out, again)
+    live = [b for b in range(len(ctx)) if q_lens[b] > 0]
+    seqs = live if len(live) <= 16 else live[::4]
+    err, mabs = pool.max_err(out, seqs)
+    report(f"[ragged {name}] error {err:.3g} (max-abs {mabs:.3g})")
+    assert err <= (TOL_INT8 if kv == "int8" else TOL_BF16)
