@@ -34,8 +34,12 @@
 //           hold row m and d = (4g + i)*(D/16) + dt.
 // INT8 KV.  K: every code is dequantised to bf16(float(code) * scale) -- the value
 // dequantize() returns (engine/kv_tier_manager.py:41), which the reference attends over --
-// as (code + 128) * s - 128 * s in one fma, exact before the single bf16 rounding, so the
-// score MFMAs see the reference's operands.  V: the codes enter the PV MFMAs
+// as (1024 + code + 128) * s - 1152 * s in one mixed-precision fma on the fp16 word a byte
+// select builds (as for V below), exact before the single bf16 rounding, so the score MFMAs
+// see the reference's operands.  (Exact codes against a per-row-scaled fp16 Q, with the key
+// scale applied to the scores, would save the per-element multiply, but the reference's
+// bf16 rounding of K then goes missing: with config 4's x20 outliers the scores reach
+// ~200 and the outputs move by up to 5%.)  V: the codes enter the PV MFMAs
 // (v_mfma_f32_16x16x32_f16) as exact fp16 integers -- two byte selects place (code + 128)
 // under a 0x64 exponent byte, giving 1024 + code + 128 exactly, and one packed fp16 add
 // removes the 1152 -- and each key's V scale is folded into its probability,
@@ -137,9 +141,12 @@ __device__ __forceinline__ uint32_t max_u16x2(uint32_t a, uint32_t b) {
                                                                 __builtin_bit_cast(u16x2_t, b)));
 }
 
-// Byte `i` of a dword holding (code + 128) bytes -> float(code) * s, exact: u * s - 128 * s.
-__device__ __forceinline__ float dequant_byte(uint32_t ux, int i, float s, float sb) {
-  return fmaf(static_cast<float>((ux >> (8 * i)) & 0xffu), s, sb);
+// Two fp16 (1024 + code + 128), as codes_f16x2 takes them -> bf16x2 of code * s, rounded
+// once: (1024 + u) * s - 1152 * s is code * s exactly (at most 19 significant bits), so each
+// fma (one v_fma_mix, the fp16 half read in place) returns it unrounded.
+__device__ __forceinline__ uint32_t dequant_pair(uint32_t biased, float s, float sb) {
+  const f16x2_t h = __builtin_bit_cast(f16x2_t, biased);
+  return pack_bf16x2(fmaf(static_cast<float>(h[0]), s, sb), fmaf(static_cast<float>(h[1]), s, sb));
 }
 
 __device__ __forceinline__ int64_t clamp_page(int32_t page, int64_t num_blocks) {
@@ -459,6 +466,7 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
     auto scale_of = [&](const u32x2_t& w, int i) {
       return f16_to_f32(static_cast<uint16_t>(w[i >> 1] >> (16 * (i & 1))));
     };
+    constexpr uint32_t k64 = 0x64646464u;  // fp16 exponent bytes of 1024
 
     // ---- V^T operands.  They do not depend on the scores: up to 32 rows they are built
     // first, so their VALU work is scheduled alongside the score MFMAs in one basic block;
@@ -474,7 +482,6 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
       if constexpr (INT8) {
         // exact fp16 codes; the V scales go into P (below).  Two byte selects interleave
         // keys j0, j1 over four d's, two more place each pair under the 0x64 exponent bytes.
-        constexpr uint32_t k64 = 0x64646464u;
 #pragma unroll
         for (int w = 0; w < Raw::kVWords; ++w)
 #pragma unroll
@@ -518,12 +525,12 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
           // the lane's key l16 of sub-tile kt: codes 8*(ks%2) .. +8 of its load ks/2
           const u32x4_t& c4 = raw.k[kt][ks >> 1];
           const float sk = f16_to_f32(static_cast<uint16_t>(raw.ks[kt]));
-          const float skb = -128.0f * sk;
+          const float skb = -1152.0f * sk;
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             const uint32_t ux = c4[(ks & 1) * 2 + h] ^ 0x80808080u;
-            kop[2 * h] = pack_bf16x2(dequant_byte(ux, 0, sk, skb), dequant_byte(ux, 1, sk, skb));
-            kop[2 * h + 1] = pack_bf16x2(dequant_byte(ux, 2, sk, skb), dequant_byte(ux, 3, sk, skb));
+            kop[2 * h] = dequant_pair(__builtin_amdgcn_perm(k64, ux, 0x04010400u), sk, skb);
+            kop[2 * h + 1] = dequant_pair(__builtin_amdgcn_perm(k64, ux, 0x04030402u), sk, skb);
           }
         } else {
           kop = raw.k[kt][ks];
