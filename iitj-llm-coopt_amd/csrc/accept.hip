@@ -7,14 +7,17 @@
 //   1. row_stats_kernel, grid (chunk, row slot, sequence): one chunk of one row per block --
 //      max of x/T and an fp64 sum of exp(x/T - max) (sampling), or max and first argmax
 //      (greedy).  Full chunks are read with unconditional 16-byte loads, all issued before use.
+//      Sampling: the block whose chunk holds the row's draft token also stores x/T there.
 //   2. greedy_kernel, grid (sequence): combines the argmax partials and applies the prefix
 //      rule.  -- or, sampling --
 //      decide_kernel, grid (chunk, sequence): every block combines its sequence's row
-//      statistics and runs the accept loop (it needs only the logits at the draft tokens),
-//      then sums the resampling weights w_j of its chunk; block 0 of each sequence publishes
-//      the accepted prefix and the decision.
+//      statistics (one chunk partial per thread, lane groups reducing each row) and wave 0
+//      makes the accept decision with a ballot over the drafts, all from one round of
+//      independent loads; then the block sums the resampling weights w_j of its chunk.
+//      Block 0 of each sequence publishes the accepted prefix and the decision.
 //   3. select_kernel, grid (sequence): finds the chunk where the cumulative weight crosses
 //      u * sum(w), scans it and writes the emitted token.
+// Per-block reductions and prefix sums in fp64 run on DPP / permlane lane exchanges.
 //
 // Numerics.  Row maxima are exact and sum(exp) is accumulated in fp64.  The probabilities at
 // the draft tokens, which decide acceptance, are formed with an fp64 exp and rounded once to
@@ -93,6 +96,7 @@ struct Workspace {
   Partial1* part1;  // [B][2*gmax+1][nch1]
   Decision* dec;    // [B]
   Partial2* part2;  // [B][nch2]
+  float* tokx;      // [B][2*gmax+1]: x/T at the row's draft token (launch 1 -> launch 2)
 };
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
@@ -109,6 +113,7 @@ __host__ __device__ inline size_t carve(Workspace* w, uintptr_t base, int B, int
   w->part1 = reinterpret_cast<Partial1*>(take(sizeof(Partial1) * B * slots * L.nch1));
   w->dec = reinterpret_cast<Decision*>(take(sizeof(Decision) * B));
   w->part2 = reinterpret_cast<Partial2*>(take(sizeof(Partial2) * B * L.nch2));
+  w->tokx = reinterpret_cast<float*>(take(sizeof(float) * B * slots));
   return off;
 }
 
@@ -229,6 +234,9 @@ __global__ __launch_bounds__(kThreads) void row_stats_kernel(Args a) {
   const void* base = is_draft ? a.drf : a.tgt;
   const int64_t stride = is_draft ? a.drf_stride : a.tgt_stride;
   const int64_t row = is_draft ? drf_row(a, b, i) : tgt_row(a, b, i);
+  // Sampling: the draft token this row is tested at (draft i and target i < g; the bonus
+  // row g has none).  The block whose chunk holds it hands x/T there to launch 2.
+  const int tok = (!GREEDY && (is_draft || i < g)) ? a.dtok[static_cast<int64_t>(b) * a.gmax + i] : -1;
   const int lo = c * a.L.chunk1;
   const int hi = min(a.V, lo + a.L.chunk1);
   const int tid = threadIdx.x;
@@ -283,6 +291,16 @@ __global__ __launch_bounds__(kThreads) void row_stats_kernel(Args a) {
     for (int e = 0; e < kMaxPerThread; ++e) {
       vals[e] *= a.inv_t;
       m = fmaxf(m, vals[e]);
+    }
+    if (tok >= lo && tok < hi) {  // uniform; one thread holds element tok
+      const int t = (tok - lo) >> 3;
+      if (tid == t % kThreads) {
+        const int pos = (t / kThreads) * 8 + ((tok - lo) & 7);
+        float x = 0.0f;
+#pragma unroll
+        for (int e = 0; e < kMaxPerThread; ++e) x = (e == pos) ? vals[e] : x;
+        a.ws.tokx[static_cast<int64_t>(b) * (2 * a.gmax + 1) + slot] = x;
+      }
     }
     m = block_max(m, shf);
     double s = 0.0;
@@ -472,13 +490,15 @@ struct WeightRow {
   }
 };
 
+// trow0 / drow0: tgt_row(a, b, 0) / drf_row(a, b, 0), read by the caller ahead of the decision.
 template <bool BF16>
-__device__ __forceinline__ WeightRow<BF16> make_weight_row(const Args& a, int b, const Decision& dec) {
+__device__ __forceinline__ WeightRow<BF16> make_weight_row(const Args& a, int64_t trow0, int64_t drow0,
+                                                           const Decision& dec) {
   WeightRow<BF16> wr;
   wr.a = &a;
   wr.mode = dec.mode;
-  wr.trow = tgt_row(a, b, dec.k);
-  wr.drow = dec.mode == kModeResidual ? drf_row(a, b, dec.k) : 0;
+  wr.trow = trow0 + dec.k;
+  wr.drow = dec.mode == kModeResidual ? drow0 + dec.k : 0;
   wr.mt_l2 = dec.rt.m * kLog2e;
   wr.mq_l2 = dec.rq.m * kLog2e;
   wr.inv_st = 1.0 / dec.rt.s;
@@ -486,80 +506,164 @@ __device__ __forceinline__ WeightRow<BF16> make_weight_row(const Args& a, int b,
   return wr;
 }
 
-// ---------------------------------------------------------------------------------------
-// Launch 2 (sampling): accept decision (recomputed by every block of the sequence) and the
-// chunk sums of the resampling weights.
-// ---------------------------------------------------------------------------------------
-template <bool BF16>
-__global__ __launch_bounds__(kThreads) void decide_kernel(Args a) {
-  __shared__ RowStat rows[kMaxSlots];
-  __shared__ Decision sdec;
-  __shared__ double shd[4], shd2[4];
-  __shared__ float sh_p[64], sh_q[64];  // p_i[d_i], q_i[d_i]
-  const int c = blockIdx.x, b = blockIdx.y;
-  const int g = gamma_of(a, b);
-  const int tid = threadIdx.x;
-  const int nrow_t = g + 1, nrow_d = a.draft_probs ? 0 : g;
-  const int32_t* d = a.dtok + static_cast<int64_t>(b) * a.gmax;
-  // The logits at the draft tokens do not depend on the row statistics: one lane per
-  // (row, draft) issues its load before the combination below.
-  const bool want_t = tid < g, want_d = tid >= 64 && tid < 64 + g;
-  const int di = want_t ? tid : tid - 64;
-  int tok = -1;
-  float x = 0.0f;
-  if (want_t || want_d) {
-    tok = d[di];
-    if (tok >= 0 && tok < a.V) {
-      if (want_t) x = ld<BF16>(a.tgt, tgt_row(a, b, di), a.tgt_stride, tok) * a.inv_t;
-      else if (a.draft_probs) x = static_cast<const float*>(a.drf)[drf_row(a, b, di) * a.drf_stride + tok];
-      else x = ld<BF16>(a.drf, drf_row(a, b, di), a.drf_stride, tok) * a.inv_t;
+// Max / sum over aligned groups of G = 8 or 16 consecutive lanes (DPP, every lane of a group
+// gets the same bits).
+template <int G>
+__device__ __forceinline__ float group_max_f32(float v) {
+  v = fmaxf(v, dpp_f32<dpp::kXor1>(v));
+  v = fmaxf(v, dpp_f32<dpp::kXor2>(v));
+  v = fmaxf(v, dpp_f32<dpp::kRowHalfMirror>(v));
+  if constexpr (G == 16) v = fmaxf(v, dpp_f32<dpp::kRowMirror>(v));
+  return v;
+}
+template <int G>
+__device__ __forceinline__ double group_sum_f64(double v) {
+  v += dpp_f64<dpp::kXor1>(v);
+  v += dpp_f64<dpp::kXor2>(v);
+  v += dpp_f64<dpp::kRowHalfMirror>(v);
+  if constexpr (G == 16) v += dpp_f64<dpp::kRowMirror>(v);
+  return v;
+}
+
+// Sampling statistics of every row slot of sequence b when a row has at most G chunks: thread
+// t takes chunk t % G of slot s0 + t / G (one load each, all slots at once, whatever g is), and
+// the G lanes of a slot reduce (max, sum * exp(m_c - max)) together.  load_group issues the
+// load; reduce_group uses it.
+struct ChunkStat {
+  float m;
+  double s;
+};
+template <int G>
+__device__ __forceinline__ ChunkStat load_group(const Args& a, int b, int s0) {
+  const int slots = 2 * a.gmax + 1;
+  const int slot = s0 + static_cast<int>(threadIdx.x) / G, c = threadIdx.x % G;
+  ChunkStat q{-INFINITY, 0.0};
+  if (slot < slots && c < a.L.nch1) {
+    const Partial1& p = a.ws.part1[(static_cast<int64_t>(b) * slots + slot) * a.L.nch1 + c];
+    q.m = p.m;
+    q.s = p.s;
+  }
+  return q;
+}
+template <int G>
+__device__ __forceinline__ void reduce_group(const Args& a, ChunkStat q, int s0, RowStat* rows) {
+  const int slot = s0 + static_cast<int>(threadIdx.x) / G;
+  const float mx = group_max_f32<G>(q.m);
+  const double t = q.s * exp(static_cast<double>(q.m) - static_cast<double>(mx));
+  const double sum = group_sum_f64<G>(q.s > 0.0 ? t : 0.0);  // empty chunks add nothing
+  if (threadIdx.x % G == 0 && slot < 2 * a.gmax + 1) {
+    rows[slot].m = mx;
+    rows[slot].argmax = -1;
+    rows[slot].s = sum;
+  }
+}
+
+// The accept decision of sequence b, made by wave 0 (threadIdx.x < 64) from the row statistics
+// in `rows` (LDS).  Lane i holds draft i's token, uniform and the logits at the token (launch 1
+// captured them); their loads are issued by the caller before the rows are combined.
+struct TokenLane {
+  int tok;
+  float xt, xq, u;
+};
+__device__ __forceinline__ TokenLane load_token_lane(const Args& a, int b) {
+  const int lane = threadIdx.x;
+  const int64_t sb = static_cast<int64_t>(b) * (2 * a.gmax + 1);
+  TokenLane t{-1, 0.0f, 0.0f, 0.0f};
+  if (lane < a.gmax) {
+    t.tok = a.dtok[static_cast<int64_t>(b) * a.gmax + lane];
+    t.u = a.u_acc[static_cast<int64_t>(b) * a.gmax + lane];
+    t.xt = a.ws.tokx[sb + lane];
+    if (!a.draft_probs) t.xq = a.ws.tokx[sb + a.gmax + 1 + lane];
+  }
+  return t;
+}
+
+__device__ __forceinline__ Decision decide_wave(const Args& a, int b, int g, TokenLane t,
+                                                const RowStat* rows, bool publish) {
+  const int lane = threadIdx.x;
+  const int tok = t.tok;
+  const float u = t.u;
+  float mt = -INFINITY, mq = -INFINITY;
+  double st = 0.0, sq = 0.0;
+  if (lane < g) {
+    mt = rows[lane].m;
+    st = rows[lane].s;
+    if (!a.draft_probs) {
+      mq = rows[a.gmax + 1 + lane].m;
+      sq = rows[a.gmax + 1 + lane].s;
     }
   }
-  combine_rows_waves(a, b, nrow_t, nrow_d, rows);
-  __syncthreads();
-  if (want_t || want_d) {
-    const bool valid = tok >= 0 && tok < a.V;
-    if (want_t) {
-      sh_p[di] = valid ? prob_at(x, rows[di].m, rows[di].s) : 0.0f;
-    } else {
-      const RowStat& rq = rows[a.gmax + 1 + di];
-      sh_q[di] = !valid ? 1.0f : (a.draft_probs ? x : prob_at(x, rq.m, rq.s));
-    }
+  const float xt = t.xt;
+  float xq = t.xq;
+  const bool live = lane < g;
+  const bool valid = tok >= 0 && tok < a.V;
+  if (a.draft_probs && live && valid) xq = static_cast<const float*>(a.drf)[drf_row(a, b, lane) * a.drf_stride + tok];
+  float ratio = 0.0f;
+  if (live) {
+    // an out-of-vocabulary draft token has p = 0, so it is rejected
+    const float p = valid ? prob_at(xt, mt, st) : 0.0f;
+    const float q = !valid ? 1.0f : (a.draft_probs ? xq : prob_at(xq, mq, sq));
+    ratio = fminf(p / fmaxf(q, 1e-20f), 1.0f);
   }
-  __syncthreads();
-  if (tid == 0) {
-    const float* u = a.u_acc + static_cast<int64_t>(b) * a.gmax;
-    int k = g, mode = kModeBonus;
-    float margin = INFINITY;
-    for (int i = 0; i < g; ++i) {
-      // an out-of-vocabulary draft token has ratio 0 and is rejected (p = 0 above)
-      const float ratio = fminf(sh_p[i] / fmaxf(sh_q[i], 1e-20f), 1.0f);
-      margin = fminf(margin, fabsf(u[i] - ratio));
-      if (u[i] >= ratio) {
-        k = i;
-        mode = kModeResidual;
-        break;
-      }
+  // k = the first i with u_i >= ratio_i; margin over the tests made up to and including it
+  const uint64_t rej = __ballot(live && u >= ratio);
+  const int k = rej ? __builtin_ctzll(rej) : g;
+  const float mg = wave_min_f32_dpp((live && lane <= k) ? fabsf(u - ratio) : INFINITY);
+  Decision d;
+  d.k = k;
+  d.mode = k < g ? kModeResidual : kModeBonus;
+  d.margin = mg;
+  d.pad = 0;
+  d.rt = rows[k];
+  d.rt.argmax = -1;
+  d.rq = (d.mode == kModeResidual && !a.draft_probs) ? rows[a.gmax + 1 + k] : d.rt;
+  if (publish) {
+    int32_t* out = a.out_tok + static_cast<int64_t>(b) * (a.gmax + 1);
+    for (int i = lane; i <= a.gmax; i += 64) {
+      if (i < k) out[i] = tok;  // i < k <= 63: i == lane, whose tok is d_i
+      else if (i > k) out[i] = -1;
     }
-    Decision dec;
-    dec.k = k;
-    dec.mode = mode;
-    dec.margin = margin;
-    dec.pad = 0;
-    dec.rt = rows[k];
-    dec.rq = (mode == kModeResidual && !a.draft_probs) ? rows[a.gmax + 1 + k] : rows[k];
-    sdec = dec;
-    if (c == 0) {
-      a.ws.dec[b] = dec;
-      int32_t* out = a.out_tok + static_cast<int64_t>(b) * (a.gmax + 1);
-      for (int i = 0; i < k; ++i) out[i] = d[i];
-      for (int i = k + 1; i <= a.gmax; ++i) out[i] = -1;
+    if (lane == 0) {
+      a.ws.dec[b] = d;
       a.acc_len[b] = k;
     }
   }
+  return d;
+}
+
+// ---------------------------------------------------------------------------------------
+// Launch 2 (sampling): accept decision (made again by every block of the sequence, from the
+// same data, so identically) and the chunk sums of the resampling weights.
+// ---------------------------------------------------------------------------------------
+template <bool BF16, int LC>
+__global__ __launch_bounds__(kThreads) void decide_kernel(Args a) {
+  __shared__ RowStat rows[kMaxSlots];
+  __shared__ Decision sdec;
+  __shared__ double shw[4], shp[4];
+  const int c = blockIdx.x, b = blockIdx.y;
+  const int g = gamma_of(a, b);
+  const int64_t trow0 = tgt_row(a, b, 0), drow0 = drf_row(a, b, 0);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  TokenLane tl{-1, 0.0f, 0.0f, 0.0f};
+  if constexpr (LC == 0) {
+    if (wave == 0) tl = load_token_lane(a, b);
+    combine_rows_waves(a, b, g + 1, a.draft_probs ? 0 : g, rows);
+  } else {
+    // the first pass's partial loads, then wave 0's token loads, then the first use
+    ChunkStat q = load_group<LC>(a, b, 0);
+    if (wave == 0) tl = load_token_lane(a, b);
+    reduce_group<LC>(a, q, 0, rows);
+    for (int s0 = kThreads / LC; s0 < 2 * a.gmax + 1; s0 += kThreads / LC)
+      reduce_group<LC>(a, load_group<LC>(a, b, s0), s0, rows);
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const Decision d = decide_wave(a, b, g, tl, rows, c == 0);
+    if (lane == 0) sdec = d;
+  }
   __syncthreads();
   const Decision dec = sdec;
-  const WeightRow<BF16> wr = make_weight_row<BF16>(a, b, dec);
+  const WeightRow<BF16> wr = make_weight_row<BF16>(a, trow0, drow0, dec);
   const int lo = c * a.L.chunk2;
   const int hi = min(a.V, lo + a.L.chunk2);
   const bool vec = a.vec_t && (dec.mode == kModeBonus || a.vec_d);
@@ -605,30 +709,36 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(Args a) {
       }
     }
   }
-  sw = block_sum(sw, shd);
-  sp = block_sum(sp, shd2);
+  sw = wave_sum_f64_dpp(sw);
+  sp = wave_sum_f64_dpp(sp);
+  if (lane == 0) {
+    shw[wave] = sw;
+    shp[wave] = sp;
+  }
+  __syncthreads();
   if (tid == 0) {
     Partial2 pp;
-    pp.w = sw;
-    pp.p = sp;
+    pp.w = (shw[0] + shw[1]) + (shw[2] + shw[3]);
+    pp.p = (shp[0] + shp[1]) + (shp[2] + shp[3]);
     a.ws.part2[static_cast<int64_t>(b) * a.L.nch2 + c] = pp;
   }
 }
 
-// Inclusive block scan of one fp64 value per thread (4 waves).
-__device__ __forceinline__ double block_inclusive_scan(double v, double* sh) {
+// Inclusive block scan of one fp64 value per thread (4 waves): the wave scans, then the
+// totals of the waves before this one added in wave order.  excl = the previous thread's
+// inclusive value, bit for bit (+0.0 for thread 0); total = thread kThreads-1's.  sh[4] must
+// not be rewritten before every thread has returned.
+__device__ __forceinline__ double block_scan_f64(double v, double* sh, double& excl, double& total) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {
-    const double o = __shfl_up(v, m, 64);
-    if (lane >= m) v += o;
-  }
-  if (lane == 63) sh[w] = v;
+  double wex;
+  const double wincl = wave_incl_scan_f64(v, wex);
+  if (lane == 63) sh[w] = wincl;
   __syncthreads();
   double off = 0.0;
   for (int q = 0; q < w; ++q) off += sh[q];
-  __syncthreads();
-  return off + v;
+  total = ((sh[0] + sh[1]) + sh[2]) + sh[3];  // == the fold off + wincl of thread kThreads-1
+  excl = lane == 0 ? off : off + wex;
+  return off + wincl;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -636,52 +746,52 @@ __device__ __forceinline__ double block_inclusive_scan(double v, double* sh) {
 // ---------------------------------------------------------------------------------------
 template <bool BF16>
 __global__ __launch_bounds__(kThreads) void select_kernel(Args a) {
-  __shared__ double shd[4];
-  __shared__ double wave_last[4];
-  __shared__ int sh_chunk, sh_last, sh_tok_min;
-  __shared__ double sh_total;
-  __shared__ float sh_margin;
+  __shared__ double shs1[4], shs2[4], shs3[4];
   __shared__ double csum[kThreads];
-  const int b = blockIdx.x, tid = threadIdx.x;
+  __shared__ int sh_cross[4], sh_lastm[4];
+  __shared__ int sh_tok_min;
+  __shared__ float sh_margin;
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const Decision dec = a.ws.dec[b];
-  const WeightRow<BF16> wr = make_weight_row<BF16>(a, b, dec);
   const Partial2* P = a.ws.part2 + static_cast<int64_t>(b) * a.L.nch2;
   double wv = 0.0, pv = 0.0;
   if (tid < a.L.nch2) {  // nch2 <= kThreads by construction
     wv = P[tid].w;
     pv = P[tid].p;
   }
+  const float ures = a.u_res[b];
+  const WeightRow<BF16> wr = make_weight_row<BF16>(a, tgt_row(a, b, 0), drf_row(a, b, 0), dec);
   if (tid == 0) {
     sh_tok_min = 0x7fffffff;
     sh_margin = 0.0f;
-    sh_chunk = -1;
-    sh_last = 0;
   }
-  // Chunk sums -> inclusive prefix sums, one chunk per thread (fp64, tree order).  The
-  // resampling weights are used unless the residual sums to zero, then the target
-  // probabilities p_k (spec_decode.py:48).
-  double cincl = block_inclusive_scan(wv, shd);
-  if (tid == kThreads - 1) sh_total = cincl;
-  __syncthreads();
-  const int use_p = (dec.mode == kModeResidual && !(sh_total > 0.0)) ? 1 : 0;  // uniform
+  // Chunk sums -> inclusive prefix sums, one chunk per thread (fp64).  The resampling weights
+  // are used unless the residual sums to zero, then the target probabilities p_k
+  // (spec_decode.py:48).
+  double cexcl, total;
+  double cincl = block_scan_f64(wv, shs1, cexcl, total);
+  const int use_p = (dec.mode == kModeResidual && !(total > 0.0)) ? 1 : 0;  // uniform
   const double mass = use_p ? pv : wv;
-  if (use_p) {
-    cincl = block_inclusive_scan(pv, shd);
-    if (tid == kThreads - 1) sh_total = cincl;
-  }
+  if (use_p) cincl = block_scan_f64(pv, shs2, cexcl, total);
   csum[tid] = cincl;
-  __syncthreads();
-  const double total = sh_total;
-  const double tau = static_cast<double>(a.u_res[b]) * total;
-  const double cexcl = tid == 0 ? 0.0 : csum[tid - 1];
+  const double tau = static_cast<double>(ures) * total;
   // the prefix is non-decreasing, so at most one chunk has excl <= tau < incl
-  if (tid < a.L.nch2 && mass > 0.0) {
-    if (cexcl <= tau && tau < cincl) sh_chunk = tid;
-    atomicMax(&sh_last, tid);
+  const bool has = tid < a.L.nch2 && mass > 0.0;
+  const uint64_t cross = __ballot(has && cexcl <= tau && tau < cincl);
+  const uint64_t hasm = __ballot(has);
+  if (lane == 0) {
+    sh_cross[wave] = cross ? wave * 64 + __builtin_ctzll(cross) : -1;
+    sh_lastm[wave] = hasm ? wave * 64 + 63 - __builtin_clzll(hasm) : 0;
   }
   __syncthreads();
   // tau within rounding of the total: the last chunk with mass
-  const int chunk = sh_chunk >= 0 ? sh_chunk : sh_last;
+  int chunk = -1, lastm = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (chunk < 0 && sh_cross[q] >= 0) chunk = sh_cross[q];
+    lastm = max(lastm, sh_lastm[q]);
+  }
+  if (chunk < 0) chunk = lastm;
   const double acc = chunk == 0 ? 0.0 : csum[chunk - 1];
   const int clo = chunk * a.L.chunk2;
   const int chi = min(a.V, clo + a.L.chunk2);
@@ -744,12 +854,9 @@ __global__ __launch_bounds__(kThreads) void select_kernel(Args a) {
     for (int e = 0; e < 8; ++e)
       if (e < n) local += static_cast<double>(use_p ? p[e] : w[e]);
   }
-  const double incl = block_inclusive_scan(local, shd);
-  // Thread t owns [acc + incl_{t-1}, acc + incl_t); incl_{t-1} comes from the neighbour.
-  const double prev_incl = __shfl_up(incl, 1, 64);
-  if ((tid & 63) == 63) wave_last[tid >> 6] = incl;
-  __syncthreads();
-  const double start = tid == 0 ? 0.0 : ((tid & 63) == 0 ? wave_last[(tid >> 6) - 1] : prev_incl);
+  double start, tot_unused;
+  const double incl = block_scan_f64(local, shs3, start, tot_unused);
+  // Thread t owns [acc + incl_{t-1}, acc + incl_t).
   const bool claim = (acc + start <= tau) && (tau < acc + incl) && (thi > tlo);
   int tok = -1;
   float mg = 0.0f;
@@ -847,7 +954,14 @@ int launch_all(Args& a, bool greedy, hipStream_t s) {
     hipLaunchKernelGGL(greedy_kernel, dim3(a.B), dim3(kThreads), 0, s, a);
     return coopt::check_launch("coopt_accept_sample/greedy");
   }
-  hipLaunchKernelGGL((decide_kernel<BF16>), dim3(a.L.nch2, a.B), dim3(kThreads), 0, s, a);
+  // rows of at most 16 chunk partials are combined by lane groups, one partial per thread
+  const dim3 g2(a.L.nch2, a.B);
+  if (a.L.nch1 <= 8)
+    hipLaunchKernelGGL((decide_kernel<BF16, 8>), g2, dim3(kThreads), 0, s, a);
+  else if (a.L.nch1 <= 16)
+    hipLaunchKernelGGL((decide_kernel<BF16, 16>), g2, dim3(kThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL((decide_kernel<BF16, 0>), g2, dim3(kThreads), 0, s, a);
   rc = coopt::check_launch("coopt_accept_sample/decide");
   if (rc != COOPT_OK) return rc;
   hipLaunchKernelGGL((select_kernel<BF16>), dim3(a.B), dim3(kThreads), 0, s, a);

@@ -81,6 +81,96 @@ __device__ __forceinline__ float add_xor32(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// ---- DPP lane exchanges (VALU, no LDS round trip) -------------------------------------
+// dpp_ctrl codes of GFX9: quad permutes, mirrors within a 16-lane row or 8-lane half row,
+// shifts within a row, and the row broadcasts used for wave-wide scans.
+namespace dpp {
+constexpr int kXor1 = 0xB1;        // quad_perm [1,0,3,2]: lane i ^ 1
+constexpr int kXor2 = 0x4E;        // quad_perm [2,3,0,1]: lane i ^ 2
+constexpr int kRowShr1 = 0x111;    // lane i - 1 within the row
+constexpr int kRowShr2 = 0x112;
+constexpr int kRowShr4 = 0x114;
+constexpr int kRowShr8 = 0x118;
+constexpr int kRowMirror = 0x140;      // lane 15 - i within the row
+constexpr int kRowHalfMirror = 0x141;  // lane 7 - i within the half row
+constexpr int kRowBcast15 = 0x142;     // lane 15 of the previous row
+constexpr int kRowBcast31 = 0x143;     // lane 31
+constexpr int kWaveShr1 = 0x138;       // lane i - 1 across the wave
+}  // namespace dpp
+
+// v of the lane CTRL names; lanes without a source (or in rows outside ROW_MASK) get `old`.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v, uint32_t old = 0) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(static_cast<int>(old), static_cast<int>(v), CTRL, ROW_MASK, 0xf, false));
+}
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ double dpp_f64(double v) {  // lanes without a source get +0.0
+  const uint64_t u = static_cast<uint64_t>(__double_as_longlong(v));
+  const uint32_t lo = dpp_u32<CTRL, ROW_MASK>(static_cast<uint32_t>(u));
+  const uint32_t hi = dpp_u32<CTRL, ROW_MASK>(static_cast<uint32_t>(u >> 32));
+  return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __uint_as_float(dpp_u32<CTRL>(__float_as_uint(v)));
+}
+
+// (own, partner) values of lane i ^ 16 / i ^ 32 for a double (see max_xor16 below: the pair
+// comes back in lane-dependent order, the same for both halves).
+__device__ __forceinline__ void swap_xor_f64(double v, bool x32, double& a, double& b) {
+  const uint64_t u = static_cast<uint64_t>(__double_as_longlong(v));
+  const uint32_t lo = static_cast<uint32_t>(u), hi = static_cast<uint32_t>(u >> 32);
+  typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+  const u2 rl = x32 ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false)
+                    : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+  const u2 rh = x32 ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false)
+                    : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+  a = __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(rh[0]) << 32) | rl[0]));
+  b = __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(rh[1]) << 32) | rl[1]));
+}
+
+// Wave-wide fp64 sum.  Every step adds a lane's value to its partner's, and a + b == b + a,
+// so every lane ends with the same bits.
+__device__ __forceinline__ double wave_sum_f64_dpp(double v) {
+  v += dpp_f64<dpp::kXor1>(v);
+  v += dpp_f64<dpp::kXor2>(v);
+  v += dpp_f64<dpp::kRowHalfMirror>(v);
+  v += dpp_f64<dpp::kRowMirror>(v);
+  double a, b;
+  swap_xor_f64(v, false, a, b);
+  v = a + b;
+  swap_xor_f64(v, true, a, b);
+  return a + b;
+}
+
+// Wave-wide fp32 minimum, every lane the same result.
+__device__ __forceinline__ float wave_min_f32_dpp(float v) {
+  v = fminf(v, dpp_f32<dpp::kXor1>(v));
+  v = fminf(v, dpp_f32<dpp::kXor2>(v));
+  v = fminf(v, dpp_f32<dpp::kRowHalfMirror>(v));
+  v = fminf(v, dpp_f32<dpp::kRowMirror>(v));
+  typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+  u2 r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fminf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fminf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Inclusive fp64 prefix sum over the wave's lanes (lane 0 first): Hillis-Steele within each
+// 16-lane row, then the row totals carried forward with the row broadcasts.  `excl` gets the
+// previous lane's inclusive value (+0.0 in lane 0), bit for bit.
+__device__ __forceinline__ double wave_incl_scan_f64(double v, double& excl) {
+  v += dpp_f64<dpp::kRowShr1>(v);
+  v += dpp_f64<dpp::kRowShr2>(v);
+  v += dpp_f64<dpp::kRowShr4>(v);
+  v += dpp_f64<dpp::kRowShr8>(v);
+  v += dpp_f64<dpp::kRowBcast15, 0xa>(v);
+  v += dpp_f64<dpp::kRowBcast31, 0xc>(v);
+  excl = dpp_f64<dpp::kWaveShr1>(v);
+  return v;
+}
+
 template <typename T>
 __device__ __forceinline__ T wave_shfl_xor(T v, int mask) {
   return __shfl_xor(v, mask, COOPT_WAVE);

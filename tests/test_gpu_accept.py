@@ -142,6 +142,33 @@ def test_draft_probability_mode_and_ragged_gamma_and_row_offsets(dev):
     compare(res, acc, toks, marg, "ragged")
 
 
+@pytest.mark.parametrize("B,g,V,gam", [
+    (2, 4, 128256, None),          # many chunks per row: the block-wide row combine
+    (3, 64, 2000, [64, 0, 37]),    # gamma_max 64: the bonus row is row 64
+    (5, 63, 2000, [63, 63, 10, 1, 0]),  # the widest gamma a single wave decides
+])
+def test_small_batch_and_long_gamma_match_oracle(dev, B, g, V, gam):
+    gen = torch.Generator(device=dev).manual_seed(100 + g)
+    tl = torch.randn(B, g + 1, V, generator=gen, device=dev) * 2.0
+    # a draft close to the target, so long prefixes are accepted
+    dl = (tl[:, :g] + torch.randn(B, g, V, generator=gen, device=dev) * 0.05).contiguous()
+    rng = np.random.default_rng(g)
+    q = OA.softmax32(dl.cpu().numpy())
+    ud = rng.random((B, g), dtype=np.float32)
+    dt = np.array([[OA.inverse_cdf(q[b, i], ud[b, i])[0] for i in range(g)] for b in range(B)])
+    dt = dt.reshape(B, g).astype(np.int64)
+    ua = rng.random((B, g), dtype=np.float32) * 0.9
+    ur = rng.random(B, dtype=np.float32)
+    kw = {}
+    if gam is not None:
+        kw["gamma_per_seq"] = torch.tensor(gam, device=dev)
+    res = M.accept(tl, dl, torch.from_numpy(dt).to(dev), 1.0, torch.from_numpy(ua).to(dev),
+                   torch.from_numpy(ur).to(dev), **kw)
+    acc, toks, marg = OA.accept_batch(tl.cpu().numpy(), dl.cpu().numpy(), dt, 1.0, ua, ur,
+                                      gamma_per_seq=None if gam is None else np.array(gam))
+    compare(res, acc, toks, marg, f"B={B} gamma={g} V={V}")
+
+
 def test_special_cases(dev):
     gen = torch.Generator(device=dev).manual_seed(7)
     V = 3000
