@@ -614,9 +614,14 @@ __device__ __forceinline__ Decision decide_wave(const Args& a, int b, int g, Tok
   d.mode = k < g ? kModeResidual : kModeBonus;
   d.margin = mg;
   d.pad = 0;
-  d.rt = rows[k];
+  // field by field from scalar reads (a whole-struct copy through the pointer went to scratch)
+  const int kq = (d.mode == kModeResidual && !a.draft_probs) ? a.gmax + 1 + k : k;
+  d.rt.m = rows[k].m;
   d.rt.argmax = -1;
-  d.rq = (d.mode == kModeResidual && !a.draft_probs) ? rows[a.gmax + 1 + k] : d.rt;
+  d.rt.s = rows[k].s;
+  d.rq.m = rows[kq].m;
+  d.rq.argmax = -1;
+  d.rq.s = rows[kq].s;
   if (publish) {
     int32_t* out = a.out_tok + static_cast<int64_t>(b) * (a.gmax + 1);
     for (int i = lane; i <= a.gmax; i += 64) {

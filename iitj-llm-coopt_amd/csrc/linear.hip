@@ -300,6 +300,9 @@ Plan plan_for(int M, int N, int K) {
   Plan p{m_tiles(M), 1, 8, 1, K};
   if (p.mt <= 4 && N < 65536) p.waves = 4;
   if (p.mt <= 4 && N >= 65536) p.nw = 4;
+  // 16 row tiles, or 4 row tiles with 4 column tiles per wave, exceed two waves' registers
+  // per SIMD (they spilled to scratch): 4-wave blocks, one wave per SIMD, hold them.
+  if (p.mt == 16 || (p.mt == 4 && p.nw == 4)) p.waves = 4;
   const int cols = p.waves * p.nw * 16;
   const int nb = (N + cols - 1) / cols;
   const int steps = K / kKB;
@@ -322,11 +325,22 @@ void launch_cfg(const Plan& p, const LinArgs& a, bool packed, hipStream_t s) {
 
 template <int MT>
 void launch_mt(const Plan& p, const LinArgs& a, bool packed, hipStream_t s) {
-  if constexpr (MT <= 4) {
-    if (p.nw == 4) return launch_cfg<MT, 4, 8, 2>(p, a, packed, s);
-    if (p.waves == 4) return launch_cfg<MT, 1, 4, 2>(p, a, packed, s);
+  if constexpr (MT == 16) {
+    launch_cfg<MT, 1, 4, 2>(p, a, packed, s);
+  } else {
+    if constexpr (MT <= 4) {
+      if (p.nw == 4) {
+        if constexpr (MT == 4) {
+          launch_cfg<MT, 4, 4, 2>(p, a, packed, s);
+        } else {
+          launch_cfg<MT, 4, 8, 2>(p, a, packed, s);
+        }
+        return;
+      }
+      if (p.waves == 4) return launch_cfg<MT, 1, 4, 2>(p, a, packed, s);
+    }
+    launch_cfg<MT, 1, 8, 2>(p, a, packed, s);
   }
-  launch_cfg<MT, 1, 8, 2>(p, a, packed, s);
 }
 
 // Tile packing: thread o writes 16-byte chunk o of the packed layout, reading it from the
