@@ -305,7 +305,19 @@ def kv_write_case(torch, M, dev, T, seed):
         for kk in ("all_cores", "threads_8"):
             legs[kk]["us_per_call"] = legs[kk]["seconds"] * 1e6
         write()
-        legs["codes_equal_to_gpu"] = bool(torch.equal(ck[blk, off], kc[slots // bs, slots % bs].cpu()))
+        # torch-CPU divides by 127 exactly; on the GPU the reference's "/ 127" is a multiply by
+        # fp32(1/127) (what the kernel restates), so a few near-tie elements round apart.
+        # Reported: how many codes the two differ in, and whether the GPU's codes equal the
+        # oracle codec's GPU-division mode on every element.
+        ndiff, total, dev_equal = 0, 0, True
+        for x, c, gc in ((hk, ck, kc), (hv, cv, vc)):
+            gpu = gc[slots // bs, slots % bs].cpu()
+            ndiff += int((c[blk, off] != gpu).sum())
+            total += gpu.numel()
+            dq, _ = OC.quantize(x.float().numpy(), 8, mode="device")
+            dev_equal &= bool(np.array_equal(dq, gpu.numpy()))
+        legs["codes_differing_from_gpu"] = f"{ndiff} of {total} (torch-CPU true division)"
+        legs["gpu_codes_equal_to_oracle_gpu_division"] = dev_equal
         legs["sample"] = f"the whole call: {T} tokens, torch-CPU"
         res["cpu"] = legs
     return res
