@@ -267,14 +267,25 @@ def accept_case(torch, M, dev, B, gamma, V, seed):
 
 
 def kv_write_case(torch, M, dev, T, seed):
-    """Config 2 shape: T new tokens (256 sequences x 5 = 1280), Hkv 8, D 128, INT8 quantise on
-    write into a 65,536-block pool, slots a seeded random subset; N(0,1) with 1% x20 outliers."""
+    """Config 2: 256 sequences append T / 256 new tokens each (5 at config 2's T = 1280; 256
+    in the T = 65,536 sweep) at existing lengths U[0, 4096), with block tables from a seeded
+    permutation of a 65,536-block pool (BlockManager's free list), so each sequence's new
+    tokens fill consecutive slots of its blocks; Hkv 8, D 128, INT8 quantise on write; N(0,1)
+    with 1% x20 outliers."""
     import numpy as np
 
-    NB, bs, Hkv, D = 65536, 16, 8, 128
+    NB, bs, Hkv, D, nseq = 65536, 16, 8, 128, 256
+    new = T // nseq
     kc, vc, ks, vs = M.allocate_kv_cache(NB, bs, Hkv, D, "int8", device=dev)
-    perm = np.random.default_rng(seed).permutation(NB * bs)[:T]
-    slots = torch.from_numpy(perm.astype(np.int64)).to(dev)
+    rng = np.random.default_rng(seed)
+    bm = M.BlockManager(NB, bs, free_order=rng.permutation(NB))
+    existing = rng.integers(0, 4096, nseq)
+    parts = []
+    for sq in range(nseq):
+        bm.ensure(sq, int(existing[sq]) + new)
+        parts.append(bm.slot_mapping(sq, int(existing[sq]), int(existing[sq]) + new).numpy())
+    slots = torch.from_numpy(np.concatenate(parts).astype(np.int64)).to(dev)
+    T = int(slots.numel())
     g = torch.Generator(device=dev).manual_seed(seed)
     kv = torch.randn(2, T, Hkv, D, generator=g, device=dev)
     kv = torch.where(torch.rand(kv.shape, generator=g, device=dev) < 0.01, kv * 20, kv)

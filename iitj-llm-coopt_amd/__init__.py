@@ -13,7 +13,8 @@ surface of mohsinmubarak/iitj-llm-coopt's engine:
 """
 from . import _lib  # noqa: F401  (imports torch first, then binds the library lazily)
 from . import fused  # noqa: F401  (rms_norm / rope_ / silu_and_mul forward stages)
-from .attention import flash_attn_varlen_func, paged_attention
+from .attention import (flash_attn_varlen_func, paged_attention, paged_attention_qkv,
+                        qkv_attention_supported)
 from .batch import Batch, WorkItem, build_batch, build_padded_batch
 from .block_manager import BlockManager, OutOfBlocks
 from .kv_blocks import allocate_block_major_kv, copy_blocks, migrate_out_of
@@ -24,7 +25,7 @@ from .kv_tier import (KVTierManager, SwappedKV, swap_in_blocks, swap_in_caches, 
 from .spec_decode import AcceptResult, accept, sample, softmax, verify
 
 __all__ = [
-    "flash_attn_varlen_func", "paged_attention", "Batch", "WorkItem", "build_batch",
+    "flash_attn_varlen_func", "paged_attention", "paged_attention_qkv", "qkv_attention_supported", "Batch", "WorkItem", "build_batch",
     "build_padded_batch", "BlockManager", "OutOfBlocks", "allocate_kv_cache", "dequantize",
     "quantize", "reshape_and_cache_flash", "AcceptResult", "accept", "sample", "softmax",
     "verify", "KVTierManager", "SwappedKV", "swap_in_blocks", "swap_out_blocks",

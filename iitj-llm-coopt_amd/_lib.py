@@ -55,6 +55,11 @@ SIGNATURES = {
                                 _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i, _i, _i,
                                 _i, _i, _i64, _p]),
     "coopt_verify_attention_workspace": (_sz, [_i, _i, _i, _i, _i, _i]),
+    "coopt_verify_attention_qkv_supported": (_i, [_i, _i, _i, _i, _i, _i, _i]),
+    "coopt_verify_attention_qkv": (_i, [_i, _p, _i64, _p, _i, _i64, _p, _p, _p, _i64, _i, _p,
+                                        _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64,
+                                        _p, _i64, _p, _p, _i, _i, _i, _i, _i, _i64, _i, _i, _f,
+                                        _p, _i64, _i64, _p, _sz, _p]),
     "coopt_verify_attention": (_i, [_i, _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _i64,
                                     _i64, _i64, _p, _i64, _p, _p, _i, _i, _i, _i, _i, _i64, _i,
                                     _i, _f, _p, _i64, _i64, _p, _sz, _p]),

@@ -9,105 +9,9 @@
 //   scale = fp16(s32), round to nearest even
 // Dequantisation (engine/kv_tier_manager.py:34-41): out = dtype(float(code) * float(scale)).
 #include "common.h"
+#include "kv_store.h"
 
 namespace {
-
-constexpr float kClampMin = 1e-8f;  // torch converts clamp_min(1e-8) to the tensor's fp32
-
-template <int QMAX>
-__device__ __forceinline__ float quant_scale(float amax) {
-  return fmaxf(amax, kClampMin) * (1.0f / static_cast<float>(QMAX));
-}
-
-// code = rint(fl(x / s32)) clamped to [-QMAX, QMAX], fl the IEEE fp32 quotient, computed as
-// rint(x * r32) with r32 = v_rcp_f32(s32) (1 ulp).  Because s32 >= amax / 127 up to rounding,
-// |x / s32| < 128, where an ulp is at most 2^-17: the reciprocal's relative error (2^-23)
-// and the product's rounding leave x * r32 within 2.5 ulp of x / s32, hence within 3 ulp
-// (< 2^-14) of fl(x / s32), so both round to the same integer unless x * r32 lies within
-// kNearTie of a half-integer.  There the IEEE division decides.
-// The result is the IEEE path's for every input (ties included), at a fraction of its work.
-constexpr float kNearTie = 0x1p-14f;
-
-template <int QMAX>
-__device__ __forceinline__ int quant_code(float x, float s32, float r32) {
-  const float q = x * r32;
-  float r = rintf(q);
-  if (fabsf(q - r) >= 0.5f - kNearTie) r = rintf(x / s32);
-  r = fminf(fmaxf(r, -static_cast<float>(QMAX)), static_cast<float>(QMAX));
-  return static_cast<int>(r);
-}
-
-// quant_code of the 8 bf16 elements in w[0..3] (element 2i in the low half of w[i]), with one
-// branch for the lane: if any element is near a boundary, all 8 take the IEEE division.
-template <int QMAX>
-__device__ __forceinline__ void quant_codes8(const uint32_t (&w)[4], float s32, int (&code)[8]) {
-  const float r32 = __builtin_amdgcn_rcpf(s32);
-  float x[8], r[8];
-  bool near = false;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    x[e] = bf16_to_f32(static_cast<uint16_t>(w[e / 2] >> (16 * (e & 1))));
-    const float q = x[e] * r32;
-    r[e] = rintf(q);
-    near |= fabsf(q - r[e]) >= 0.5f - kNearTie;
-  }
-  if (near) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) r[e] = rintf(x[e] / s32);
-  }
-#pragma unroll
-  for (int e = 0; e < 8; ++e)
-    code[e] = static_cast<int>(fminf(fmaxf(r[e], -static_cast<float>(QMAX)), static_cast<float>(QMAX)));
-}
-
-// ---------------------------------------------------------------------------------------
-// KV write.  One lane per 16-byte chunk (8 bf16) of a (token, head) vector; G = D/8 lanes
-// (an aligned power-of-two group inside the wave) cover one vector, and each lane handles
-// the same chunk of K and of V, so every load and store is a 16- or 8-byte access.
-// ---------------------------------------------------------------------------------------
-// Lane c of a G-lane group stores elements [8c, 8c + 8) of one (token, head) K and V vector
-// at cache element offset c_off: bf16 as is, or INT8 codes with the group's fp16 scale at
-// s_off (kv_tier_manager.quantize(x, 8) per vector, engine/kv_tier_manager.py:21-31).
-template <int G, bool INT8>
-__device__ __forceinline__ void store_kv_chunk(uint4 kr, uint4 vr, void* kc, void* vc,
-                                               int64_t c_off, uint16_t* ks, uint16_t* vs,
-                                               int64_t s_off, int c) {
-  if constexpr (!INT8) {
-    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(kc) + c_off) = kr;
-    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(vc) + c_off) = vr;
-  } else {
-    const uint32_t kw[4] = {kr.x, kr.y, kr.z, kr.w};
-    const uint32_t vw[4] = {vr.x, vr.y, vr.z, vr.w};
-    uint32_t kmax = 0, vmax = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      // |bf16| ordering equals integer ordering of the low 15 bits for finite values.
-      const uint32_t k0 = kw[i] & 0x7fffu, k1 = (kw[i] >> 16) & 0x7fffu;
-      const uint32_t v0 = vw[i] & 0x7fffu, v1 = (vw[i] >> 16) & 0x7fffu;
-      kmax = max(kmax, max(k0, k1));
-      vmax = max(vmax, max(v0, v1));
-    }
-    kmax = group_max_u32<G>(kmax);
-    vmax = group_max_u32<G>(vmax);
-    const float ksc = quant_scale<127>(bf16_to_f32(static_cast<uint16_t>(kmax)));
-    const float vsc = quant_scale<127>(bf16_to_f32(static_cast<uint16_t>(vmax)));
-    int kcode[8], vcode[8];
-    quant_codes8<127>(kw, ksc, kcode);
-    quant_codes8<127>(vw, vsc, vcode);
-    uint32_t kq[2] = {0, 0}, vq[2] = {0, 0};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      kq[i / 4] |= (static_cast<uint32_t>(kcode[i]) & 0xffu) << (8 * (i & 3));
-      vq[i / 4] |= (static_cast<uint32_t>(vcode[i]) & 0xffu) << (8 * (i & 3));
-    }
-    *reinterpret_cast<uint2*>(static_cast<int8_t*>(kc) + c_off) = make_uint2(kq[0], kq[1]);
-    *reinterpret_cast<uint2*>(static_cast<int8_t*>(vc) + c_off) = make_uint2(vq[0], vq[1]);
-    if (c == 0) {
-      ks[s_off] = f32_to_f16(ksc);
-      vs[s_off] = f32_to_f16(vsc);
-    }
-  }
-}
 
 template <int G, bool INT8>
 __global__ __launch_bounds__(256) void kv_write_kernel(
@@ -170,9 +74,6 @@ struct QkvArgs {
   int bs_shift;  // log2(block_size) when it is a power of two, else -1
 };
 
-__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
-  return f32_to_bf16(a) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
-}
 
 // Elements [col, col + 8) of row t: bf16 from the qkv output, or bf16(sum of the partials).
 __device__ __forceinline__ uint4 qkv_chunk(const QkvArgs& a, int t, int64_t col) {
@@ -230,34 +131,8 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(QkvArgs a) {
   QkvChunk<KS> xc, vc;
   xc.load(a, t, static_cast<int64_t>(h) * D + c * 8);
   if (is_k) vc.load(a, t, static_cast<int64_t>(a.Hq + a.Hkv + hk) * D + c * 8);
-  p = p < 0 ? 0 : (p >= a.max_pos ? a.max_pos - 1 : p);
-  const bool first = c < G / 2;
-  const int i0 = (first ? c : c - G / 2) * 8;
-  const uint16_t* cp = a.cos + p * a.tab_stride + i0;
-  const uint16_t* sp = a.sin + p * a.tab_stride + i0;
-  const uint4 cr = *reinterpret_cast<const uint4*>(cp), sr = *reinterpret_cast<const uint4*>(sp);
-  const uint4 xr = xc.get(a);
-  // partner words (elements i +- D/2) from lane c ^ (G/2)
-  uint32_t xw[4] = {xr.x, xr.y, xr.z, xr.w}, pw[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) pw[e] = __shfl_xor(xw[e], G / 2, COOPT_WAVE);
-  const uint32_t cw[4] = {cr.x, cr.y, cr.z, cr.w}, sw[4] = {sr.x, sr.y, sr.z, sr.w};
-  uint32_t yw[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    float y[2];
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const float x = bf16_to_f32(static_cast<uint16_t>(xw[e] >> (16 * hh)));
-      const float xp = bf16_to_f32(static_cast<uint16_t>(pw[e] >> (16 * hh)));
-      const float cs = bf16_to_f32(static_cast<uint16_t>(cw[e] >> (16 * hh)));
-      const float sn = bf16_to_f32(static_cast<uint16_t>(sw[e] >> (16 * hh)));
-      // first half: x1 c - x2 s; second half: x2 c + x1 s (x = own element, xp = partner)
-      y[hh] = first ? fmaf(x, cs, -(xp * sn)) : fmaf(x, cs, xp * sn);
-    }
-    yw[e] = pack2_bf16(y[0], y[1]);
-  }
-  const uint4 yr = make_uint4(yw[0], yw[1], yw[2], yw[3]);
+  const RopeTab rt = rope_tab<G>(a.cos, a.sin, a.tab_stride, p, a.max_pos, c);
+  const uint4 yr = rope_chunk<G>(xc.get(a), rt, c);
   if (!is_k) {
     *reinterpret_cast<uint4*>(a.q_out + t * a.q_ts + h * a.q_hs + c * 8) = yr;
     return;

@@ -1,0 +1,161 @@
+// Device helpers shared by the kernels that write the paged KV cache: the symmetric absmax
+// INT8 quantiser, the per-chunk KV store, and neox RoPE on one 16-byte chunk of a head vector.
+//
+// Quantisation follows kv_tier_manager.quantize (engine/kv_tier_manager.py:21-31) as torch
+// executes it on a GPU tensor:
+//   amax  = max |x| over the last dim (exact in any format)
+//   s32   = max(amax, fp32(1e-8)) * fp32(1/qmax)   -- torch's GPU path turns "tensor / python
+//           scalar" into a multiply by the fp32 reciprocal of the scalar
+//   code  = int8(clamp(round_half_even(x / s32), -qmax, qmax))   -- IEEE fp32 division
+//   scale = fp16(s32), round to nearest even
+#pragma once
+
+#include "common.h"
+
+namespace {
+
+constexpr float kClampMin = 1e-8f;  // torch converts clamp_min(1e-8) to the tensor's fp32
+
+template <int QMAX>
+__device__ __forceinline__ float quant_scale(float amax) {
+  return fmaxf(amax, kClampMin) * (1.0f / static_cast<float>(QMAX));
+}
+
+// code = rint(fl(x / s32)) clamped to [-QMAX, QMAX], fl the IEEE fp32 quotient, computed as
+// rint(x * r32) with r32 = v_rcp_f32(s32) (1 ulp).  Because s32 >= amax / 127 up to rounding,
+// |x / s32| < 128, where an ulp is at most 2^-17: the reciprocal's relative error (2^-23)
+// and the product's rounding leave x * r32 within 2.5 ulp of x / s32, hence within 3 ulp
+// (< 2^-14) of fl(x / s32), so both round to the same integer unless x * r32 lies within
+// kNearTie of a half-integer.  There the IEEE division decides.
+// The result is the IEEE path's for every input (ties included), at a fraction of its work.
+constexpr float kNearTie = 0x1p-14f;
+
+template <int QMAX>
+__device__ __forceinline__ int quant_code(float x, float s32, float r32) {
+  const float q = x * r32;
+  float r = rintf(q);
+  if (fabsf(q - r) >= 0.5f - kNearTie) r = rintf(x / s32);
+  r = fminf(fmaxf(r, -static_cast<float>(QMAX)), static_cast<float>(QMAX));
+  return static_cast<int>(r);
+}
+
+// quant_code of the 8 bf16 elements in w[0..3] (element 2i in the low half of w[i]), with one
+// branch for the lane: if any element is near a boundary, all 8 take the IEEE division.
+template <int QMAX>
+__device__ __forceinline__ void quant_codes8(const uint32_t (&w)[4], float s32, int (&code)[8]) {
+  const float r32 = __builtin_amdgcn_rcpf(s32);
+  float x[8], r[8];
+  bool near = false;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    x[e] = bf16_to_f32(static_cast<uint16_t>(w[e / 2] >> (16 * (e & 1))));
+    const float q = x[e] * r32;
+    r[e] = rintf(q);
+    near |= fabsf(q - r[e]) >= 0.5f - kNearTie;
+  }
+  if (near) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = rintf(x[e] / s32);
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    code[e] = static_cast<int>(fminf(fmaxf(r[e], -static_cast<float>(QMAX)), static_cast<float>(QMAX)));
+}
+
+// ---------------------------------------------------------------------------------------
+// KV write.  One lane per 16-byte chunk (8 bf16) of a (token, head) vector; G = D/8 lanes
+// (an aligned power-of-two group inside the wave) cover one vector, and each lane handles
+// the same chunk of K and of V, so every load and store is a 16- or 8-byte access.
+// ---------------------------------------------------------------------------------------
+// Lane c of a G-lane group stores elements [8c, 8c + 8) of one (token, head) K and V vector
+// at cache element offset c_off: bf16 as is, or INT8 codes with the group's fp16 scale at
+// s_off (kv_tier_manager.quantize(x, 8) per vector, engine/kv_tier_manager.py:21-31).
+template <int G, bool INT8>
+__device__ __forceinline__ void store_kv_chunk(uint4 kr, uint4 vr, void* kc, void* vc,
+                                               int64_t c_off, uint16_t* ks, uint16_t* vs,
+                                               int64_t s_off, int c) {
+  if constexpr (!INT8) {
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(kc) + c_off) = kr;
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(vc) + c_off) = vr;
+  } else {
+    const uint32_t kw[4] = {kr.x, kr.y, kr.z, kr.w};
+    const uint32_t vw[4] = {vr.x, vr.y, vr.z, vr.w};
+    uint32_t kmax = 0, vmax = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // |bf16| ordering equals integer ordering of the low 15 bits for finite values.
+      const uint32_t k0 = kw[i] & 0x7fffu, k1 = (kw[i] >> 16) & 0x7fffu;
+      const uint32_t v0 = vw[i] & 0x7fffu, v1 = (vw[i] >> 16) & 0x7fffu;
+      kmax = max(kmax, max(k0, k1));
+      vmax = max(vmax, max(v0, v1));
+    }
+    kmax = group_max_u32<G>(kmax);
+    vmax = group_max_u32<G>(vmax);
+    const float ksc = quant_scale<127>(bf16_to_f32(static_cast<uint16_t>(kmax)));
+    const float vsc = quant_scale<127>(bf16_to_f32(static_cast<uint16_t>(vmax)));
+    int kcode[8], vcode[8];
+    quant_codes8<127>(kw, ksc, kcode);
+    quant_codes8<127>(vw, vsc, vcode);
+    uint32_t kq[2] = {0, 0}, vq[2] = {0, 0};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      kq[i / 4] |= (static_cast<uint32_t>(kcode[i]) & 0xffu) << (8 * (i & 3));
+      vq[i / 4] |= (static_cast<uint32_t>(vcode[i]) & 0xffu) << (8 * (i & 3));
+    }
+    *reinterpret_cast<uint2*>(static_cast<int8_t*>(kc) + c_off) = make_uint2(kq[0], kq[1]);
+    *reinterpret_cast<uint2*>(static_cast<int8_t*>(vc) + c_off) = make_uint2(vq[0], vq[1]);
+    if (c == 0) {
+      ks[s_off] = f32_to_f16(ksc);
+      vs[s_off] = f32_to_f16(vsc);
+    }
+  }
+}
+
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+  return f32_to_bf16(a) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+}
+
+// neox RoPE (engine/model.py:92-94) on lane c's chunk (elements [8c, 8c + 8)) of a G-lane
+// group holding one head vector (D = 8G): element i pairs with i + D/2, which lives in lane
+// c ^ (G/2) of the same group, so every lane of the group must run this together.  The
+// rotation is rounded to bf16 per element, as the reference's bf16 ops round it.
+struct RopeTab {
+  uint4 cos, sin;
+};
+template <int G>
+__device__ __forceinline__ RopeTab rope_tab(const uint16_t* cos, const uint16_t* sin, int64_t stride,
+                                            int64_t p, int max_pos, int c) {
+  p = p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p);
+  const int i0 = (c < G / 2 ? c : c - G / 2) * 8;
+  RopeTab t;
+  t.cos = *reinterpret_cast<const uint4*>(cos + p * stride + i0);
+  t.sin = *reinterpret_cast<const uint4*>(sin + p * stride + i0);
+  return t;
+}
+template <int G>
+__device__ __forceinline__ uint4 rope_chunk(uint4 xr, const RopeTab& t, int c) {
+  const bool first = c < G / 2;
+  // partner words (elements i +- D/2) from lane c ^ (G/2)
+  uint32_t xw[4] = {xr.x, xr.y, xr.z, xr.w}, pw[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) pw[e] = __shfl_xor(xw[e], G / 2, COOPT_WAVE);
+  const uint32_t cw[4] = {t.cos.x, t.cos.y, t.cos.z, t.cos.w}, sw[4] = {t.sin.x, t.sin.y, t.sin.z, t.sin.w};
+  uint32_t yw[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float y[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const float x = bf16_to_f32(static_cast<uint16_t>(xw[e] >> (16 * hh)));
+      const float xp = bf16_to_f32(static_cast<uint16_t>(pw[e] >> (16 * hh)));
+      const float cs = bf16_to_f32(static_cast<uint16_t>(cw[e] >> (16 * hh)));
+      const float sn = bf16_to_f32(static_cast<uint16_t>(sw[e] >> (16 * hh)));
+      // first half: x1 c - x2 s; second half: x2 c + x1 s (x = own element, xp = partner)
+      y[hh] = first ? fmaf(x, cs, -(xp * sn)) : fmaf(x, cs, xp * sn);
+    }
+    yw[e] = pack2_bf16(y[0], y[1]);
+  }
+  return make_uint4(yw[0], yw[1], yw[2], yw[3]);
+}
+
+}  // namespace

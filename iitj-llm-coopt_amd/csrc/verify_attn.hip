@@ -52,6 +52,7 @@
 #include <math.h>
 
 #include "common.h"
+#include "kv_store.h"
 
 namespace {
 
@@ -92,7 +93,25 @@ struct AttnArgs {
   float* part_o;
   int B;
   int plan;  // blocks order the items longest first (plan_item)
+  // Fused qkv epilogue (coopt_verify_attention_qkv): qkv_mode 0 = q is given; 1 = bf16 qkv
+  // projection rows; 2 = their fp32 split-K partials.  The block computes its own q rows
+  // (RoPE'd, straight into LDS) and writes its KV head's new K/V to the cache first.
+  // The cache writes go through kc / vc / ks / vs (the same caches the kernel reads).
+  int qkv_mode;
+  const void* qkv_src;  // bf16 rows (mode 1) or fp32 partials (mode 2)
+  int64_t qkv_stride;   // mode 1: row stride (elements); mode 2: slice stride (floats)
+  int qkv_ks;           // mode 2: slices
+  const int64_t* pos;
+  const uint16_t* cos;
+  const uint16_t* sin;
+  int tab_stride;
+  int max_pos;
+  const int64_t* slots;
 };
+
+// Partials of a fused epilogue are reduced with a compile-time slice bound (every load
+// unconditional, see Partials4); launches with more slices are rejected on the host.
+constexpr int kQkvMaxSlices = 4;
 
 // Batches of up to kPlanSeqs sequences can be ordered by the blocks themselves (one wave,
 // one lane per sequence); larger ones run in grid order.
@@ -212,7 +231,8 @@ __device__ void plan_item(const AttnArgs& a, int lane, int* out) {
 // stride 1), so a lane's four scales of a sub-tile are one 8-byte load; DB: double-buffer
 // the wave's tiles in registers (RT <= 2, and RT 3 with the smaller INT8 tiles; the other
 // shapes need the registers for accumulators).
-template <int D, bool INT8, int RT, bool SC>
+// FUSED: the block runs the qkv epilogue of its rows first (a.qkv_mode != 0).
+template <int D, bool INT8, int RT, bool SC, bool FUSED>
 __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(AttnArgs a) {
   using Raw = RawTile<D, INT8>;
   constexpr int kWaves = waves_for(RT);
@@ -272,23 +292,95 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
   constexpr int kQCh = D / 8;  // 16-byte chunks per row
   constexpr int kQIter = (kRows * kQCh + kBlock - 1) / kBlock;
   u32x4_t qreg[kQIter];
+  constexpr bool fused = FUSED;
 #pragma unroll
   for (int it = 0; it < kQIter; ++it) {
     const int idx = it * kBlock + tid;
     const int r = idx / kQCh, c = idx % kQCh;
     qreg[it] = u32x4_t{0, 0, 0, 0};
-    if (r < R) {
+    if (r < R && !fused) {
       const int hl = r / n, j = r - hl * n;
       qreg[it] = *reinterpret_cast<const u32x4_t*>(a.q + static_cast<int64_t>(q0 + j) * a.q_ts +
                                                    static_cast<int64_t>(hkv * a.G + hl) * a.q_hs + c * 8);
     }
   }
+  // Fused epilogue (engine/model.py:238-243 for this block's rows): every G-lane group
+  // (G = D/8) takes one vector -- a q head of a row (RoPE, into the LDS row stage_q would
+  // fill) or a row's k and v of this KV head (RoPE on k, then the cache write of
+  // reshape_and_cache_flash, INT8 quantised as coopt_kv_write does).  stage_q's barrier
+  // orders these cache writes before any of the block's loads of the new keys; a wave's first
+  // tile is loaded before that barrier only if it holds none of them.
+  auto fused_epilogue = [&]() {
+    constexpr int GL = D / 8;
+    const int nq = a.G * n, nvec = nq + n;
+    const int Hq = a.G * a.Hkv;
+    const int width = (Hq + 2 * a.Hkv) * D;
+    const int64_t num_slots = a.num_blocks << a.bs_shift;
+    for (int base = 0; base < nvec * GL; base += kBlock) {  // uniform trip count
+      const int lid = base + tid;
+      const int vi = lid / GL, c = lid % GL;
+      if (vi >= nvec) continue;  // whole groups: nvec * GL is a multiple of GL
+      const bool is_kv = vi >= nq;
+      const int j = is_kv ? vi - nq : vi % n;
+      const int hl = is_kv ? 0 : vi / n;
+      const int t = q0 + j;
+      const int head = is_kv ? Hq + hkv : hkv * a.G + hl;
+      const int64_t p = a.pos[t];
+      const int64_t slot = is_kv ? a.slots[t] : -1;
+      const int64_t col = static_cast<int64_t>(head) * D + c * 8;
+      const int64_t vcol = static_cast<int64_t>(Hq + a.Hkv + hkv) * D + c * 8;
+      uint4 xr, vr = make_uint4(0, 0, 0, 0);
+      if (a.qkv_mode == 2) {
+        // x, then v: one chunk's partials in registers at a time (the first tile's buffer is
+        // live here), the same order of adds as the reduction of coopt_linear's partials
+        const float* pr = static_cast<const float*>(a.qkv_src) + static_cast<int64_t>(t) * width;
+        auto reduce8 = [&](int64_t cc) {
+          Partials4<kQkvMaxSlices> lo, hi;
+          lo.load(pr + cc, a.qkv_ks, a.qkv_stride);
+          hi.load(pr + cc + 4, a.qkv_ks, a.qkv_stride);
+          const float4 l = lo.sum(a.qkv_ks), h = hi.sum(a.qkv_ks);
+          return make_uint4(pack2_bf16(l.x, l.y), pack2_bf16(l.z, l.w), pack2_bf16(h.x, h.y),
+                            pack2_bf16(h.z, h.w));
+        };
+        xr = reduce8(col);
+        asm volatile("" ::: "memory");  // keep v's loads after x's sum
+        if (is_kv) vr = reduce8(vcol);
+      } else {
+        const uint16_t* rr = static_cast<const uint16_t*>(a.qkv_src) + static_cast<int64_t>(t) * a.qkv_stride;
+        xr = *reinterpret_cast<const uint4*>(rr + col);
+        if (is_kv) vr = *reinterpret_cast<const uint4*>(rr + vcol);
+      }
+      const RopeTab tab = rope_tab<GL>(a.cos, a.sin, a.tab_stride, p, a.max_pos, c);
+      const uint4 yr = rope_chunk<GL>(xr, tab, c);
+      if (!is_kv) {
+        const int r = hl * n + j;  // < R <= kRows
+        *reinterpret_cast<uint4*>(lds + r * kQPitch + c * 16) = yr;
+      } else if (slot >= 0 && slot < num_slots) {  // padding rows write nothing
+        const int64_t blk = slot >> a.bs_shift;
+        const int64_t off = slot & bs_mask;
+        store_kv_chunk<GL, INT8>(yr, vr, const_cast<void*>(a.kc), const_cast<void*>(a.vc),
+                                 blk * a.c_bs + off * a.c_ts + hkv * a.c_hs + c * 8,
+                                 const_cast<uint16_t*>(a.ks), const_cast<uint16_t*>(a.vs),
+                                 blk * a.s_bs + off * a.s_ts + hkv * a.s_hs, c);
+      }
+    }
+    // Q rows past R are zero, as stage_q leaves them
+    for (int idx = tid; idx < (kRows - R) * kQCh; idx += kBlock) {
+      const int r = R + idx / kQCh, c = idx % kQCh;
+      *reinterpret_cast<u32x4_t*>(lds + r * kQPitch + c * 16) = u32x4_t{0, 0, 0, 0};
+    }
+  };
+  // Run here, before the attention's own state is set up: its scalars (kernel-argument
+  // fields) are dead again by the time the loop's page bases and offsets are live.
+  if constexpr (FUSED) fused_epilogue();
   auto stage_q = [&]() {
+    if (!fused) {
 #pragma unroll
-    for (int it = 0; it < kQIter; ++it) {
-      const int idx = it * kBlock + tid;
-      const int r = idx / kQCh, c = idx % kQCh;
-      if (r < kRows) *reinterpret_cast<u32x4_t*>(lds + r * kQPitch + c * 16) = qreg[it];
+      for (int it = 0; it < kQIter; ++it) {
+        const int idx = it * kBlock + tid;
+        const int r = idx / kQCh, c = idx % kQCh;
+        if (r < kRows) *reinterpret_cast<u32x4_t*>(lds + r * kQPitch + c * 16) = qreg[it];
+      }
     }
     __syncthreads();
   };
@@ -658,8 +750,11 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
     const int tlast = nfull - 1;
     int tA = wave;
     int64_t nx0 = 0, nx1 = 0;  // pages of the wave's next tile to load
-    if (tA < nfull) load_full(bufA, tA, first_pg0, first_pg1);
+    // fused: a first tile holding keys this launch writes ([L - n, L)) loads after the barrier
+    const bool defer = fused && k_begin + (tA + 1) * kTileKeys > L - n;
+    if (tA < nfull && !defer) load_full(bufA, tA, first_pg0, first_pg1);
     stage_q();  // the Q loads complete while the first tile's are in flight
+    if (tA < nfull && defer) load_full(bufA, tA, first_pg0, first_pg1);
     if (tA < nfull) {
       vcheck(bufA);
       int tB = grab();
@@ -928,13 +1023,28 @@ AttnWs attn_ws_layout(int B, int Hkv, int D, int rmax, int max_splits) {
   return w;
 }
 
+// Shapes the fused epilogue is instantiated for: up to 32 rows (a speculative step's verify
+// and draft shapes), except bf16 at head dim 128 with 32 rows, which would spill registers.
+constexpr int kFusedMaxRT = 2;
+constexpr bool fused_ok(int D, bool int8, int RT) {
+  return RT >= 1 && RT <= kFusedMaxRT && (int8 || D != 128 || RT == 1);
+}
+
 template <int D, bool INT8, bool SC>
 int launch_rt(int RT, const AttnArgs& a, dim3 grid, hipStream_t s) {
+  if (a.qkv_mode) {
+    if (!fused_ok(D, INT8, RT)) return COOPT_EINVAL;  // the caller checked; not reached
+    if constexpr (fused_ok(D, INT8, 2)) {
+      if (RT == 2) hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 2, SC, true>), grid, dim3(64 * waves_for(2)), 0, s, a);
+    }
+    if (RT == 1) hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 1, SC, true>), grid, dim3(64 * waves_for(1)), 0, s, a);
+    return coopt::check_launch("coopt_verify_attention_qkv");  // one split: no merge launch
+  }
   switch (RT) {
-    case 1: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 1, SC>), grid, dim3(64 * waves_for(1)), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 2, SC>), grid, dim3(64 * waves_for(2)), 0, s, a); break;
-    case 3: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 3, SC>), grid, dim3(64 * waves_for(3)), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 4, SC>), grid, dim3(64 * waves_for(4)), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 1, SC, false>), grid, dim3(64 * waves_for(1)), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 2, SC, false>), grid, dim3(64 * waves_for(2)), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 3, SC, false>), grid, dim3(64 * waves_for(3)), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 4, SC, false>), grid, dim3(64 * waves_for(4)), 0, s, a); break;
     default: return COOPT_EINVAL;
   }
   int rc = coopt::check_launch("coopt_verify_attention");
@@ -959,59 +1069,80 @@ extern "C" size_t coopt_verify_attention_workspace(int B, int Hq, int Hkv, int D
   return attn_ws_layout(B, Hkv, D, rmax, sh.max_splits).total;
 }
 
-extern "C" int coopt_verify_attention(int kv_dtype, const void* q, int64_t q_tok_stride,
-                                      int64_t q_head_stride, const void* k_cache,
-                                      const void* v_cache, int64_t c_blk_stride,
-                                      int64_t c_tok_stride, int64_t c_head_stride,
-                                      const void* k_scale, const void* v_scale,
-                                      int64_t s_blk_stride, int64_t s_tok_stride,
-                                      int64_t s_head_stride, const int32_t* block_table,
-                                      int64_t bt_stride, const int32_t* cu_seqlens_q,
-                                      const int32_t* seq_lens, int B, int Hq, int Hkv, int D,
-                                      int block_size, int64_t num_blocks, int max_seqlen_q,
-                                      int max_seqlen_k, float softmax_scale, void* out,
-                                      int64_t o_tok_stride, int64_t o_head_stride,
-                                      void* workspace, size_t workspace_bytes,
-                                      coopt_stream_t stream) {
-  COOPT_REQUIRE(kv_dtype == COOPT_DT_BF16 || kv_dtype == COOPT_DT_I8,
-                "kv_dtype must be COOPT_DT_BF16 or COOPT_DT_I8");
-  COOPT_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0, "Hq must be a multiple of Hkv");
-  COOPT_REQUIRE(D == 64 || D == 128, "head_dim must be 64 or 128");
-  COOPT_REQUIRE(block_size >= 16 && (block_size & (block_size - 1)) == 0,
-                "block_size must be a power of two >= 16");
-  COOPT_REQUIRE(max_seqlen_q > 0 && max_seqlen_k > 0, "max_seqlen_q/k must be positive");
+namespace {
+
+// The fused epilogue's inputs (coopt_verify_attention_qkv); null for coopt_verify_attention.
+struct FusedQkv {
+  const void* qkv;
+  int64_t qkv_tok_stride;
+  const float* part;
+  int ks;
+  int64_t slice_stride;
+  const int64_t* positions;
+  const void* cos;
+  const void* sin;
+  int64_t table_stride;
+  int max_pos;
+  const int64_t* slot_mapping;
+};
+
+#define ATTN_REQUIRE(cond, msg)                              \
+  do {                                                       \
+    if (!(cond)) {                                           \
+      coopt::set_error(std::string(who) + ": " + (msg));     \
+      return COOPT_EINVAL;                                   \
+    }                                                        \
+  } while (0)
+
+int verify_attention_impl(const char* who, const FusedQkv* fz, int kv_dtype, const void* q,
+                          int64_t q_tok_stride, int64_t q_head_stride, const void* k_cache,
+                          const void* v_cache, int64_t c_blk_stride, int64_t c_tok_stride,
+                          int64_t c_head_stride, const void* k_scale, const void* v_scale,
+                          int64_t s_blk_stride, int64_t s_tok_stride, int64_t s_head_stride,
+                          const int32_t* block_table, int64_t bt_stride,
+                          const int32_t* cu_seqlens_q, const int32_t* seq_lens, int B, int Hq,
+                          int Hkv, int D, int block_size, int64_t num_blocks, int max_seqlen_q,
+                          int max_seqlen_k, float softmax_scale, void* out, int64_t o_tok_stride,
+                          int64_t o_head_stride, void* workspace, size_t workspace_bytes,
+                          coopt_stream_t stream) {
+  ATTN_REQUIRE(kv_dtype == COOPT_DT_BF16 || kv_dtype == COOPT_DT_I8,
+               "kv_dtype must be COOPT_DT_BF16 or COOPT_DT_I8");
+  ATTN_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0, "Hq must be a multiple of Hkv");
+  ATTN_REQUIRE(D == 64 || D == 128, "head_dim must be 64 or 128");
+  ATTN_REQUIRE(block_size >= 16 && (block_size & (block_size - 1)) == 0,
+               "block_size must be a power of two >= 16");
+  ATTN_REQUIRE(max_seqlen_q > 0 && max_seqlen_k > 0, "max_seqlen_q/k must be positive");
   const int G = Hq / Hkv;
-  COOPT_REQUIRE(G * max_seqlen_q <= 64, "(Hq/Hkv) * max_seqlen_q must be <= 64");
-  COOPT_REQUIRE(bt_stride >= (max_seqlen_k + block_size - 1) / block_size,
-                "block_table narrower than ceil(max_seqlen_k / block_size)");
+  ATTN_REQUIRE(G * max_seqlen_q <= 64, "(Hq/Hkv) * max_seqlen_q must be <= 64");
+  ATTN_REQUIRE(bt_stride >= (max_seqlen_k + block_size - 1) / block_size,
+               "block_table narrower than ceil(max_seqlen_k / block_size)");
   if (B == 0) return COOPT_OK;
-  COOPT_REQUIRE(q && k_cache && v_cache && block_table && cu_seqlens_q && seq_lens && out,
-                "null pointer");
-  COOPT_REQUIRE(coopt::aligned16(q) && coopt::aligned16(out) && q_tok_stride % 8 == 0 &&
-                    q_head_stride % 8 == 0 && o_tok_stride % 8 == 0 && o_head_stride % 8 == 0,
-                "q/out rows must be 16-byte aligned");
+  ATTN_REQUIRE((q || fz) && k_cache && v_cache && block_table && cu_seqlens_q && seq_lens && out,
+               "null pointer");
+  ATTN_REQUIRE((fz || (coopt::aligned16(q) && q_tok_stride % 8 == 0 && q_head_stride % 8 == 0)) &&
+                   coopt::aligned16(out) && o_tok_stride % 8 == 0 && o_head_stride % 8 == 0,
+               "q/out rows must be 16-byte aligned");
   const bool int8 = kv_dtype == COOPT_DT_I8;
   if (int8) {
-    COOPT_REQUIRE(k_scale && v_scale, "INT8 KV needs k_scale and v_scale");
-    COOPT_REQUIRE(coopt::aligned16(k_cache) && coopt::aligned16(v_cache) && c_blk_stride % 16 == 0 &&
-                      c_tok_stride % 16 == 0 && c_head_stride % 16 == 0,
-                  "INT8 cache rows must be 16-byte aligned");
+    ATTN_REQUIRE(k_scale && v_scale, "INT8 KV needs k_scale and v_scale");
+    ATTN_REQUIRE(coopt::aligned16(k_cache) && coopt::aligned16(v_cache) && c_blk_stride % 16 == 0 &&
+                     c_tok_stride % 16 == 0 && c_head_stride % 16 == 0,
+                 "INT8 cache rows must be 16-byte aligned");
   } else {
-    COOPT_REQUIRE(coopt::aligned16(k_cache) && coopt::aligned16(v_cache) && c_blk_stride % 8 == 0 &&
-                      c_tok_stride % 8 == 0 && c_head_stride % 8 == 0,
-                  "bf16 cache rows must be 16-byte aligned");
+    ATTN_REQUIRE(coopt::aligned16(k_cache) && coopt::aligned16(v_cache) && c_blk_stride % 8 == 0 &&
+                     c_tok_stride % 8 == 0 && c_head_stride % 8 == 0,
+                 "bf16 cache rows must be 16-byte aligned");
   }
   const size_t need = coopt_verify_attention_workspace(B, Hq, Hkv, D, max_seqlen_q, max_seqlen_k);
   if (workspace_bytes < need || workspace == nullptr) {
-    coopt::set_error("coopt_verify_attention: workspace too small");
+    coopt::set_error(std::string(who) + ": workspace too small");
     return COOPT_EWORKSPACE;
   }
-  COOPT_REQUIRE(num_blocks > 0, "num_blocks must be positive");
+  ATTN_REQUIRE(num_blocks > 0, "num_blocks must be positive");
   // lanes address a page's rows with 32-bit byte offsets
-  COOPT_REQUIRE(c_tok_stride > 0 && (block_size * c_tok_stride + D) * (int8 ? 1 : 2) < (int64_t{1} << 31) &&
-                    (!int8 || (s_tok_stride >= 0 && block_size * s_tok_stride * 2 < (int64_t{1} << 31))),
-                "cache token stride too large for one page");
-  coopt::clear_error();
+  ATTN_REQUIRE(c_tok_stride > 0 && (block_size * c_tok_stride + D) * (int8 ? 1 : 2) < (int64_t{1} << 31) &&
+                   (!int8 || (s_tok_stride >= 0 && block_size * s_tok_stride * 2 < (int64_t{1} << 31))),
+               "cache token stride too large for one page");
 
   AttnArgs a{};
   a.q = static_cast<const uint16_t*>(q);
@@ -1052,6 +1183,39 @@ extern "C" int coopt_verify_attention(int kv_dtype, const void* q, int64_t q_tok
   char* base = static_cast<char*>(workspace);
   a.part_ml = reinterpret_cast<float2*>(base + w.ml_off);
   a.part_o = reinterpret_cast<float*>(base + w.o_off);
+  if (fz) {
+    // one block per (sequence, KV head) owns that pair's rows: the epilogue cannot be shared
+    // between the blocks of a split context
+    ATTN_REQUIRE(fused_ok(D, int8, (a.rmax + 15) / 16),
+                 "(Hq/Hkv) * max_seqlen_q must be <= 32 (<= 16 with bf16 KV at head_dim 128)");
+    ATTN_REQUIRE(shape.max_splits == 1,
+                 "this launch splits contexts (B * Hkv too small for max_seqlen_k); call "
+                 "coopt_qkv_epilogue and coopt_verify_attention instead");
+    ATTN_REQUIRE((fz->qkv != nullptr) != (fz->part != nullptr), "exactly one of qkv / part");
+    ATTN_REQUIRE(!fz->part || (fz->ks >= 1 && fz->ks <= kQkvMaxSlices && coopt::aligned16(fz->part) &&
+                               fz->slice_stride % 4 == 0),
+                 "part needs 1 <= ks <= 4 slices, 16-byte aligned");
+    ATTN_REQUIRE(!fz->qkv || (coopt::aligned16(fz->qkv) && fz->qkv_tok_stride % 8 == 0 &&
+                              fz->qkv_tok_stride >= static_cast<int64_t>(Hq + 2 * Hkv) * D),
+                 "qkv rows must be 16-byte aligned and hold (Hq + 2 Hkv) * D elements");
+    ATTN_REQUIRE(fz->positions && fz->cos && fz->sin && fz->slot_mapping, "null pointer");
+    ATTN_REQUIRE(coopt::aligned16(fz->cos) && coopt::aligned16(fz->sin) && fz->table_stride % 8 == 0 &&
+                     fz->table_stride >= D / 2 && fz->max_pos > 0,
+                 "cos/sin tables must be 16-byte aligned rows of >= D/2 bf16");
+    ATTN_REQUIRE(fz->table_stride < (int64_t{1} << 31) && (num_blocks << shift) / block_size == num_blocks,
+                 "table stride or pool size out of range");
+    a.qkv_mode = fz->part ? 2 : 1;
+    a.qkv_src = fz->part ? static_cast<const void*>(fz->part) : fz->qkv;
+    a.qkv_stride = fz->part ? fz->slice_stride : fz->qkv_tok_stride;
+    a.qkv_ks = fz->ks;
+    a.pos = fz->positions;
+    a.cos = static_cast<const uint16_t*>(fz->cos);
+    a.sin = static_cast<const uint16_t*>(fz->sin);
+    a.tab_stride = static_cast<int>(fz->table_stride);
+    a.max_pos = fz->max_pos;
+    a.slots = fz->slot_mapping;
+  }
+  coopt::clear_error();
 
   const int RT = (a.rmax + 15) / 16;
   const dim3 grid = shape.plan ? dim3(B * Hkv) : dim3(a.max_splits, Hkv, B);
@@ -1061,4 +1225,62 @@ extern "C" int coopt_verify_attention(int kv_dtype, const void* q, int64_t q_tok
                   (reinterpret_cast<uintptr_t>(k_scale) & 7u) == 0 &&
                   (reinterpret_cast<uintptr_t>(v_scale) & 7u) == 0;
   return D == 128 ? launch_d<128>(int8, sc, RT, a, grid, s) : launch_d<64>(int8, sc, RT, a, grid, s);
+}
+
+#undef ATTN_REQUIRE
+
+}  // namespace
+
+extern "C" int coopt_verify_attention(int kv_dtype, const void* q, int64_t q_tok_stride,
+                                      int64_t q_head_stride, const void* k_cache,
+                                      const void* v_cache, int64_t c_blk_stride,
+                                      int64_t c_tok_stride, int64_t c_head_stride,
+                                      const void* k_scale, const void* v_scale,
+                                      int64_t s_blk_stride, int64_t s_tok_stride,
+                                      int64_t s_head_stride, const int32_t* block_table,
+                                      int64_t bt_stride, const int32_t* cu_seqlens_q,
+                                      const int32_t* seq_lens, int B, int Hq, int Hkv, int D,
+                                      int block_size, int64_t num_blocks, int max_seqlen_q,
+                                      int max_seqlen_k, float softmax_scale, void* out,
+                                      int64_t o_tok_stride, int64_t o_head_stride,
+                                      void* workspace, size_t workspace_bytes,
+                                      coopt_stream_t stream) {
+  return verify_attention_impl("coopt_verify_attention", nullptr, kv_dtype, q, q_tok_stride,
+                               q_head_stride, k_cache, v_cache, c_blk_stride, c_tok_stride,
+                               c_head_stride, k_scale, v_scale, s_blk_stride, s_tok_stride,
+                               s_head_stride, block_table, bt_stride, cu_seqlens_q, seq_lens, B,
+                               Hq, Hkv, D, block_size, num_blocks, max_seqlen_q, max_seqlen_k,
+                               softmax_scale, out, o_tok_stride, o_head_stride, workspace,
+                               workspace_bytes, stream);
+}
+
+extern "C" int coopt_verify_attention_qkv_supported(int kv_dtype, int B, int Hq, int Hkv, int D,
+                                                    int max_seqlen_q, int max_seqlen_k) {
+  if (kv_dtype != COOPT_DT_BF16 && kv_dtype != COOPT_DT_I8) return 0;
+  if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv || max_seqlen_q <= 0 || max_seqlen_k <= 0) return 0;
+  if (D != 64 && D != 128) return 0;
+  const int rmax = (Hq / Hkv) * max_seqlen_q;
+  if (!fused_ok(D, kv_dtype == COOPT_DT_I8, (rmax + 15) / 16)) return 0;
+  return attn_shape(B, Hkv, rmax, max_seqlen_k).max_splits == 1 ? 1 : 0;
+}
+
+extern "C" int coopt_verify_attention_qkv(
+    int kv_dtype, const void* qkv, int64_t qkv_tok_stride, const float* part, int ks,
+    int64_t slice_stride, const int64_t* positions, const void* cos, const void* sin,
+    int64_t table_stride, int max_pos, const int64_t* slot_mapping, void* k_cache, void* v_cache,
+    int64_t c_blk_stride, int64_t c_tok_stride, int64_t c_head_stride, void* k_scale,
+    void* v_scale, int64_t s_blk_stride, int64_t s_tok_stride, int64_t s_head_stride,
+    const int32_t* block_table, int64_t bt_stride, const int32_t* cu_seqlens_q,
+    const int32_t* seq_lens, int B, int Hq, int Hkv, int D, int block_size, int64_t num_blocks,
+    int max_seqlen_q, int max_seqlen_k, float softmax_scale, void* out, int64_t o_tok_stride,
+    int64_t o_head_stride, void* workspace, size_t workspace_bytes, coopt_stream_t stream) {
+  const FusedQkv fz{qkv, qkv_tok_stride, part, ks, slice_stride, positions, cos, sin,
+                    table_stride, max_pos, slot_mapping};
+  return verify_attention_impl("coopt_verify_attention_qkv", &fz, kv_dtype, nullptr, 0, 0,
+                               k_cache, v_cache, c_blk_stride, c_tok_stride, c_head_stride,
+                               k_scale, v_scale, s_blk_stride, s_tok_stride, s_head_stride,
+                               block_table, bt_stride, cu_seqlens_q, seq_lens, B, Hq, Hkv, D,
+                               block_size, num_blocks, max_seqlen_q, max_seqlen_k, softmax_scale,
+                               out, o_tok_stride, o_head_stride, workspace, workspace_bytes,
+                               stream);
 }

@@ -26,9 +26,11 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from .attention import paged_attention, workspace_bytes
+from .attention import (paged_attention, paged_attention_qkv, qkv_attention_supported,
+                        workspace_bytes)
 from .batch import row_slots
-from .fused import (linear, linear_silu, pack_gate_up_weight, pack_linear_weight, rms_norm, rope_,
+from .fused import (LinearPartials, linear, linear_silu, pack_gate_up_weight, pack_linear_weight,
+                    rms_norm, rope_,
                     row_major, silu_and_mul)
 from .kv_cache import allocate_kv_cache, qkv_rope_and_cache, reshape_and_cache_flash
 from .spec_decode import AcceptResult, accept
@@ -145,11 +147,17 @@ class RandomLlama:
         d = None
         for li, L in enumerate(self.layers):
             h = ops.rms_norm(x if d is None else d, None if d is None else x, L["ln1"], s.eps)
-            # qkv projection, RoPE and the KV write: split-K partials straight into one
-            # epilogue launch that writes q and the paged cache (engine/model.py:238-243)
+            # qkv projection, RoPE, the KV write and attention (engine/model.py:238-247):
+            # split-K partials straight into one launch that reduces them, writes the paged
+            # cache and attends (ops.attend_qkv), or into the epilogue launch that writes q
+            # and the cache, then attention
             qkv = ops.linear(h, L["qkv"], defer_reduce=True)
-            q = ops.qkv_epilogue(kv, li, qkv, pos, self.cos, self.sin, slots, H, Hkv, D)
-            attn = ops.attend(kv, li, q, meta, self.scale)
+            attend_qkv = getattr(ops, "attend_qkv", None)
+            attn = None if attend_qkv is None else attend_qkv(
+                kv, li, qkv, pos, self.cos, self.sin, slots, meta, self.scale, H, Hkv, D)
+            if attn is None:
+                q = ops.qkv_epilogue(kv, li, qkv, pos, self.cos, self.sin, slots, H, Hkv, D)
+                attn = ops.attend(kv, li, q, meta, self.scale)
             # gate_up + SiLU·mul is one launch at draft row counts (linear_silu); o, down and
             # otherwise gate_up feed only the fused add + norm or SiLU, which reduce their
             # split-K partials as they read them
@@ -198,10 +206,13 @@ class PagedKV:
 
 
 class HipOps:
-    """The gfx950 kernels behind the step, with preallocated workspaces (capture-safe)."""
+    """The gfx950 kernels behind the step, with preallocated workspaces (capture-safe).
+    fuse_qkv: run each layer's qkv epilogue inside its attention launch where the shape
+    allows (attend_qkv); the results are the same bit for bit."""
 
-    def __init__(self, device):
+    def __init__(self, device, fuse_qkv=True):
         self.device = torch.device(device)
+        self.fuse_qkv = fuse_qkv
         self._ws = {}
 
     def workspace(self, key, nbytes):
@@ -246,6 +257,21 @@ class HipOps:
         ws = self.workspace(("attn", q.shape[2]), nb)
         return paged_attention(q, kc, vc, cu, seq_lens, kv.block_table[:B], S, max_k, scale, ks,
                                vs, workspace=ws)
+
+    def attend_qkv(self, kv: PagedKV, layer, qkv, pos, cos, sin, slots, meta, scale, H, Hkv, D):
+        """qkv_epilogue + attend as one launch, or None where that launch does not take the
+        shape (the caller then makes the two calls)."""
+        if not self.fuse_qkv or (isinstance(qkv, LinearPartials) and qkv.ks > 4):
+            return None
+        kc, vc, ks, vs = kv.layers[layer]
+        cu, seq_lens, S, max_k = meta
+        B = seq_lens.numel()
+        if not qkv_attention_supported(kv.kv_dtype, B, H, Hkv, D, S, max_k):
+            return None
+        ws = self.workspace(("attn", D), workspace_bytes(B, H, Hkv, D, S, max_k))
+        return paged_attention_qkv(qkv, pos, cos, sin, slots, kc, vc, cu, seq_lens,
+                                   kv.block_table[:B], S, max_k, H, scale, kv.kv_dtype, ks, vs,
+                                   workspace=ws)
 
     def sample(self, logits, u, temperature, out=None):
         """One token per row: inverse-CDF draw from softmax(logits / T) (argmax if T <= 0)."""

@@ -256,6 +256,44 @@ int coopt_verify_attention(int kv_dtype,
                            void* workspace, size_t workspace_bytes, coopt_stream_t stream);
 
 /*
+ * The qkv epilogue and the verification attention of one layer in one launch: replaces
+ * F.linear(h, qkv).split -> rotary_embedding(q, k) -> reshape_and_cache_flash(k, v) ->
+ * flash_attn_varlen_func(q, ...) at engine/model.py:238-247 (what coopt_qkv_epilogue followed
+ * by coopt_verify_attention do), bit for bit the same outputs and cache contents.  The block
+ * of (sequence b, KV head h) reduces and rotates its rows' q heads straight into on-chip
+ * memory, writes its rows' K and V of head h to the cache (INT8 quantised with cache_dtype
+ * COOPT_DT_I8), then attends.
+ *   qkv / part, ks, slice_stride, positions, cos, sin, table_stride, max_pos, slot_mapping:
+ *       as coopt_qkv_epilogue (exactly one of qkv / part; part with 1 <= ks <= 4 slices);
+ *       rows are the T = cu_seqlens_q[B] query rows.
+ *   caches, scales, block_table, cu_seqlens_q, seq_lens, sizes, out, workspace: as
+ *       coopt_verify_attention (kv_dtype the cache type); the caches are written here.
+ * Contract: row j of sequence b writes key position seq_lens[b] - n_b + j of b's pages (its
+ * slot_mapping entry points there, or is -1 for a padding row), as the reference writes a
+ * step's tokens before attending over them; blocks read their new keys back only after
+ * writing them.
+ * Supported where coopt_verify_attention_qkv_supported() returns 1: one context split per
+ * (sequence, KV head) at this B and max_seqlen_k, and (Hq/Hkv) * max_seqlen_q <= 32 (<= 16
+ * with bf16 KV at head_dim 128).  Elsewhere the call returns COOPT_EINVAL; use the two calls.
+ */
+int coopt_verify_attention_qkv_supported(int kv_dtype, int B, int Hq, int Hkv, int D,
+                                         int max_seqlen_q, int max_seqlen_k);
+int coopt_verify_attention_qkv(int kv_dtype, const void* qkv, int64_t qkv_tok_stride,
+                               const float* part, int ks, int64_t slice_stride,
+                               const int64_t* positions, const void* cos, const void* sin,
+                               int64_t table_stride, int max_pos, const int64_t* slot_mapping,
+                               void* k_cache, void* v_cache,
+                               int64_t c_blk_stride, int64_t c_tok_stride, int64_t c_head_stride,
+                               void* k_scale, void* v_scale,
+                               int64_t s_blk_stride, int64_t s_tok_stride, int64_t s_head_stride,
+                               const int32_t* block_table, int64_t bt_stride,
+                               const int32_t* cu_seqlens_q, const int32_t* seq_lens,
+                               int B, int Hq, int Hkv, int D, int block_size, int64_t num_blocks,
+                               int max_seqlen_q, int max_seqlen_k, float softmax_scale,
+                               void* out, int64_t o_tok_stride, int64_t o_head_stride,
+                               void* workspace, size_t workspace_bytes, coopt_stream_t stream);
+
+/*
  * Fused speculative acceptance for a batch (engine/spec_decode.py:20-49, looped over the
  * batch at engine/engine.py:437-446), with the random draws made explicit:
  *   temperature > 0:  p_i = softmax(target_i * (1/T)), q_i = softmax(draft_i * (1/T))
