@@ -252,13 +252,22 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
   constexpr int kRegions = kWaves * kRegionFloats * 4 <= kLdsBudget ? kWaves
                            : ((kWaves / 2) * kRegionFloats * 4 <= kLdsBudget ? kWaves / 2 : 1);
   constexpr int kOBytes = kRegions * kRegionFloats * 4;
-  __shared__ __attribute__((aligned(16))) unsigned char lds[kQBytes > kOBytes ? kQBytes : kOBytes];
+  // kOwn: every wave has a region of its own and Q sits beside the regions (within the 160 KB
+  // of a CU), so a wave stores its accumulators the moment its last tile is done and one
+  // barrier precedes the output pass, which weights each region by 2^(m_w - M) as it sums.
+  // Otherwise Q shares the space with the regions and the merge rescales before it stores.
+  constexpr bool kOwn = kRegions == kWaves && kOBytes + kQBytes <= 150 * 1024;
+  // Q stays at offset 0: the loop's Q reads then fit the LDS instructions' immediate offsets.
+  constexpr int kOOff = kOwn ? (kQBytes + 15) / 16 * 16 : 0;
+  constexpr int kLdsBytes = kOwn ? kOOff + kOBytes : (kQBytes > kOBytes ? kQBytes : kOBytes);
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
+  unsigned char* const qsh = lds;
   __shared__ float sm_m[kWaves][kRows];
   __shared__ float sm_l[kWaves][kRows];
   __shared__ float sm_M[kRows];
   __shared__ float sm_L[kRows];
   __shared__ int sm_plan[4];
-  float* osh = reinterpret_cast<float*>(lds);
+  float* osh = reinterpret_cast<float*>(lds + kOOff);
   const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, l16 = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
@@ -354,7 +363,7 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
       const uint4 yr = rope_chunk<GL>(xr, tab, c);
       if (!is_kv) {
         const int r = hl * n + j;  // < R <= kRows
-        *reinterpret_cast<uint4*>(lds + r * kQPitch + c * 16) = yr;
+        *reinterpret_cast<uint4*>(qsh + r * kQPitch + c * 16) = yr;
       } else if (slot >= 0 && slot < num_slots) {  // padding rows write nothing
         const int64_t blk = slot >> a.bs_shift;
         const int64_t off = slot & bs_mask;
@@ -367,7 +376,7 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
     // Q rows past R are zero, as stage_q leaves them
     for (int idx = tid; idx < (kRows - R) * kQCh; idx += kBlock) {
       const int r = R + idx / kQCh, c = idx % kQCh;
-      *reinterpret_cast<u32x4_t*>(lds + r * kQPitch + c * 16) = u32x4_t{0, 0, 0, 0};
+      *reinterpret_cast<u32x4_t*>(qsh + r * kQPitch + c * 16) = u32x4_t{0, 0, 0, 0};
     }
   };
   // Run here, before the attention's own state is set up: its scalars (kernel-argument
@@ -379,7 +388,7 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
       for (int it = 0; it < kQIter; ++it) {
         const int idx = it * kBlock + tid;
         const int r = idx / kQCh, c = idx % kQCh;
-        if (r < kRows) *reinterpret_cast<u32x4_t*>(lds + r * kQPitch + c * 16) = qreg[it];
+        if (r < kRows) *reinterpret_cast<u32x4_t*>(qsh + r * kQPitch + c * 16) = qreg[it];
       }
     }
     __syncthreads();
@@ -393,7 +402,7 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
   }
   // the lane's Q operand of (rt, ks): row rt*16 + l16, the 8 elements from d_of(ks) (the
   // contraction map of the K loads)
-  const unsigned char* qlds = lds + l16 * kQPitch;
+  const unsigned char* qlds = qsh + l16 * kQPitch;
   auto q_byte = [&](int ks) {
     return INT8 ? 2 * (64 * (ks >> 1) + 16 * grp + 8 * (ks & 1)) : 2 * (32 * ks + 8 * grp);
   };
@@ -802,8 +811,6 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
     vcheck(buf);
     compute_tile(buf, nfull);
   }
-  __syncthreads();  // Q in LDS is dead; the merge below reuses the space
-
   // ---- merge the waves ----
   // the wave's o and l are relative to 2^(m_run + e_v) (e_v = 0 for bf16 KV)
   const float ev_f = INT8 ? static_cast<float>(e_v) : 0.0f;
@@ -811,66 +818,104 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
   for (int rt = 0; rt < RT; ++rt) {
     m_run[rt] += ev_f;
     l_run[rt] = add_xor32(add_xor16(l_run[rt]));
-    if (grp == 0) {
-      sm_m[wave][rt * 16 + l16] = m_run[rt];
-      sm_l[wave][rt * 16 + l16] = l_run[rt];
-    }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const int r = rt * 16 + l16;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][r]);
-    float Lsum = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w)
-      if (sm_m[w][r] > -INFINITY) Lsum += sm_l[w][r] * exp2_fast(sm_m[w][r] - M);
-    const float f = m_run[rt] > -INFINITY ? exp2_fast(m_run[rt] - M) : 0.0f;
-#pragma unroll
-    for (int dt = 0; dt < kDt; ++dt) o[rt][dt] *= f;
-    if (wave == 0 && grp == 0) {
-      sm_M[r] = M;
-      sm_L[r] = Lsum;
-    }
   }
   // lane's accumulators: row rt*16 + l16, d = (4g + i) * kDt + dt -- kDt contiguous floats
-  // for each (rt, i).  Wave w stores them into region w % kRegions in round w / kRegions
-  // (later rounds add); the output pass below sums the regions in order.
+  // for each (rt, i); stored into `region` (add: onto what an earlier wave stored there)
+  auto store_acc = [&](float* region, bool add) {
 #pragma unroll
-  for (int round = 0; round < kWaves / kRegions; ++round) {
-    if (wave / kRegions == round) {
-      float* region = osh + (wave % kRegions) * kRegionFloats;
+    for (int rt = 0; rt < RT; ++rt) {
+      const int r = rt * 16 + l16;
+      if (rt * 16 >= R) break;  // row tiles of padding only (uniform)
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        const int r = rt * 16 + l16;
-        if (rt * 16 >= R) break;  // row tiles of padding only (uniform)
+      for (int i = 0; i < 4; ++i) {
+        float* dst = region + r * kOPitch + (grp * 4 + i) * kDt;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float* dst = region + r * kOPitch + (grp * 4 + i) * kDt;
-#pragma unroll
-          for (int d4 = 0; d4 < kDt / 4; ++d4) {
-            const f32x4_t x = {o[rt][d4 * 4 + 0][i], o[rt][d4 * 4 + 1][i], o[rt][d4 * 4 + 2][i],
-                               o[rt][d4 * 4 + 3][i]};
-            f32x4_t* dp = reinterpret_cast<f32x4_t*>(dst + 4 * d4);
-            if (round == 0) *dp = x;
-            else *dp = *dp + x;
-          }
+        for (int d4 = 0; d4 < kDt / 4; ++d4) {
+          const f32x4_t x = {o[rt][d4 * 4 + 0][i], o[rt][d4 * 4 + 1][i], o[rt][d4 * 4 + 2][i],
+                             o[rt][d4 * 4 + 3][i]};
+          f32x4_t* dp = reinterpret_cast<f32x4_t*>(dst + 4 * d4);
+          if (!add) *dp = x;
+          else *dp = *dp + x;
         }
       }
     }
-    __syncthreads();
-  }
-  // row r, elements [8c, 8c + 8) of the merged (unnormalised) output
-  auto merged8 = [&](int r, int c, f32x4_t& lo, f32x4_t& hi) {
-    const float* src = osh + r * kOPitch + c * 8;
-    lo = *reinterpret_cast<const f32x4_t*>(src);
-    hi = *reinterpret_cast<const f32x4_t*>(src + 4);
+  };
+  if constexpr (kOwn) {
+    // no wait for the other waves: the region and the (m, l) slots are this wave's alone
 #pragma unroll
-    for (int g = 1; g < kRegions; ++g) {
-      lo += *reinterpret_cast<const f32x4_t*>(src + g * kRegionFloats);
-      hi += *reinterpret_cast<const f32x4_t*>(src + g * kRegionFloats + 4);
+    for (int rt = 0; rt < RT; ++rt) {
+      if (grp == 0) {
+        sm_m[wave][rt * 16 + l16] = m_run[rt];
+        sm_l[wave][rt * 16 + l16] = l_run[rt];
+      }
+    }
+    store_acc(osh + wave * kRegionFloats, false);
+    __syncthreads();
+  } else {
+    __syncthreads();  // Q in LDS is dead; the merge below reuses the space
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      if (grp == 0) {
+        sm_m[wave][rt * 16 + l16] = m_run[rt];
+        sm_l[wave][rt * 16 + l16] = l_run[rt];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int r = rt * 16 + l16;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][r]);
+      float Lsum = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w)
+        if (sm_m[w][r] > -INFINITY) Lsum += sm_l[w][r] * exp2_fast(sm_m[w][r] - M);
+      const float f = m_run[rt] > -INFINITY ? exp2_fast(m_run[rt] - M) : 0.0f;
+#pragma unroll
+      for (int dt = 0; dt < kDt; ++dt) o[rt][dt] *= f;
+      if (wave == 0 && grp == 0) {
+        sm_M[r] = M;
+        sm_L[r] = Lsum;
+      }
+    }
+    // wave w stores into region w % kRegions in round w / kRegions (later rounds add); the
+    // output pass sums the regions in order
+#pragma unroll
+    for (int round = 0; round < kWaves / kRegions; ++round) {
+      if (wave / kRegions == round) store_acc(osh + (wave % kRegions) * kRegionFloats, round > 0);
+      __syncthreads();
+    }
+  }
+  // row r, elements [8c, 8c + 8) of the merged (unnormalised) output, relative to 2^M, and
+  // the row's (M, L)
+  auto merged8 = [&](int r, int c, f32x4_t& lo, f32x4_t& hi, float& M, float& Lsum) {
+    const float* src = osh + r * kOPitch + c * 8;
+    if constexpr (kOwn) {
+      M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][r]);
+      Lsum = 0.0f;
+      lo = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      hi = lo;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float mw = sm_m[w][r];
+        const float f = mw > -INFINITY ? exp2_fast(mw - M) : 0.0f;
+        Lsum += sm_l[w][r] * f;
+        lo += *reinterpret_cast<const f32x4_t*>(src + w * kRegionFloats) * f;
+        hi += *reinterpret_cast<const f32x4_t*>(src + w * kRegionFloats + 4) * f;
+      }
+    } else {
+      M = sm_M[r];
+      Lsum = sm_L[r];
+      lo = *reinterpret_cast<const f32x4_t*>(src);
+      hi = *reinterpret_cast<const f32x4_t*>(src + 4);
+#pragma unroll
+      for (int g = 1; g < kRegions; ++g) {
+        lo += *reinterpret_cast<const f32x4_t*>(src + g * kRegionFloats);
+        hi += *reinterpret_cast<const f32x4_t*>(src + g * kRegionFloats + 4);
+      }
     }
   };
 
@@ -878,10 +923,10 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
   if (nsplit == 1) {
     for (int idx = tid; idx < R * kCh; idx += kBlock) {
       const int r = idx / kCh, c = idx % kCh;
-      const float Lr = sm_L[r];
-      const float inv = Lr > 0.0f ? 1.0f / Lr : 0.0f;
       f32x4_t lo, hi;
-      merged8(r, c, lo, hi);
+      float Mr, Lr;
+      merged8(r, c, lo, hi, Mr, Lr);
+      const float inv = Lr > 0.0f ? 1.0f / Lr : 0.0f;
       u32x4_t v;
       v[0] = pack_bf16x2(lo[0] * inv, lo[1] * inv);
       v[1] = pack_bf16x2(lo[2] * inv, lo[3] * inv);
@@ -900,12 +945,13 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
   for (int idx = tid; idx < R * kCh; idx += kBlock) {
     const int r = idx / kCh, c = idx % kCh;
     f32x4_t lo, hi;
-    merged8(r, c, lo, hi);
+    float Mr, Lr;
+    merged8(r, c, lo, hi, Mr, Lr);
     float* dst = a.part_o + (pbase + r) * D + c * 8;
     reinterpret_cast<f32x4_t*>(dst)[0] = lo;
     reinterpret_cast<f32x4_t*>(dst)[1] = hi;
+    if (c == 0) a.part_ml[pbase + r] = make_float2(Mr, Lr);
   }
-  if (tid < R) a.part_ml[pbase + tid] = make_float2(sm_M[tid], sm_L[tid]);
   };  // run_piece
 
   // Clamps keep a malformed call (seq_len > max_seqlen_k, q_len > max_seqlen_q, block ids
