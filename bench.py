@@ -162,11 +162,11 @@ def cpu_attention(torch, q, kc, vc, ks, vs, table, seq, qlen, seqs, D):
     return out
 
 
-def attention_case(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128, cpu_sample=0):
-    """Verify attention over len(ctx) sequences with ctx[b] cached tokens and q_len new rows
-    each (seq_len = ctx + q_len), Hq 32 / Hkv 8, head size D (128: the target; 64: the draft),
-    block size 16, block tables a seeded permutation of a shared pool.  K/V are N(0,1) with 1%
-    x20 outliers, quantised on write for INT8."""
+def attention_setup(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128):
+    """The paged cache of an attention case: len(ctx) sequences with ctx[b] cached tokens and
+    q_len new rows each (seq_len = ctx + q_len), Hq 32 / Hkv 8, head size D, block size 16,
+    block tables a seeded permutation of a shared pool.  K/V are N(0,1) with 1% x20 outliers,
+    quantised on write for INT8."""
     import numpy as np
 
     Hq, Hkv, bs = 32, 8, 16
@@ -176,12 +176,12 @@ def attention_case(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128, cpu_sample=0
     W = -(-seq // bs)
     nblk = int(W.sum()) + 1
     perm = np.random.default_rng(seed).permutation(nblk)
-    table = np.zeros((B, int(W.max())), np.int32)
+    table_np = np.zeros((B, int(W.max())), np.int32)
     o = 0
     for b in range(B):
-        table[b, :W[b]] = perm[o:o + W[b]]
+        table_np[b, :W[b]] = perm[o:o + W[b]]
         o += int(W[b])
-    table = torch.from_numpy(table).to(dev)
+    table = torch.from_numpy(table_np).to(dev)
     kc, vc, ks, vs = M.allocate_kv_cache(nblk, bs, Hkv, D, kv_dtype, device=dev)
     g = torch.Generator(device=dev).manual_seed(seed)
     slots = torch.arange(nblk * bs, device=dev)
@@ -192,15 +192,25 @@ def attention_case(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128, cpu_sample=0
         kv = kv.to(torch.bfloat16)
         M.reshape_and_cache_flash(kv[0], kv[1], kc, vc, slots[lo:hi], kv_dtype, ks, vs)
         del kv
-    q = torch.randn(B * qlen, Hq, D, generator=g, device=dev).to(torch.bfloat16)
     cu = torch.arange(B + 1, dtype=torch.int32, device=dev) * qlen
     sl = torch.from_numpy(seq.astype(np.int32)).to(dev)
-    max_k = int(seq.max())
+    per_tok = Hkv * D * 2 * 2 if kv_dtype == "auto" else Hkv * (2 * D + 2 * 2)
+    return dict(Hq=Hq, Hkv=Hkv, bs=bs, ctx=ctx, B=B, seq=seq, table_np=table_np, table=table,
+                caches=(kc, vc, ks, vs), gen=g, cu=cu, sl=sl, max_k=int(seq.max()),
+                per_tok=per_tok)
+
+
+def attention_case(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128, cpu_sample=0):
+    """Verify attention (coopt_verify_attention) over the cache of attention_setup."""
+    st = attention_setup(torch, M, dev, ctx, qlen, kv_dtype, seed, D)
+    Hq, Hkv, B, seq, ctx = st["Hq"], st["Hkv"], st["B"], st["seq"], st["ctx"]
+    kc, vc, ks, vs = st["caches"]
+    table, cu, sl, max_k, g = st["table"], st["cu"], st["sl"], st["max_k"], st["gen"]
+    q = torch.randn(B * qlen, Hq, D, generator=g, device=dev).to(torch.bfloat16)
     out = torch.empty_like(q)
     ws = torch.empty(M.attention.workspace_bytes(B, Hq, Hkv, D, qlen, max_k), dtype=torch.uint8,
                      device=dev)
-    per_tok = Hkv * D * 2 * 2 if kv_dtype == "auto" else Hkv * (2 * D + 2 * 2)
-    nbytes = int(seq.sum()) * per_tok + 2 * B * qlen * Hq * D * 2
+    nbytes = int(seq.sum()) * st["per_tok"] + 2 * B * qlen * Hq * D * 2
 
     def fn():
         M.paged_attention(q, kc, vc, cu, sl, table, qlen, max_k, D ** -0.5, ks, vs, out, ws)
@@ -225,6 +235,52 @@ def attention_case(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128, cpu_sample=0
         legs["sample"] = f"{len(seqs)} of {B} sequences ({share:.1%} of the keys), fp32 torch on the host"
         res["cpu"] = legs
     return res
+
+
+def attention_qkv_case(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128, hidden=4096):
+    """The step's form of the call: coopt_verify_attention_qkv, the qkv projection's split-K
+    partials in (coopt_linear_packed with defer_reduce, as the step runs it: hidden -> (Hq +
+    2 Hkv) D over B q_len rows), RoPE, the new rows' K/V written at key positions ctx ..
+    ctx + q_len - 1, and the attention over the cache of attention_setup.  Algorithmic bytes:
+    the K/V of every key (the new ones read back after their write), the partials once, the
+    new rows' K/V written, the RoPE table rows and the output."""
+    import numpy as np
+
+    st = attention_setup(torch, M, dev, ctx, qlen, kv_dtype, seed, D)
+    Hq, Hkv, bs, B, seq, ctx = st["Hq"], st["Hkv"], st["bs"], st["B"], st["seq"], st["ctx"]
+    kc, vc, ks, vs = st["caches"]
+    g = st["gen"]
+    T, width = B * qlen, (Hq + 2 * Hkv) * D
+    x = torch.randn(T, hidden, generator=g, device=dev).to(torch.bfloat16)
+    w = M.fused.pack_linear_weight((torch.randn(width, hidden, generator=g, device=dev) * 0.02)
+                                   .to(torch.bfloat16))
+    part = M.fused.linear(x, w, defer_reduce=True)
+    if not isinstance(part, M.fused.LinearPartials):
+        raise RuntimeError("expected split-K partials from the qkv projection")
+    pos_np = np.concatenate([np.arange(c, c + qlen) for c in ctx]).astype(np.int64)
+    tb = st["table_np"]
+    slot_np = np.concatenate([tb[b][np.arange(c, c + qlen) // bs] * bs + np.arange(c, c + qlen) % bs
+                              for b, c in enumerate(ctx)]).astype(np.int64)
+    pos, slots = torch.from_numpy(pos_np).to(dev), torch.from_numpy(slot_np).to(dev)
+    max_pos = st["max_k"] + 8
+    inv = 500000.0 ** (-torch.arange(0, D // 2, dtype=torch.float64) * 2 / D)
+    ang = torch.arange(max_pos, dtype=torch.float64)[:, None] * inv[None, :]
+    cos, sin = ang.cos().to(dev, torch.bfloat16), ang.sin().to(dev, torch.bfloat16)
+    if not M.qkv_attention_supported(kv_dtype, B, Hq, Hkv, D, qlen, st["max_k"]):
+        raise RuntimeError("shape not taken by the fused call")
+    out = torch.empty(T, Hq, D, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(M.attention.workspace_bytes(B, Hq, Hkv, D, qlen, st["max_k"]),
+                     dtype=torch.uint8, device=dev)
+
+    def fn():
+        M.paged_attention_qkv(part, pos, cos, sin, slots, kc, vc, st["cu"], st["sl"], st["table"],
+                              qlen, st["max_k"], Hq, D ** -0.5, kv_dtype, ks, vs, out, ws)
+
+    nbytes = (int(seq.sum()) * st["per_tok"] + part.ks * T * width * 4 + T * st["per_tok"]
+              + T * D * 2 + T * Hq * D * 2)
+    res = {"kv": kv_dtype, "head_dim": D, "batch": B, "q_len": qlen, "ctx": int(ctx.max()),
+           "qkv_partials": part.ks, "hidden": hidden}
+    return rate(res, nbytes, *time_launches(torch, dev, fn))
 
 
 def accept_case(torch, M, dev, B, gamma, V, seed):
@@ -512,6 +568,9 @@ KERNEL_CASES = {
     "attention_step_target": lambda t, M, d, s: attention_case(t, M, d, [1100] * 32, 5, "int8", s),
     "attention_step_draft": lambda t, M, d, s: attention_case(t, M, d, [1100] * 32, 1, "auto", s, D=64),
     "attention_step_draft_q2": lambda t, M, d, s: attention_case(t, M, d, [1100] * 32, 2, "auto", s, D=64),
+    # the same launches as the step makes them: the qkv epilogue inside the attention launch
+    "attention_qkv_step_target": lambda t, M, d, s: attention_qkv_case(t, M, d, [1100] * 32, 5, "int8", s),
+    "attention_qkv_step_draft": lambda t, M, d, s: attention_qkv_case(t, M, d, [1100] * 32, 1, "auto", s, D=64, hidden=2048),
     # config 1 (B=8) and the metric's B=32
     "accept_b8": lambda t, M, d, s: accept_case(t, M, d, 8, 4, 128256, s),
     "accept_b32": lambda t, M, d, s: accept_case(t, M, d, 32, 4, 128256, s),

@@ -122,10 +122,14 @@ __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
 struct RopeTab {
   uint4 cos, sin;
 };
+// the table row a position reads: positions outside [0, max_pos) read the nearest row
+__device__ __forceinline__ int64_t clamp_pos(int64_t p, int max_pos) {
+  return p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p);
+}
 template <int G>
 __device__ __forceinline__ RopeTab rope_tab(const uint16_t* cos, const uint16_t* sin, int64_t stride,
                                             int64_t p, int max_pos, int c) {
-  p = p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p);
+  p = clamp_pos(p, max_pos);
   const int i0 = (c < G / 2 ? c : c - G / 2) * 8;
   RopeTab t;
   t.cos = *reinterpret_cast<const uint4*>(cos + p * stride + i0);

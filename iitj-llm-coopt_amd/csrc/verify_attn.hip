@@ -334,6 +334,10 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
       const int hl = is_kv ? 0 : vi / n;
       const int t = q0 + j;
       const int head = is_kv ? Hq + hkv : hkv * a.G + hl;
+      // The RoPE rows of the row's key position L - n + j, which is its position in every
+      // step; loaded with the partials, and again below only if positions[t] says otherwise
+      const int64_t p_key = L - n + j;
+      RopeTab tab = rope_tab<GL>(a.cos, a.sin, a.tab_stride, p_key, a.max_pos, c);
       const int64_t p = a.pos[t];
       const int64_t slot = is_kv ? a.slots[t] : -1;
       const int64_t col = static_cast<int64_t>(head) * D + c * 8;
@@ -359,7 +363,8 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
         xr = *reinterpret_cast<const uint4*>(rr + col);
         if (is_kv) vr = *reinterpret_cast<const uint4*>(rr + vcol);
       }
-      const RopeTab tab = rope_tab<GL>(a.cos, a.sin, a.tab_stride, p, a.max_pos, c);
+      if (clamp_pos(p, a.max_pos) != clamp_pos(p_key, a.max_pos))
+        tab = rope_tab<GL>(a.cos, a.sin, a.tab_stride, p, a.max_pos, c);
       const uint4 yr = rope_chunk<GL>(xr, tab, c);
       if (!is_kv) {
         const int r = hl * n + j;  // < R <= kRows
@@ -380,7 +385,9 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
     }
   };
   // Run here, before the attention's own state is set up: its scalars (kernel-argument
-  // fields) are dead again by the time the loop's page bases and offsets are live.
+  // fields) are dead again by the time the loop's page bases and offsets are live.  (Run
+  // after the first tile's loads are issued, to overlap them, it made the compiler move
+  // ~35 scalars into vector-register lanes and measured slower.)
   if constexpr (FUSED) fused_epilogue();
   auto stage_q = [&]() {
     if (!fused) {

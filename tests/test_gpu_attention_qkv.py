@@ -30,7 +30,7 @@ def rope_tables(max_pos, D, dev, theta=500000.0):
     return ang.cos().to(torch.bfloat16).to(dev), ang.sin().to(torch.bfloat16).to(dev)
 
 
-def build(dev, B, Hq, Hkv, D, S, ctx, n_real, kv, qkv_kind, seed, bs=16):
+def build(dev, B, Hq, Hkv, D, S, ctx, n_real, kv, qkv_kind, seed, bs=16, pos_shift=None):
     gen = torch.Generator(device=dev).manual_seed(seed)
     rng = np.random.default_rng(seed)
     W = [-(-(c + S) // bs) for c in ctx]
@@ -53,7 +53,7 @@ def build(dev, B, Hq, Hkv, D, S, ctx, n_real, kv, qkv_kind, seed, bs=16):
     for b in range(B):
         for j in range(S):
             p = ctx[b] + j
-            pos.append(p)
+            pos.append(p + (pos_shift(b, j) if pos_shift else 0))
             slots.append(int(table[b][p // bs]) * bs + p % bs if j < n_real[b] else -1)
     T = B * S
     hidden = 4096 if D == 128 else 2048     # the target's and the draft's hidden sizes
@@ -64,7 +64,7 @@ def build(dev, B, Hq, Hkv, D, S, ctx, n_real, kv, qkv_kind, seed, bs=16):
         assert isinstance(qkv, M.fused.LinearPartials), "expected the split-K kernel path"
         assert 1 <= qkv.ks <= 4, qkv.ks
         report(f"[fused qkv] B={B} S={S} D={D}: {qkv.ks} K slice(s)")
-    cos, sin = rope_tables(max(c + S for c in ctx) + 8, D, dev)
+    cos, sin = rope_tables(max(max(pos), max(c + S for c in ctx)) + 8, D, dev)
     meta = dict(pos=torch.tensor(pos, dtype=torch.int64, device=dev),
                 slots=torch.tensor(slots, dtype=torch.int64, device=dev),
                 cu=(torch.arange(B + 1, dtype=torch.int32, device=dev) * S),
@@ -119,6 +119,29 @@ def test_fused_equals_epilogue_then_attention(dev, label, kv, D, B, S, kind):
     for x, y in zip(ca, cb):
         if x is not None:
             assert torch.equal(x, y), f"{label}: caches differ"
+
+
+def test_positions_other_than_key_positions(dev):
+    """RoPE positions that differ from the rows' key positions (the kernel loads the table rows
+    of the key position first and reloads on a mismatch), including one past the table."""
+    B, S, D, Hq, Hkv, kv = 32, 5, 128, 32, 8, "int8"
+    rng = np.random.default_rng(5)
+    ctx = rng.integers(30, 900, B).tolist()
+    n_real = [S] * B
+
+    def shift(b, j):
+        return 0 if b % 3 == 0 else (3 * b + j if b % 3 == 1 else -(ctx[b] + j) - 5 + 4 * j)
+
+    caches, qkv, m = build(dev, B, Hq, Hkv, D, S, ctx, n_real, kv, "partials", seed=11,
+                           pos_shift=shift)
+    # a table that ends before the largest position: that row reads the last table row
+    m["cos"], m["sin"] = m["cos"][:-9], m["sin"][:-9]
+    ref, got, ca, cb = run_both(caches, qkv, m, Hq, Hkv, D, kv)
+    report(f"[fused qkv] shifted positions: max |diff| {float((ref.float() - got.float()).abs().max()):.3g}")
+    assert torch.equal(ref, got)
+    for x, y in zip(ca, cb):
+        if x is not None:
+            assert torch.equal(x, y), "caches differ"
 
 
 def test_unsupported_shapes_are_refused(dev):
