@@ -44,6 +44,11 @@ SIGNATURES = {
     "coopt_linear_partials": (_i, [_p, _i64, _p, _i64, _i, _i, _i, _p, _sz, _p]),
     "coopt_linear_pack_weight": (_i, [_p, _i64, _i, _i, _p, _p]),
     "coopt_row_slots": (_i, [_p, _i64, _i, _p, _p, _i, _i, _i, _p, _p, _p, _p]),
+    "coopt_spec_step_begin": (_i, [_p, _i64, _i, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i, _i,
+                                   _i, _i, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p]),
+    "coopt_spec_step_verify_tokens": (_i, [_p, _i64, _i, _i, _p, _p, _p]),
+    "coopt_spec_step_commit": (_i, [_p, _p, _p, _i, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _i,
+                                    _p]),
     "coopt_linear_pack_gate_up": (_i, [_p, _i64, _i, _i, _p, _p]),
     "coopt_linear_silu_supported": (_i, [_i, _i, _i]),
     "coopt_linear_silu_packed": (_i, [_p, _i64, _p, _i, _i, _i, _p, _i64, _p]),

@@ -18,7 +18,8 @@ BUILD_DIR = os.path.join(HERE, "_build")
 LIB_NAME = "libcoopt_amd.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 
-SOURCES = ["abi.hip", "kv_cache.hip", "kv_blocks.hip", "accept.hip", "verify_attn.hip", "fused.hip", "linear.hip"]
+SOURCES = ["abi.hip", "kv_cache.hip", "kv_blocks.hip", "accept.hip", "verify_attn.hip", "fused.hip",
+           "linear.hip", "spec_step.hip"]
 
 ARCH = "gfx950"
 # -packed-fp32-ops: keep hipcc from forming packed fp32 VALU ops (the pool's known hazard).

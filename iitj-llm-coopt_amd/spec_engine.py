@@ -133,8 +133,9 @@ class RandomLlama:
         other.cos, other.sin, other.scale = self.cos.to(device), self.sin.to(device), self.scale
         return other
 
-    def forward(self, ops, kv, ids, pos, slots, meta, logits_out=None):
-        """ids/pos/slots [T]; meta: attention metadata for ops.attend; returns logits [T, V].
+    def forward(self, ops, kv, ids, pos, slots, meta, logits_out=None, keep_rows=None):
+        """ids/pos/slots [T]; meta: attention metadata for ops.attend; returns logits [T, V],
+        or only the rows `keep_rows` (int64 indices into the T rows) of them.
 
         The layer structure of the reference's fused forward (engine/model.py:220-255): the
         residual stream x is updated in place by the fused add + RMSNorm, RoPE rotates q and k
@@ -165,6 +166,8 @@ class RandomLlama:
             h = ops.rms_norm(o, x, L["ln2"], s.eps)
             d = ops.linear(ops.linear_silu(h, L["gate_up"]), L["down"], defer_reduce=True)
         h = ops.rms_norm(d, x, self.norm, s.eps)
+        if keep_rows is not None:
+            h = h.index_select(0, keep_rows)
         return ops.linear(h, self.lm_head, out=logits_out)
 
 
@@ -376,7 +379,8 @@ class SpecDecoder:
         V = target.s.vocab
         self.draft_logits = torch.empty((Bc, self.smax - 1, V), dtype=torch.bfloat16, device=dev)
         self.target_logits = torch.empty((Bc * self.smax, V), dtype=torch.bfloat16, device=dev)
-        self.draft_tok = torch.zeros((Bc, self.smax - 1), dtype=torch.int32, device=dev)
+        # proposal i of slot b at prop[i, b]: each draft sample writes its row in place
+        self.prop = torch.zeros((self.smax - 1, Bc), dtype=torch.int32, device=dev)
         self.nu = Bc * (2 * gamma + 1)
         self.u = torch.zeros(self.nu, dtype=torch.float32, device=dev)
         self.u_ctr = torch.zeros((), **i64)
@@ -386,8 +390,18 @@ class SpecDecoder:
         self._acc_len = torch.zeros(Bc, dtype=torch.int32, device=dev)
         self._margin = torch.zeros(Bc, dtype=torch.float32, device=dev)
         self._acc_tok = {S: torch.zeros((Bc, S), dtype=torch.int32, device=dev) for S in self.strides}
+        # the step's bookkeeping (coopt_spec_step_*): catch-up, proposal and verify rows
+        i32 = dict(dtype=torch.int32, device=dev)
+        self._cu_start, self._cu_nreal, self._cu_keep = (torch.zeros(Bc, **i64) for _ in range(3))
+        self._cu_tok = torch.zeros(Bc * max_catchup, **i64)
+        self._pr_start = torch.zeros((max(self.smax - 2, 1), Bc), **i64)
+        self._pr_nreal = torch.zeros((max(self.smax - 2, 1), Bc), **i64)
+        self._v_start, self._v_nreal, self._dc_final = (torch.zeros(Bc, **i64) for _ in range(3))
+        self._vtok = {S: torch.zeros((Bc, S), **i32) for S in self.strides}
+        self._dtok = {S: torch.zeros((Bc, max(S - 1, 1)), **i32) for S in self.strides}
+        self._s_len = torch.zeros(Bc, **i32)          # sample outputs other than the token
+        self._s_margin = torch.zeros(Bc, dtype=torch.float32, device=dev)
         self.res = AcceptResult(self._acc_len, self._acc_tok[self.smax], self._margin)
-        self.ar = {S: torch.arange(S, **i64) for S in range(1, max(self.smax, max_catchup) + 1)}
         self._cu = {}
         self._row0 = {}
         self.graphs = {}
@@ -404,6 +418,11 @@ class SpecDecoder:
     @property
     def g(self):
         return self.gmax
+
+    @property
+    def draft_tok(self):
+        """The last step's proposals as [slot, i] (a view of the proposal-major buffer)."""
+        return self.prop.t()
 
     def set_uniforms(self, table):
         """table [rows, (2*gamma_max + 1) * Bcap] fp32 (layout in the class docstring); the next
@@ -537,76 +556,70 @@ class SpecDecoder:
         return self._row0[key]
 
     # ---- one speculative step -------------------------------------------------------------
-    def _rows(self, model, kv, Bc, start, S, tokens, n_real, logits_out=None):
+    def _rows(self, model, kv, Bc, start, S, tokens, n_real, logits_out=None, keep_rows=None):
         """Forward S rows per sequence at positions start..start+S-1 over slots [0, Bc); rows
         j >= n_real[b] are padding (KV write skipped, seq_len = start + S as in the padded
         graph layout).  Positions, slots and seq_lens come from one coopt_row_slots launch."""
         pos, slots, seq_lens = self.ops.row_slots(kv, start, S, n_real)
         meta = (self._meta(Bc, S), seq_lens, S, self.max_len)
         return model.forward(self.ops, kv, tokens.reshape(-1), pos.reshape(-1), slots, meta,
-                             logits_out=logits_out)
+                             logits_out=logits_out, keep_rows=keep_rows)
 
     @torch.inference_mode()
     def _step(self, Bc, G, S_t, S_c):
-        T, V = self.T, self.t.s.vocab
+        T = self.T
         gm, Bcap = self.gmax, self.Bcap
-        u = torch.index_select(self.u_table, 0, torch.remainder(self.u_ctr, self.u_table.shape[0]).view(1))
-        self.u.copy_(u.view(-1))
-        self.u_ctr += 1
         u_draft = self.u[: gm * Bcap].view(gm, Bcap)
         u_acc = self.u[gm * Bcap: 2 * gm * Bcap].view(Bcap, gm)
         u_res = self.u[2 * gm * Bcap:]
-        live, greq = self.live_dev[:Bc], self.gamma_dev[:Bc]
-        n, dc = self.n[:Bc], self.dc[:Bc]
-        zero = torch.zeros_like(n)
-        lag = n - dc
-        want = live & (greq > 0)
-        spec = want & (lag <= 2)
-        lagging = want & (lag > 2)
-        geff = torch.where(spec, greq, zero)
-        m = torch.where(spec, lag, torch.where(lagging, torch.clamp(lag - 1, max=S_c), zero))
-        # draft: catch-up over tokens[dc : dc + m] (stride S_c) and the first proposal
-        dc1 = dc.clone()
+        vt, dt = self._vtok[S_t], self._dtok[S_t]
+        lib, dev = _lib.load(), self.hist.device
+        stream = _lib.stream_handle(dev)
+        # the step's uniforms, each sequence's mode, and every row the draft and the verify run
+        # (engine/engine.py:354-389, 414-417): one launch
+        _lib.check(lib.coopt_spec_step_begin(
+            _lib.ptr(self.u_table), self.u_table.shape[0], self.nu, _lib.ptr(self.u_ctr),
+            _lib.ptr(self.u), _lib.ptr(self.live_dev), _lib.ptr(self.gamma_dev), _lib.ptr(self.n),
+            _lib.ptr(self.dc), _lib.ptr(self.hist), self.hist.stride(0), self.max_len, Bc, G, S_c,
+            S_t, _lib.ptr(self.gamma_eff), _lib.ptr(self._cu_start), _lib.ptr(self._cu_nreal),
+            _lib.ptr(self._cu_tok), _lib.ptr(self._cu_keep), _lib.ptr(self._pr_start),
+            _lib.ptr(self._pr_nreal), self._pr_start.stride(0), _lib.ptr(self._v_start),
+            _lib.ptr(self._v_nreal), _lib.ptr(vt), _lib.ptr(self._dc_final), stream),
+            "coopt_spec_step_begin")
         if G > 0:
-            start = torch.where(live, dc, zero)
-            idx = (start.unsqueeze(1) + self.ar[S_c]).clamp(max=self.max_len - 1)
-            toks = torch.gather(self.hist[:Bc], 1, idx)
-            logits = self._rows(self.d, self.dkv, Bc, start, S_c, toks, m).view(Bc, S_c, V)
-            last = torch.gather(logits, 1, (m - 1).clamp(min=0).view(Bc, 1, 1).expand(Bc, 1, V))
-            self.draft_logits[:Bc, 0] = last[:, 0]
-            self.draft_tok[:Bc, 0] = self.ops.sample(self.draft_logits[:Bc, 0], u_draft[0, :Bc], T)
-            dc1 = dc1 + m
+            # draft catch-up over tokens[dc : dc + m] (stride S_c); only the row the first
+            # proposal is drawn from goes through the logits projection
+            self._rows(self.d, self.dkv, Bc, self._cu_start[:Bc], S_c, self._cu_tok[: Bc * S_c],
+                       self._cu_nreal[:Bc], logits_out=self.draft_logits[:Bc, 0],
+                       keep_rows=self._cu_keep[:Bc])
+            self._sample(0, Bc, u_draft[0, :Bc])
             for i in range(1, G):
-                active = (spec & (geff > i)).long()
-                start = torch.where(live, dc1, zero)
-                self._rows(self.d, self.dkv, Bc, start, 1, self.draft_tok[:Bc, i - 1].long(), active,
-                           logits_out=self.draft_logits[:Bc, i])
-                dc1 = dc1 + active
-                self.draft_tok[:Bc, i] = self.ops.sample(self.draft_logits[:Bc, i], u_draft[i, :Bc], T)
+                self._rows(self.d, self.dkv, Bc, self._pr_start[i - 1, :Bc], 1, self.prop[i - 1, :Bc],
+                           self._pr_nreal[i - 1, :Bc], logits_out=self.draft_logits[:Bc, i])
+                self._sample(i, Bc, u_draft[i, :Bc])
         # target verify over [last token] + drafts (stride S_t; rows past gamma_eff + 1 padding)
-        start = torch.where(live, n - 1, zero)
-        last_tok = torch.gather(self.hist[:Bc], 1, start.unsqueeze(1))
-        vt = torch.cat([last_tok, self.draft_tok[:Bc, : S_t - 1].long()], 1)
-        self._rows(self.t, self.tkv, Bc, start, S_t, vt, torch.where(live, geff + 1, zero),
+        _lib.check(lib.coopt_spec_step_verify_tokens(
+            _lib.ptr(self.prop), self.prop.stride(0), Bc, S_t, _lib.ptr(vt), _lib.ptr(dt), stream),
+            "coopt_spec_step_verify_tokens")
+        self._rows(self.t, self.tkv, Bc, self._v_start[:Bc], S_t, vt[:Bc], self._v_nreal[:Bc],
                    logits_out=self.target_logits[: Bc * S_t])
-        self.gamma_eff[:Bc] = geff.to(torch.int32)
         res = AcceptResult(self._acc_len[:Bc], self._acc_tok[S_t][:Bc], self._margin[:Bc])
-        res = self.ops.accept(self.target_logits[: Bc * S_t], self.draft_logits.view(Bcap * (self.smax - 1), V),
-                              self.draft_tok[:Bc, : S_t - 1], T, u_acc[:Bc, : S_t - 1], u_res[:Bc],
+        res = self.ops.accept(self.target_logits[: Bc * S_t], self.draft_logits.view(Bcap * (self.smax - 1), -1),
+                              dt[:Bc, : S_t - 1], T, u_acc[:Bc, : S_t - 1], u_res[:Bc],
                               out=res, gamma_per_seq=self.gamma_eff[:Bc],
                               target_row0=self._rows0(Bc, S_t), draft_row0=self._rows0(Bc, self.smax - 1))
-        acc = torch.where(live, res.accepted_len.long(), zero)
         # append drafts[:k] + [token] to live histories; rollback is the length update
-        pos = (n.unsqueeze(1) + self.ar[S_t]).clamp(max=self.max_len - 1)
-        keep = (self.ar[S_t].unsqueeze(0) <= acc.unsqueeze(1)) & live.unsqueeze(1)
-        old = torch.gather(self.hist[:Bc], 1, pos)
-        self.hist[:Bc].scatter_(1, pos, torch.where(keep, res.tokens.long(), old))
-        new_n = torch.where(live, n + acc + 1, n)
-        self.dc[:Bc] = torch.where(live, torch.minimum(dc1, new_n - 1), dc)
-        self.n[:Bc] = new_n
-        self.emitted += torch.where(live, acc + 1, zero).sum()
-        self.drafted += geff.sum()
-        self.accepted += acc.sum()
+        # (engine/engine.py:444-446, 455, 463-470): one launch
+        _lib.check(lib.coopt_spec_step_commit(
+            _lib.ptr(self.live_dev), _lib.ptr(res.accepted_len), _lib.ptr(res.tokens), S_t,
+            _lib.ptr(self.gamma_eff), _lib.ptr(self._dc_final), _lib.ptr(self.n), _lib.ptr(self.dc),
+            _lib.ptr(self.hist), self.hist.stride(0), self.max_len, _lib.ptr(self.emitted),
+            _lib.ptr(self.drafted), _lib.ptr(self.accepted), Bc, stream), "coopt_spec_step_commit")
+
+    def _sample(self, i, Bc, u):
+        """Draft token i of every slot, drawn from draft_logits[:, i] into prop[i] in place."""
+        out = AcceptResult(self._s_len[:Bc], self.prop[i, :Bc].view(Bc, 1), self._s_margin[:Bc])
+        self.ops.sample(self.draft_logits[:Bc, i], u, self.T, out=out)
 
     def step(self):
         """One eager step (same device work as a graph replay, launched from the host)."""

@@ -42,6 +42,10 @@
  *                           / verify row counts             253 (qkv, o, gate_up, down)
  *   coopt_linear_*packed    the same, tile-packed weights   engine/model.py:238, 248, 253
  *   coopt_linear_silu_packed  gate_up + silu_and_mul        engine/model.py:250-252
+ *   coopt_spec_step_begin /  the host-side bookkeeping of   engine/engine.py:354-389,
+ *   _verify_tokens / _commit one speculative step: lag,     414-417, 444-446, 455,
+ *                           catch-up, proposal rows, verify 463-470
+ *                           rows, append, rollback, counters
  */
 #ifndef COOPT_AMD_H
 #define COOPT_AMD_H
@@ -465,6 +469,56 @@ int coopt_linear_pack_gate_up(const void* w, int64_t ldw, int F, int K, void* ou
 int coopt_linear_silu_supported(int M, int F, int K);
 int coopt_linear_silu_packed(const void* x, int64_t ldx, const void* w_gu_packed, int M, int F,
                              int K, void* y, int64_t ldy, coopt_stream_t stream);
+
+/*
+ * Bookkeeping of one speculative step on the device, for the batch in slots [0, Bc) of a
+ * decoder's state (engine/engine.py:338-470 for a batch in which every sequence decodes; the
+ * reference walks Python lists on the host between launches).  One workgroup each; sizes up
+ * to a few hundred sequences.  State per slot: live [Bc] uint8 (0/1), gamma [Bc] int64 (the
+ * caller's draft length), n [Bc] int64 (tokens so far), dc [Bc] int64 (draft KV length,
+ * draft_computed), hist [Bc][hist_stride] int64 (tokens; positions < max_len).
+ *
+ * coopt_spec_step_begin (engine/engine.py:354-389, 414-417): the step's uniforms u[0, nu) =
+ * u_table row (*u_counter mod u_rows), then *u_counter += 1.  Per sequence, with lag = n - dc:
+ * gamma_eff = gamma if live, gamma > 0 and lag <= 2 (speculate), else 0; the draft catch-up
+ * (G > 0 only) starts at cu_start = dc (0 when not live) with cu_nreal = lag when speculating,
+ * min(lag - 1, S_c) when lagging, 0 otherwise, tokens cu_tokens [Bc][S_c] = hist[start + j]
+ * (clamped to max_len - 1), and cu_keep_rows [Bc] = b S_c + max(cu_nreal - 1, 0), the catch-up
+ * row the first proposal is drawn from; proposal i = 1 .. G - 1 starts at pr_start[i - 1][b]
+ * (row stride pr_stride) with pr_nreal = 1 while gamma_eff > i, draft_computed advancing by
+ * that; the verify rows start at v_start = n - 1 with v_nreal = gamma_eff + 1 (0 and 0 when not
+ * live) and token v_tokens[b][0] = hist[v_start] (v_tokens [Bc][S_t]); dc_final = draft_computed
+ * after the draft phase.
+ */
+int coopt_spec_step_begin(const float* u_table, int64_t u_rows, int nu, int64_t* u_counter,
+                          float* u, const uint8_t* live, const int64_t* gamma, const int64_t* n,
+                          const int64_t* dc, const int64_t* hist, int64_t hist_stride,
+                          int64_t max_len, int Bc, int G, int S_c, int S_t, int32_t* gamma_eff,
+                          int64_t* cu_start, int64_t* cu_nreal, int64_t* cu_tokens,
+                          int64_t* cu_keep_rows, int64_t* pr_start, int64_t* pr_nreal,
+                          int64_t pr_stride, int64_t* v_start, int64_t* v_nreal,
+                          int32_t* v_tokens, int64_t* dc_final, coopt_stream_t stream);
+
+/*
+ * After the proposals (engine/engine.py:414-417): proposals [S_t - 1][prop_stride] int32
+ * (proposal i of sequence b at i * prop_stride + b) into v_tokens[b][1 + i] ([Bc][S_t]) and
+ * the accept test's draft rows draft_tokens [Bc][S_t - 1].
+ */
+int coopt_spec_step_verify_tokens(const int32_t* proposals, int64_t prop_stride, int Bc, int S_t,
+                                  int32_t* v_tokens, int32_t* draft_tokens, coopt_stream_t stream);
+
+/*
+ * After the accept (engine/engine.py:444-446, 455, 463-470): for each live sequence with
+ * k = accepted_len (clamped to [0, S_t - 1]), hist[n + j] = tokens[b][j] for j <= k (positions
+ * < max_len; tokens [Bc][S_t] int32), n += k + 1, dc = min(dc_final, n - 1) (the rollback:
+ * num_computed = len - 1 and draft_computed clamped to it); *emitted += sum(k + 1),
+ * *drafted += sum(gamma_eff), *accepted += sum(k) over the live sequences.
+ */
+int coopt_spec_step_commit(const uint8_t* live, const int32_t* accepted_len, const int32_t* tokens,
+                           int S_t, const int32_t* gamma_eff, const int64_t* dc_final, int64_t* n,
+                           int64_t* dc, int64_t* hist, int64_t hist_stride, int64_t max_len,
+                           int64_t* emitted, int64_t* drafted, int64_t* accepted, int Bc,
+                           coopt_stream_t stream);
 
 #ifdef __cplusplus
 }
