@@ -231,8 +231,11 @@ __device__ void plan_item(const AttnArgs& a, int lane, int* out) {
 // stride 1), so a lane's four scales of a sub-tile are one 8-byte load; DB: double-buffer
 // the wave's tiles in registers (RT <= 2, and RT 3 with the smaller INT8 tiles; the other
 // shapes need the registers for accumulators).
-// FUSED: the block runs the qkv epilogue of its rows first (a.qkv_mode != 0).
-template <int D, bool INT8, int RT, bool SC, bool FUSED>
+// FUSED: the block runs the qkv epilogue of its rows first, from bf16 rows (1) or split-K
+// partials (2) -- a.qkv_mode, fixed at compile time so the epilogue's loads all issue at once
+// (a run-time choice of input made the compiler wait for every earlier load where the two
+// input paths joined).
+template <int D, bool INT8, int RT, bool SC, int FUSED>
 __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(AttnArgs a) {
   using Raw = RawTile<D, INT8>;
   constexpr int kWaves = waves_for(RT);
@@ -301,7 +304,7 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
   constexpr int kQCh = D / 8;  // 16-byte chunks per row
   constexpr int kQIter = (kRows * kQCh + kBlock - 1) / kBlock;
   u32x4_t qreg[kQIter];
-  constexpr bool fused = FUSED;
+  constexpr bool fused = FUSED != 0;
 #pragma unroll
   for (int it = 0; it < kQIter; ++it) {
     const int idx = it * kBlock + tid;
@@ -339,29 +342,32 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
       const int64_t p_key = L - n + j;
       RopeTab tab = rope_tab<GL>(a.cos, a.sin, a.tab_stride, p_key, a.max_pos, c);
       const int64_t p = a.pos[t];
-      const int64_t slot = is_kv ? a.slots[t] : -1;
+      const int64_t slot_t = a.slots[t];
+      const int64_t slot = is_kv ? slot_t : -1;
       const int64_t col = static_cast<int64_t>(head) * D + c * 8;
-      const int64_t vcol = static_cast<int64_t>(Hq + a.Hkv + hkv) * D + c * 8;
-      uint4 xr, vr = make_uint4(0, 0, 0, 0);
-      if (a.qkv_mode == 2) {
-        // x, then v: one chunk's partials in registers at a time (the first tile's buffer is
-        // live here), the same order of adds as the reduction of coopt_linear's partials
+      // q lanes point their (unused) v loads at their own x chunk: every load is issued
+      // unconditionally, and before any value is used
+      const int64_t vcol = is_kv ? static_cast<int64_t>(Hq + a.Hkv + hkv) * D + c * 8 : col;
+      uint4 xr, vr;
+      if constexpr (FUSED == 2) {
+        // the same order of adds as the reduction of coopt_linear's partials
         const float* pr = static_cast<const float*>(a.qkv_src) + static_cast<int64_t>(t) * width;
-        auto reduce8 = [&](int64_t cc) {
-          Partials4<kQkvMaxSlices> lo, hi;
-          lo.load(pr + cc, a.qkv_ks, a.qkv_stride);
-          hi.load(pr + cc + 4, a.qkv_ks, a.qkv_stride);
+        Partials4<kQkvMaxSlices> xlo, xhi, vlo, vhi;
+        xlo.load(pr + col, a.qkv_ks, a.qkv_stride);
+        xhi.load(pr + col + 4, a.qkv_ks, a.qkv_stride);
+        vlo.load(pr + vcol, a.qkv_ks, a.qkv_stride);
+        vhi.load(pr + vcol + 4, a.qkv_ks, a.qkv_stride);
+        auto pack8 = [&](const Partials4<kQkvMaxSlices>& lo, const Partials4<kQkvMaxSlices>& hi) {
           const float4 l = lo.sum(a.qkv_ks), h = hi.sum(a.qkv_ks);
           return make_uint4(pack2_bf16(l.x, l.y), pack2_bf16(l.z, l.w), pack2_bf16(h.x, h.y),
                             pack2_bf16(h.z, h.w));
         };
-        xr = reduce8(col);
-        asm volatile("" ::: "memory");  // keep v's loads after x's sum
-        if (is_kv) vr = reduce8(vcol);
+        xr = pack8(xlo, xhi);
+        vr = pack8(vlo, vhi);
       } else {
         const uint16_t* rr = static_cast<const uint16_t*>(a.qkv_src) + static_cast<int64_t>(t) * a.qkv_stride;
         xr = *reinterpret_cast<const uint4*>(rr + col);
-        if (is_kv) vr = *reinterpret_cast<const uint4*>(rr + vcol);
+        vr = *reinterpret_cast<const uint4*>(rr + vcol);
       }
       if (clamp_pos(p, a.max_pos) != clamp_pos(p_key, a.max_pos))
         tab = rope_tab<GL>(a.cos, a.sin, a.tab_stride, p, a.max_pos, c);
@@ -1087,17 +1093,24 @@ template <int D, bool INT8, bool SC>
 int launch_rt(int RT, const AttnArgs& a, dim3 grid, hipStream_t s) {
   if (a.qkv_mode) {
     if (!fused_ok(D, INT8, RT)) return COOPT_EINVAL;  // the caller checked; not reached
+    const bool part = a.qkv_mode == 2;
     if constexpr (fused_ok(D, INT8, 2)) {
-      if (RT == 2) hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 2, SC, true>), grid, dim3(64 * waves_for(2)), 0, s, a);
+      if (RT == 2) {
+        if (part) hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 2, SC, 2>), grid, dim3(64 * waves_for(2)), 0, s, a);
+        else hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 2, SC, 1>), grid, dim3(64 * waves_for(2)), 0, s, a);
+      }
     }
-    if (RT == 1) hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 1, SC, true>), grid, dim3(64 * waves_for(1)), 0, s, a);
+    if (RT == 1) {
+      if (part) hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 1, SC, 2>), grid, dim3(64 * waves_for(1)), 0, s, a);
+      else hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 1, SC, 1>), grid, dim3(64 * waves_for(1)), 0, s, a);
+    }
     return coopt::check_launch("coopt_verify_attention_qkv");  // one split: no merge launch
   }
   switch (RT) {
-    case 1: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 1, SC, false>), grid, dim3(64 * waves_for(1)), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 2, SC, false>), grid, dim3(64 * waves_for(2)), 0, s, a); break;
-    case 3: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 3, SC, false>), grid, dim3(64 * waves_for(3)), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 4, SC, false>), grid, dim3(64 * waves_for(4)), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 1, SC, 0>), grid, dim3(64 * waves_for(1)), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 2, SC, 0>), grid, dim3(64 * waves_for(2)), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 3, SC, 0>), grid, dim3(64 * waves_for(3)), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 4, SC, 0>), grid, dim3(64 * waves_for(4)), 0, s, a); break;
     default: return COOPT_EINVAL;
   }
   int rc = coopt::check_launch("coopt_verify_attention");
