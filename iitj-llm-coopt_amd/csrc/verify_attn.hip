@@ -274,23 +274,30 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
   const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, l16 = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  // One piece: keys [sidx * split, min(L, (sidx + 1) * split)) of (sequence b, KV head hkv)
-  // with query rows [q0, q0 + n); L = min(seq_lens[b], max_seqlen_k).
-  auto run_piece = [&](const int b, const int hkv, const int sidx, const int q0, const int n,
-                       const int L) {
   // The block table is read-only here: reading it through the constant address space lets
   // the wave-uniform page lookups be scalar loads, which do not wait behind (or drain) the
   // wave's outstanding K/V vector loads.
   typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
+  const int64_t bt_last = a.bt_stride - 1;
+  // The pages of the wave's first tile of piece sidx of sequence b, looked up before L is
+  // known: they are used only if that tile is full, i.e. all its keys are < L, where no
+  // clamp to L - 1 applies (the index is kept inside the table row regardless).
+  auto first_pages = [&](int b, int sidx, int32_t& p0, int32_t& p1) {
+    const const_i32_ptr tb = (const_i32_ptr)(a.bt + static_cast<int64_t>(b) * a.bt_stride);
+    const int kb = sidx * a.split + wave * kTileKeys;
+    p0 = tb[min<int64_t>(kb >> a.bs_shift, bt_last)];
+    p1 = tb[min<int64_t>((kb + 16) >> a.bs_shift, bt_last)];
+  };
+
+  // One piece: keys [sidx * split, min(L, (sidx + 1) * split)) of (sequence b, KV head hkv)
+  // with query rows [q0, q0 + n); L = min(seq_lens[b], max_seqlen_k); pg0 / pg1 the pages of
+  // the wave's first tile (first_pages).
+  auto run_piece = [&](const int b, const int hkv, const int sidx, const int q0, const int n,
+                       const int L, const int32_t pg0, const int32_t pg1) {
   const const_i32_ptr table = (const_i32_ptr)(a.bt + static_cast<int64_t>(b) * a.bt_stride);
   const int k_begin = sidx * a.split;
-  // The pages of the wave's first tile, looked up before L is tested: they are used only if
-  // that tile is full, i.e. all its keys are < L, where no clamp to L - 1 applies (the index
-  // is kept inside the table row regardless).
-  const int64_t bt_last = a.bt_stride - 1;
-  const int kb_first = k_begin + wave * kTileKeys;
-  const int64_t first_pg0 = clamp_page(table[min<int64_t>(kb_first >> a.bs_shift, bt_last)], a.num_blocks);
-  const int64_t first_pg1 = clamp_page(table[min<int64_t>((kb_first + 16) >> a.bs_shift, bt_last)], a.num_blocks);
+  const int64_t first_pg0 = clamp_page(pg0, a.num_blocks);
+  const int64_t first_pg1 = clamp_page(pg1, a.num_blocks);
   if (n <= 0) return;
   const int nsplit = L > 0 ? (L + a.split - 1) / a.split : 1;
   if (sidx >= nsplit) return;
@@ -970,6 +977,7 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
   // Clamps keep a malformed call (seq_len > max_seqlen_k, q_len > max_seqlen_q, block ids
   // outside the pool) inside its buffers: such calls give wrong rows, never stray accesses.
   int b, hkv, sidx, q0, n, L;
+  int32_t pg0, pg1;
   if (a.plan) {
     if (wave == 0) plan_item(a, lane, sm_plan);
     __syncthreads();
@@ -979,15 +987,26 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
     L = __builtin_amdgcn_readfirstlane(sm_plan[3]);
     hkv = static_cast<int>(blockIdx.x) % a.Hkv;
     sidx = 0;
+    first_pages(b, sidx, pg0, pg1);
   } else {
     b = blockIdx.z;
     hkv = blockIdx.y;
     sidx = blockIdx.x;
-    q0 = a.cu[b];
-    n = a.cu[b + 1] - q0;
-    L = min(a.seq_lens[b], a.max_seqlen_k);
+    // every scalar the block's first loads depend on, in one round: the row range, the key
+    // count and the first tile's pages, and the kernel-argument lines the Q / K / V (or
+    // epilogue) addressing reads.  The empty asm keeps these loads from being spread over the
+    // code that uses them, each behind a wait of its own.
+    const const_i32_ptr cuc = (const_i32_ptr)a.cu;
+    const const_i32_ptr slc = (const_i32_ptr)a.seq_lens;
+    const int c0 = cuc[b], c1 = cuc[b + 1], sl = slc[b];
+    first_pages(b, sidx, pg0, pg1);
+    const void* line4 = FUSED != 0 ? static_cast<const void*>(a.slots) : static_cast<const void*>(a.q);
+    asm volatile("" ::"s"(c0), "s"(c1), "s"(sl), "s"(pg0), "s"(pg1), "s"(a.kc), "s"(line4));
+    q0 = c0;
+    n = c1 - c0;
+    L = min(sl, a.max_seqlen_k);
   }
-  run_piece(b, hkv, sidx, q0, n, L);
+  run_piece(b, hkv, sidx, q0, n, L, pg0, pg1);
 }
 
 // Second launch: combines the split partials of every (sequence, KV head) that needed more
