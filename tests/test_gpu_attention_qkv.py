@@ -30,7 +30,8 @@ def rope_tables(max_pos, D, dev, theta=500000.0):
     return ang.cos().to(torch.bfloat16).to(dev), ang.sin().to(torch.bfloat16).to(dev)
 
 
-def build(dev, B, Hq, Hkv, D, S, ctx, n_real, kv, qkv_kind, seed, bs=16, pos_shift=None):
+def build(dev, B, Hq, Hkv, D, S, ctx, n_real, kv, qkv_kind, seed, bs=16, pos_shift=None,
+          token_major=False):
     gen = torch.Generator(device=dev).manual_seed(seed)
     rng = np.random.default_rng(seed)
     W = [-(-(c + S) // bs) for c in ctx]
@@ -41,7 +42,15 @@ def build(dev, B, Hq, Hkv, D, S, ctx, n_real, kv, qkv_kind, seed, bs=16, pos_shi
     for b in range(B):
         table[b, :W[b]] = perm[o:o + W[b]]
         o += W[b]
-    kc, vc, ks, vs = M.allocate_kv_cache(NB, bs, Hkv, D, kv, device=dev)
+    if token_major:
+        # the reference's own layout: token-major caches and scales (scale token stride Hkv)
+        cdt = torch.int8 if kv == "int8" else torch.bfloat16
+        kc = torch.zeros(NB, bs, Hkv, D, dtype=cdt, device=dev)
+        vc = torch.zeros_like(kc)
+        ks = torch.zeros(NB, bs, Hkv, dtype=torch.float16, device=dev) if kv == "int8" else None
+        vs = None if ks is None else torch.zeros_like(ks)
+    else:
+        kc, vc, ks, vs = M.allocate_kv_cache(NB, bs, Hkv, D, kv, device=dev)
     # the cached context, written through the KV write
     ctx_slots = np.concatenate([table[b][np.arange(ctx[b]) // bs] * bs + np.arange(ctx[b]) % bs
                                 for b in range(B)]).astype(np.int64)
@@ -100,6 +109,13 @@ CASES = [
     ("bf16 D64 S2 partials", "auto", 64, 32, 2, "partials"),
     ("bf16 D128 S4 bf16 rows", "auto", 128, 32, 4, "bf16"),
     ("int8 D128 S8, 64 sequences (ordered grid)", "int8", 128, 64, 8, "bf16"),
+    # the other instantiations the call can reach: INT8 at head_dim 64, bf16 head_dim 128
+    # from partials at one row tile, and INT8 over the reference's token-major scale caches
+    ("int8 D64 S2 partials", "int8", 64, 32, 2, "partials"),
+    ("int8 D64 S5 bf16 rows", "int8", 64, 32, 5, "bf16"),
+    ("bf16 D128 S2 partials", "auto", 128, 32, 2, "partials"),
+    ("int8 D128 S5 partials, token-major scales", "int8", 128, 32, 5, "partials-tm"),
+    ("int8 D128 S2 bf16 rows, token-major scales", "int8", 128, 32, 2, "bf16-tm"),
 ]
 
 
@@ -112,7 +128,9 @@ def test_fused_equals_epilogue_then_attention(dev, label, kv, D, B, S, kind):
     n_real = rng.integers(1, S + 1, B).tolist()  # ragged real rows, the rest padding
     n_real[1] = S
     assert M.qkv_attention_supported(kv, B, Hq, Hkv, D, S, max(c + S for c in ctx)), label
-    caches, qkv, m = build(dev, B, Hq, Hkv, D, S, ctx, n_real, kv, kind, seed=B + S)
+    tm = kind.endswith("-tm")
+    caches, qkv, m = build(dev, B, Hq, Hkv, D, S, ctx, n_real, kv, kind.removesuffix("-tm"),
+                           seed=B + S, token_major=tm)
     ref, got, ca, cb = run_both(caches, qkv, m, Hq, Hkv, D, kv)
     report(f"[fused qkv] {label}: max |diff| {float((ref.float() - got.float()).abs().max()):.3g}")
     assert torch.equal(ref, got), label
