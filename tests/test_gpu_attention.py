@@ -190,20 +190,21 @@ def test_int8_path_exact_scales_at_least_as_accurate(dev):
     assert ea <= eb * 1.05 + 1e-6 and ea <= TOL_INT8
 
 
-def test_int8_scale_layouts_agree(dev):
+@pytest.mark.parametrize("D", [128, 64])
+def test_int8_scale_layouts_agree(dev, D):
     """Scale caches with adjacent tokens (allocate_kv_cache's head-major storage, one vector
     load per four keys) and token-major contiguous scales (per-key loads) give identical
     outputs."""
     rng = np.random.default_rng(11)
     ctx = rng.integers(1, 2500, 6)
-    pool = Pool(ctx, [4] * 6, 32, 8, 128, dev, "int8", seed=11, outlier=0.01)
+    pool = Pool(ctx, [4] * 6, 32, 8, D, dev, "int8", seed=11, outlier=0.01)
     assert pool.ks.stride(1) == 1
     a = pool.run()
     ks, vs = pool.ks.contiguous(), pool.vs.contiguous()
     assert ks.stride(1) != 1
     b = M.flash_attn_varlen_func(q=pool.q, k=pool.kc, v=pool.vc, cu_seqlens_q=pool.cu,
                                  max_seqlen_q=4, seqused_k=pool.seq_lens,
-                                 max_seqlen_k=int(pool.seq_lens.max()), softmax_scale=128 ** -0.5,
+                                 max_seqlen_k=int(pool.seq_lens.max()), softmax_scale=D ** -0.5,
                                  block_table=pool.table, k_scale=ks, v_scale=vs)
     assert torch.equal(a, b)
 
@@ -331,6 +332,14 @@ RAGGED = [
     ("32 sequences (one round)", _ragged(_r, 32, 512, 4096), [5] * 32, 128, "auto"),
     ("6 sequences, 64 rows", [3000, 40, 900, 6000, 10, 2500], [16] * 6, 128, "auto"),
     ("65 sequences (grid order)", _ragged(_r, 65, 16, 3000), [5] * 65, 128, "int8"),
+    # every row-tile count at head_dim 64 (20, 36 and 64 rows), and 64 INT8 rows at 128
+    ("20, head dim 64, 5 rows", _ragged(_r, 20, 0, 3000), [5] * 20, 64, "auto"),
+    ("20, head dim 64, 5 rows, int8", _ragged(_r, 20, 0, 3000), [5] * 20, 64, "int8"),
+    ("16, head dim 64, gamma 8", _ragged(_r, 16, 1, 4000), [9] * 16, 64, "auto"),
+    ("16, head dim 64, gamma 8, int8", _ragged(_r, 16, 1, 4000), [9] * 16, 64, "int8"),
+    ("6, head dim 64, 64 rows", [2000, 33, 700, 5000, 3, 1500], [16] * 6, 64, "auto"),
+    ("6, head dim 64, 64 rows, int8", [2000, 33, 700, 5000, 3, 1500], [16] * 6, 64, "int8"),
+    ("6 sequences, 64 rows, int8", [1200, 5, 4000, 640, 2900, 77], [16] * 6, 128, "int8"),
 ]
 
 
