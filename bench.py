@@ -436,6 +436,31 @@ def kv_swap_all_case(torch, M, dev, seed, tokens=4096, layers=32, bits=8):
                 *time_launches(torch, dev, fn))
 
 
+def kv_swap_in_all_case(torch, M, dev, seed, tokens=4096, layers=32, bits=8):
+    """Swap codec back, one launch: dequantise a `tokens`-token sequence's INT8 swap rows of
+    all `layers` layers' K and V and scatter them into the bf16 caches' blocks (head-major
+    storage, blocks a seeded permutation of the pool)."""
+    import numpy as np
+
+    NB, bs, Hkv, D = 2 * tokens // 16, 16, 8, 128
+    g = torch.Generator(device=dev).manual_seed(seed)
+    caches = []
+    for _ in range(2 * layers):
+        c, _, _, _ = M.allocate_kv_cache(NB, bs, Hkv, D, "auto", device=dev)
+        c.copy_(torch.randn(c.shape, generator=g, device=dev).to(torch.bfloat16))
+        caches.append(c)
+    nb = tokens // bs
+    blocks = torch.from_numpy(np.random.default_rng(seed).permutation(NB)[:nb].astype(np.int64)).to(dev)
+    q, sc = M.swap_out_caches(caches, blocks, bits)
+
+    def fn():
+        M.swap_in_caches(q, sc, bits, blocks, caches)
+
+    nbytes = 2 * layers * (nb * bs * Hkv * (D * 2 + D * bits // 8 + 2)) + nb * 8
+    return rate({"tokens": tokens, "layers": layers, "caches": 2 * layers, "bits": bits}, nbytes,
+                *time_launches(torch, dev, fn))
+
+
 def kv_tier_case(torch, M, dev, seed, tokens=4096, layers=32):
     """KVTierManager swap_out + swap_in of one `tokens`-token sequence of a Llama-3.1-8B-shaped
     target (32 layers, bf16 caches, INT8 tier): codec launches plus the PCIe copies to and from
@@ -579,6 +604,7 @@ KERNEL_CASES = {
     "kv_write_t65536": lambda t, M, d, s: kv_write_case(t, M, d, 65536, s),
     "kv_swap_out_4096tok": lambda t, M, d, s: kv_swap_case(t, M, d, s),
     "kv_swap_out_4096tok_32layers": lambda t, M, d, s: kv_swap_all_case(t, M, d, s),
+    "kv_swap_in_4096tok_32layers": lambda t, M, d, s: kv_swap_in_all_case(t, M, d, s),
     "kv_tier_roundtrip": lambda t, M, d, s: kv_tier_case(t, M, d, s),
     "kv_migrate_256x2MiB": lambda t, M, d, s: migrate_case(t, M, d, s),
     # the step's weight-streaming projections, tile-packed as in the step: target qkv / down

@@ -26,14 +26,19 @@ __global__ __launch_bounds__(256) void kv_write_kernel(
   // Groups are aligned inside the wave, so a whole group leaves together.
   if (t >= T) return;
   const int h = blockIdx.y;
+  // The K and V chunks load with the slot (none depends on another); the empty asm takes all
+  // three, so the compiler neither sinks the K / V loads past the slot test nor waits for the
+  // slot before issuing them: one memory round trip instead of two.
+  const uint4 kr = *reinterpret_cast<const uint4*>(k + t * k_ts + h * k_hs + c * 8);
+  const uint4 vr = *reinterpret_cast<const uint4*>(v + t * v_ts + h * v_hs + c * 8);
   const int64_t slot = slot_mapping[t];
+  asm volatile("" ::"v"(kr.x), "v"(kr.y), "v"(kr.z), "v"(kr.w), "v"(vr.x), "v"(vr.y), "v"(vr.z),
+               "v"(vr.w), "v"(slot));
   if (slot < 0 || slot >= num_slots) return;
   // power-of-two block sizes (bs_shift >= 0) take a shift and a mask
   const int64_t blk = bs_shift >= 0 ? slot >> bs_shift : slot / block_size;
   const int64_t off = bs_shift >= 0 ? slot & ((int64_t{1} << bs_shift) - 1) : slot % block_size;
 
-  const uint4 kr = *reinterpret_cast<const uint4*>(k + t * k_ts + h * k_hs + c * 8);
-  const uint4 vr = *reinterpret_cast<const uint4*>(v + t * v_ts + h * v_hs + c * 8);
   const int64_t c_off = blk * c_bs + off * c_ts + h * c_hs + c * 8;
   store_kv_chunk<G, INT8>(kr, vr, kc, vc, c_off, ks, vs, blk * s_bs + off * s_ts + h * s_hs, c);
 }
@@ -277,46 +282,101 @@ struct CacheSet {
   uint16_t* s[kMaxSwapCaches];  // INT8 caches: their fp16 scale caches
 };
 
-template <int G, int BITS, bool SRC8>
-__global__ __launch_bounds__(256) void swap_out_kernel(
+// One workgroup moves one slab of U * kSwapThreads chunks (of 8 elements) of one swapped
+// block for one cache: a thread takes U chunks, kSwapThreads apart, and issues every load
+// before it uses the first, so it keeps U loads in flight rather than one (one 16-byte load
+// per thread left the stream at about half the HBM rate).  U = 4 for swap_out and 2 for
+// swap_in measured best (32 layers' K and V of a 4096-token sequence: 250 -> 190 us and
+// 224 -> 145 us; 8 was slower at both, and 4 left one layer's swap_out 0.4 us slower than
+// one chunk per thread, which launches too small to fill the GPU therefore keep).
+// Nothing in a slab branches: a load under a branch is waited for where the branch joins,
+// and the compiler sinks a load into the branch of its only store.  So a chunk index past
+// the block stands for the same chunk of the block's first vector (its G-lane group stays
+// whole) and that lane stores the same bytes as the lane that owns the chunk, and every lane
+// of a vector stores its (identical) scale.
+// Chunk idx of a block is (token t, head h, chunk c) with idx = (t * Hkv + h) * G + c, the
+// order of the swapped rows, so the swapped side is read or written contiguously.
+constexpr int kSwapThreads = 256;
+constexpr int kSwapOutU = 4;
+constexpr int kSwapInU = 2;
+constexpr int64_t kSwapSmallGrid = 2048;
+
+template <int N>
+struct SwapVec;  // the register type of N bytes
+template <>
+struct SwapVec<16> { using T = uint4; };
+template <>
+struct SwapVec<8> { using T = uint2; };
+template <>
+struct SwapVec<4> { using T = uint32_t; };
+
+// The chunk of round u of this thread in the slab that starts at chunk `base` of its block.
+template <int G>
+__device__ __forceinline__ int swap_chunk(int base, int u, int nchunk) {
+  const int idx = base + u * kSwapThreads + static_cast<int>(threadIdx.x);
+  return idx < nchunk ? idx : idx % G;
+}
+
+template <int G, int BITS, bool SRC8, int U = kSwapOutU>
+__global__ __launch_bounds__(kSwapThreads) void swap_out_kernel(
     CacheSet cs, int64_t c_bs, int64_t c_ts, int64_t c_hs, int64_t s_bs, int64_t s_ts, int64_t s_hs,
-    const int64_t* __restrict__ ids, int nid, int bs, int Hkv, int64_t num_blocks,
+    const int64_t* __restrict__ ids, int slabs, int bs, int Hkv, int64_t num_blocks,
     unsigned char* __restrict__ q, uint16_t* __restrict__ scale, int64_t q_stride,
     int64_t s_stride) {
   const void* __restrict__ cache = cs.c[blockIdx.y];
   const uint16_t* __restrict__ cscale = cs.s[blockIdx.y];
-  q += blockIdx.y * q_stride;
-  scale += blockIdx.y * s_stride;
-  constexpr int D = G * 8;
   constexpr int kOut = SwapElt<BITS>::kBytes;
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int c = static_cast<int>(gid % G);
-  const int64_t vec = gid / G;
-  if (vec >= static_cast<int64_t>(nid) * bs * Hkv) return;  // whole groups leave together
+  using In = typename SwapVec<SRC8 ? 8 : 16>::T;
+  const int i = static_cast<int>(blockIdx.x) / slabs;
+  const int base = (static_cast<int>(blockIdx.x) - i * slabs) * (U * kSwapThreads);
   const int per_blk = bs * Hkv;
-  const int i = static_cast<int>(vec / per_blk);
-  const int rem = static_cast<int>(vec % per_blk);
-  const int t = rem / Hkv, h = rem % Hkv;
+  const int nchunk = per_blk * G;
+  const int64_t vec0 = static_cast<int64_t>(i) * per_blk;
+  q += blockIdx.y * q_stride + vec0 * G * kOut;
+  scale += blockIdx.y * s_stride + vec0;
   const int64_t blk = ids[i];
-  unsigned char* qo = q + vec * (D / 8) * kOut + c * kOut;
-  if (blk < 0 || blk >= num_blocks) {
-    if constexpr (kOut == 16) *reinterpret_cast<uint4*>(qo) = make_uint4(0, 0, 0, 0);
-    else if constexpr (kOut == 8) *reinterpret_cast<uint2*>(qo) = make_uint2(0, 0);
-    else *reinterpret_cast<uint32_t*>(qo) = 0;
-    if (BITS != 16 && c == 0) scale[vec] = 0;
+  if (blk < 0 || blk >= num_blocks) {  // uniform: the block's rows read as zeros
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int idx = swap_chunk<G>(base, u, nchunk);
+      unsigned char* qo = q + static_cast<int64_t>(idx) * kOut;
+      if constexpr (kOut == 16) *reinterpret_cast<uint4*>(qo) = make_uint4(0, 0, 0, 0);
+      else if constexpr (kOut == 8) *reinterpret_cast<uint2*>(qo) = make_uint2(0, 0);
+      else *reinterpret_cast<uint32_t*>(qo) = 0;
+      if (BITS != 16) scale[idx / G] = 0;
+    }
     return;
   }
-  const int64_t off = blk * c_bs + t * c_ts + h * c_hs + c * 8;
-  if constexpr (SRC8) {
-    *reinterpret_cast<uint2*>(qo) = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(cache) + off);
-    if (c == 0) scale[vec] = cscale[blk * s_bs + t * s_ts + h * s_hs];
-  } else {
-    const uint4 x = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(cache) + off);
-    if constexpr (BITS == 16) {
-      *reinterpret_cast<uint4*>(qo) = x;
+  In x[U];
+  uint16_t xs[U];  // an INT8 cache: the vector's scale
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int idx = swap_chunk<G>(base, u, nchunk);
+    const int v = idx / G, c = idx % G;
+    const int t = v / Hkv, h = v - t * Hkv;
+    const int64_t off = blk * c_bs + t * c_ts + h * c_hs + c * 8;
+    if constexpr (SRC8) {
+      x[u] = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(cache) + off);
+      xs[u] = cscale[blk * s_bs + t * s_ts + h * s_hs];
+    } else {
+      x[u] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(cache) + off);
+    }
+  }
+  // keeps the scheduler from moving each load down to its store (the copying forms have no
+  // other work between them)
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int idx = swap_chunk<G>(base, u, nchunk);
+    unsigned char* qo = q + static_cast<int64_t>(idx) * kOut;
+    if constexpr (SRC8) {
+      *reinterpret_cast<uint2*>(qo) = make_uint2(x[u].x, x[u].y);
+      scale[idx / G] = xs[u];
+    } else if constexpr (BITS == 16) {
+      *reinterpret_cast<uint4*>(qo) = make_uint4(x[u].x, x[u].y, x[u].z, x[u].w);
     } else {
       constexpr int QMAX = BITS == 8 ? 127 : 7;
-      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+      const uint32_t w[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
       uint32_t amax = 0;
 #pragma unroll
       for (int e = 0; e < 4; ++e) amax = max(amax, max(w[e] & 0x7fffu, (w[e] >> 16) & 0x7fffu));
@@ -336,63 +396,74 @@ __global__ __launch_bounds__(256) void swap_out_kernel(
           b |= ((static_cast<uint32_t>(code[2 * j] + 8) | (static_cast<uint32_t>(code[2 * j + 1] + 8) << 4)) & 0xffu) << (8 * j);
         *reinterpret_cast<uint32_t*>(qo) = b;
       }
-      if (c == 0) scale[vec] = f32_to_f16(s32);
+      scale[idx / G] = f32_to_f16(s32);
     }
   }
 }
 
-template <int G, int BITS, bool DST8>
-__global__ __launch_bounds__(256) void swap_in_kernel(
+template <int G, int BITS, bool DST8, int U = kSwapInU>
+__global__ __launch_bounds__(kSwapThreads) void swap_in_kernel(
     const unsigned char* __restrict__ q, const uint16_t* __restrict__ scale, int64_t q_stride,
-    int64_t s_stride, const int64_t* __restrict__ ids, int nid, int bs, int Hkv,
+    int64_t s_stride, const int64_t* __restrict__ ids, int slabs, int bs, int Hkv,
     int64_t num_blocks, CacheSet cs, int64_t c_bs, int64_t c_ts, int64_t c_hs, int64_t s_bs,
     int64_t s_ts, int64_t s_hs) {
   void* __restrict__ cache = const_cast<void*>(cs.c[blockIdx.y]);
   uint16_t* __restrict__ cscale = cs.s[blockIdx.y];
-  q += blockIdx.y * q_stride;
-  scale += blockIdx.y * s_stride;
-  constexpr int D = G * 8;
   constexpr int kIn = SwapElt<BITS>::kBytes;
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int c = static_cast<int>(gid % G);
-  const int64_t vec = gid / G;
-  if (vec >= static_cast<int64_t>(nid) * bs * Hkv) return;
+  using In = typename SwapVec<kIn>::T;
+  const int i = static_cast<int>(blockIdx.x) / slabs;
+  const int base = (static_cast<int>(blockIdx.x) - i * slabs) * (U * kSwapThreads);
   const int per_blk = bs * Hkv;
-  const int i = static_cast<int>(vec / per_blk);
-  const int rem = static_cast<int>(vec % per_blk);
-  const int t = rem / Hkv, h = rem % Hkv;
+  const int nchunk = per_blk * G;
   const int64_t blk = ids[i];
-  if (blk < 0 || blk >= num_blocks) return;
-  const unsigned char* qi = q + vec * (D / 8) * kIn + c * kIn;
-  const int64_t off = blk * c_bs + t * c_ts + h * c_hs + c * 8;
-  if constexpr (DST8) {
-    *reinterpret_cast<uint2*>(static_cast<int8_t*>(cache) + off) = *reinterpret_cast<const uint2*>(qi);
-    if (c == 0) cscale[blk * s_bs + t * s_ts + h * s_hs] = scale[vec];
-  } else if constexpr (BITS == 16) {
-    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(cache) + off) = *reinterpret_cast<const uint4*>(qi);
-  } else {
-    const float s = f16_to_f32(scale[vec]);
-    int code[8];
-    if constexpr (BITS == 8) {
-      const uint2 r = *reinterpret_cast<const uint2*>(qi);
-      const uint32_t b[2] = {r.x, r.y};
+  if (blk < 0 || blk >= num_blocks) return;  // uniform: skipped
+  const int64_t vec0 = static_cast<int64_t>(i) * per_blk;
+  q += blockIdx.y * q_stride + vec0 * G * kIn;
+  scale += blockIdx.y * s_stride + vec0;
+  In r[U];
+  uint16_t sv[U];  // the vector's scale
 #pragma unroll
-      for (int e = 0; e < 8; ++e) code[e] = static_cast<int8_t>((b[e / 4] >> (8 * (e & 3))) & 0xffu);
+  for (int u = 0; u < U; ++u) {
+    const int idx = swap_chunk<G>(base, u, nchunk);
+    r[u] = *reinterpret_cast<const In*>(q + static_cast<int64_t>(idx) * kIn);
+    sv[u] = BITS != 16 ? scale[idx / G] : 0;
+  }
+  __builtin_amdgcn_sched_barrier(0);  // as in swap_out_kernel
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int idx = swap_chunk<G>(base, u, nchunk);
+    const int v = idx / G, c = idx % G;
+    const int t = v / Hkv, h = v - t * Hkv;
+    const int64_t off = blk * c_bs + t * c_ts + h * c_hs + c * 8;
+    if constexpr (DST8) {
+      *reinterpret_cast<uint2*>(static_cast<int8_t*>(cache) + off) = make_uint2(r[u].x, r[u].y);
+      cscale[blk * s_bs + t * s_ts + h * s_hs] = sv[u];
+    } else if constexpr (BITS == 16) {
+      *reinterpret_cast<uint4*>(static_cast<uint16_t*>(cache) + off) =
+          make_uint4(r[u].x, r[u].y, r[u].z, r[u].w);
     } else {
-      const uint32_t b = *reinterpret_cast<const uint32_t*>(qi);
+      const float sc = f16_to_f32(sv[u]);
+      int code[8];
+      if constexpr (BITS == 8) {
+        const uint32_t b[2] = {r[u].x, r[u].y};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t byte = (b >> (8 * j)) & 0xffu;
-        code[2 * j] = static_cast<int>(byte & 0x0fu) - 8;
-        code[2 * j + 1] = static_cast<int>(byte >> 4) - 8;
+        for (int e = 0; e < 8; ++e) code[e] = static_cast<int8_t>((b[e / 4] >> (8 * (e & 3))) & 0xffu);
+      } else {
+        const uint32_t b = r[u];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t byte = (b >> (8 * j)) & 0xffu;
+          code[2 * j] = static_cast<int>(byte & 0x0fu) - 8;
+          code[2 * j + 1] = static_cast<int>(byte >> 4) - 8;
+        }
       }
-    }
-    uint32_t o[4];
+      uint32_t o[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e)  // dtype(float(code) * float(scale)); the product is exact
-      o[e] = f32_to_bf16(static_cast<float>(code[2 * e]) * s) |
-             (static_cast<uint32_t>(f32_to_bf16(static_cast<float>(code[2 * e + 1]) * s)) << 16);
-    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(cache) + off) = make_uint4(o[0], o[1], o[2], o[3]);
+      for (int e = 0; e < 4; ++e)  // dtype(float(code) * float(scale)); the product is exact
+        o[e] = f32_to_bf16(static_cast<float>(code[2 * e]) * sc) |
+               (static_cast<uint32_t>(f32_to_bf16(static_cast<float>(code[2 * e + 1]) * sc)) << 16);
+      *reinterpret_cast<uint4*>(static_cast<uint16_t*>(cache) + off) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
   }
 }
 
@@ -401,20 +472,36 @@ int launch_swap(bool out, int G, const CacheSet& cs, int n, int64_t c_bs, int64_
                 int64_t s_bs, int64_t s_ts, int64_t s_hs, const int64_t* ids, int nid,
                 int bs, int Hkv, int64_t num_blocks, void* q, void* scale, int64_t q_stride,
                 int64_t s_stride, hipStream_t stream) {
-  const int64_t threads = static_cast<int64_t>(nid) * bs * Hkv * G;
-  const dim3 grid(static_cast<unsigned>((threads + 255) / 256), static_cast<unsigned>(n));
-#define COOPT_SW(GV)                                                                              \
-  case GV:                                                                                        \
-    if (out)                                                                                      \
-      hipLaunchKernelGGL((swap_out_kernel<GV, BITS, I8>), grid, dim3(256), 0, stream, cs, c_bs,   \
-                         c_ts, c_hs, s_bs, s_ts, s_hs, ids, nid, bs, Hkv, num_blocks,             \
-                         static_cast<unsigned char*>(q), static_cast<uint16_t*>(scale), q_stride, \
-                         s_stride);                                                               \
-    else                                                                                          \
-      hipLaunchKernelGGL((swap_in_kernel<GV, BITS, I8>), grid, dim3(256), 0, stream,             \
-                         static_cast<const unsigned char*>(q), static_cast<const uint16_t*>(scale), \
-                         q_stride, s_stride, ids, nid, bs, Hkv, num_blocks, cs, c_bs, c_ts, c_hs, \
-                         s_bs, s_ts, s_hs);                                                       \
+  if (nid == 0 || n == 0) return COOPT_OK;
+  const int64_t chunks = static_cast<int64_t>(bs) * Hkv * G;  // of one block
+  // U chunks per thread (section above); a launch that would then fill fewer than
+  // kSwapSmallGrid workgroups (one layer of a short sequence) takes one chunk per thread, as
+  // its time is latency, not bandwidth
+  int U = out ? kSwapOutU : kSwapInU;
+  if (nid * ((chunks + U * kSwapThreads - 1) / (U * kSwapThreads)) * n < kSwapSmallGrid) U = 1;
+  const int64_t slabs = (chunks + U * kSwapThreads - 1) / (U * kSwapThreads);
+  COOPT_REQUIRE(chunks <= INT32_MAX && static_cast<int64_t>(nid) * slabs <= INT32_MAX,
+                "swap too large for one launch");
+  const dim3 grid(static_cast<unsigned>(nid * slabs), static_cast<unsigned>(n));
+  const int sl = static_cast<int>(slabs);
+#define COOPT_SW_U(GV, UO, UI)                                                                    \
+  if (out)                                                                                        \
+    hipLaunchKernelGGL((swap_out_kernel<GV, BITS, I8, UO>), grid, dim3(kSwapThreads), 0, stream,  \
+                       cs, c_bs, c_ts, c_hs, s_bs, s_ts, s_hs, ids, sl, bs, Hkv, num_blocks,      \
+                       static_cast<unsigned char*>(q), static_cast<uint16_t*>(scale), q_stride,   \
+                       s_stride);                                                                 \
+  else                                                                                            \
+    hipLaunchKernelGGL((swap_in_kernel<GV, BITS, I8, UI>), grid, dim3(kSwapThreads), 0, stream,   \
+                       static_cast<const unsigned char*>(q), static_cast<const uint16_t*>(scale), \
+                       q_stride, s_stride, ids, sl, bs, Hkv, num_blocks, cs, c_bs, c_ts, c_hs,    \
+                       s_bs, s_ts, s_hs);
+#define COOPT_SW(GV)                                  \
+  case GV:                                            \
+    if (U == 1) {                                     \
+      COOPT_SW_U(GV, 1, 1)                            \
+    } else {                                          \
+      COOPT_SW_U(GV, kSwapOutU, kSwapInU)             \
+    }                                                 \
     break;
   switch (G) {
     COOPT_SW(1)
@@ -427,6 +514,7 @@ int launch_swap(bool out, int G, const CacheSet& cs, int n, int64_t c_bs, int64_
     default:
       return COOPT_EINVAL;
   }
+#undef COOPT_SW_U
 #undef COOPT_SW
   return coopt::check_launch(out ? "coopt_kv_swap_out" : "coopt_kv_swap_in");
 }

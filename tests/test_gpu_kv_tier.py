@@ -214,3 +214,59 @@ def test_multi_cache_swap_falls_back_on_mixed_layouts(dev):
     for i, c in enumerate((a, b)):
         qi, si = M.swap_out_blocks(c, ids, 8)
         assert torch.equal(q[i], qi) and torch.equal(s[i], si)
+
+
+@pytest.mark.parametrize("kv,bits", [("auto", 16), ("auto", 8), ("auto", 4), ("int8", 8)])
+@pytest.mark.parametrize("H,D", [(8, 128), (4, 64), (3, 128)])
+def test_wide_swap_matches_reference_lines(dev, kv, bits, H, D):
+    """A swap wide enough for the several-chunks-per-thread kernels (64 caches x 40 ids; one
+    cache alone takes the one-chunk form): codes and scales equal to the reference lines and
+    to per-cache calls; restored caches equal to dequantize and to per-cache restores.  The
+    (4, 64) and (3, 128) geometries leave lanes past a block's end, which must not write."""
+    NB, BS, n = 48, 16, 64
+    rng = np.random.default_rng(H * D + bits)
+    ids_np = rng.permutation(NB)[:40].astype(np.int64)
+    ids_np[[3, 17]] = [-1, NB + 5]          # out of the pool: zeros out, skipped in
+    ids = torch.from_numpy(ids_np).to(dev)
+    valid = torch.from_numpy((ids_np >= 0) & (ids_np < NB)).to(dev)
+    caches, scales = [], []
+    for i in range(n):
+        kc, _, ks, _ = M.allocate_kv_cache(NB, BS, H, D, kv, device=dev)
+        x = kv_values((NB * BS, H, D), dev, seed=300 + i)
+        M.reshape_and_cache_flash(x, x, kc, kc.clone(), torch.arange(NB * BS, device=dev), kv, ks,
+                                  None if ks is None else ks.clone())
+        caches.append(kc)
+        scales.append(ks)
+    q, s = M.swap_out_caches(caches, ids, bits, scales)
+    vid = ids[valid]
+    for i in (0, 1, 31, 63):
+        if kv == "int8":
+            rq, rs = caches[i][vid], scales[i][vid]          # INT8 caches move as they are
+        else:
+            rq, rs = ref_quantize(caches[i][vid], bits)
+        assert torch.equal(q[i][valid].view(rq.dtype), rq), i
+        assert bool((q[i][~valid].view(torch.uint8) == 0).all()), i
+        if rs is not None:
+            assert torch.equal(s[i][valid], rs), i
+            assert bool((s[i][~valid] == 0).all()), i
+        qi, si = M.swap_out_blocks(caches[i], ids, bits, scales[i])
+        assert torch.equal(q[i], qi), i
+        if si is not None:
+            assert torch.equal(s[i], si), i
+    # restore into fresh caches: the swapped rows dequantised, every other block untouched
+    fresh = [M.allocate_kv_cache(NB, BS, H, D, kv, device=dev) for _ in range(n)]
+    tgt, tsc = [f[0] for f in fresh], [f[2] for f in fresh]
+    M.swap_in_caches(q, s, bits, ids, tgt, tsc)
+    for i in (0, 1, 31, 63):
+        want = torch.zeros_like(tgt[i])
+        if kv == "int8":
+            want[vid] = caches[i][vid]
+            want_s = torch.zeros_like(tsc[i])
+            want_s[vid] = scales[i][vid]
+            assert torch.equal(tsc[i], want_s), i
+        else:
+            want[vid] = ref_dequantize(q[i][valid], None if s is None else s[i][valid], bits)
+        assert torch.equal(tgt[i].view(torch.uint8), want.view(torch.uint8)), i
+        one, _, one_s, _ = M.allocate_kv_cache(NB, BS, H, D, kv, device=dev)
+        M.swap_in_blocks(q[i], None if s is None else s[i], bits, ids, one, one_s)
+        assert torch.equal(tgt[i].view(torch.uint8), one.view(torch.uint8)), i
