@@ -461,6 +461,22 @@ def kv_swap_in_all_case(torch, M, dev, seed, tokens=4096, layers=32, bits=8):
                 *time_launches(torch, dev, fn))
 
 
+def codec_case(torch, M, dev, seed, direction, rows=262144, D=128, bits=8):
+    """The standalone codec (kv_tier_manager.quantize / dequantize): bf16 [rows, D] <-> INT8
+    codes + fp16 scales per row; rows = 32768 tokens x 8 heads (64 MiB of bf16)."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    x = torch.randn(rows, D, generator=g, device=dev).to(torch.bfloat16)
+    q, sc = M.quantize(x, bits)
+    if direction == "quantize":
+        def fn():
+            M.quantize(x, bits)
+    else:
+        def fn():
+            M.dequantize(q, sc, bits, torch.bfloat16)
+    nbytes = rows * (D * 2 + D * bits // 8 + 2)
+    return rate({"rows": rows, "D": D, "bits": bits}, nbytes, *time_launches(torch, dev, fn))
+
+
 def kv_tier_case(torch, M, dev, seed, tokens=4096, layers=32):
     """KVTierManager swap_out + swap_in of one `tokens`-token sequence of a Llama-3.1-8B-shaped
     target (32 layers, bf16 caches, INT8 tier): codec launches plus the PCIe copies to and from
@@ -606,6 +622,8 @@ KERNEL_CASES = {
     "kv_swap_out_4096tok_32layers": lambda t, M, d, s: kv_swap_all_case(t, M, d, s),
     "kv_swap_in_4096tok_32layers": lambda t, M, d, s: kv_swap_in_all_case(t, M, d, s),
     "kv_tier_roundtrip": lambda t, M, d, s: kv_tier_case(t, M, d, s),
+    "codec_quantize_64MiB": lambda t, M, d, s: codec_case(t, M, d, s, "quantize"),
+    "codec_dequantize_64MiB": lambda t, M, d, s: codec_case(t, M, d, s, "dequantize"),
     "kv_migrate_256x2MiB": lambda t, M, d, s: migrate_case(t, M, d, s),
     # the step's weight-streaming projections, tile-packed as in the step: target qkv / down
     # at the verify rows (B (gamma+1) = 160), draft lm_head at the draft rows (B = 32)

@@ -317,6 +317,61 @@ __device__ __forceinline__ int swap_chunk(int base, int u, int nchunk) {
   return idx < nchunk ? idx : idx % G;
 }
 
+// The swapped form of one 8-element bf16 chunk (words w, element 2i in the low half of w[i])
+// of a G-lane group's vector: kv_tier_manager.quantize per vector (engine/kv_tier_manager.py:
+// 21-31) -- INT8 codes in lo / hi, or INT4 nibbles (even element low, +8 offset) in lo --
+// and the vector's fp16 scale.  Every lane of the group must call it together.
+struct QuantChunk {
+  uint32_t lo, hi;
+  uint16_t scale;
+};
+template <int G, int BITS>
+__device__ __forceinline__ QuantChunk quant_chunk(const uint32_t (&w)[4]) {
+  constexpr int QMAX = BITS == 8 ? 127 : 7;
+  uint32_t amax = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) amax = max(amax, max(w[e] & 0x7fffu, (w[e] >> 16) & 0x7fffu));
+  amax = group_max_u32<G>(amax);
+  const float s32 = quant_scale<QMAX>(bf16_to_f32(static_cast<uint16_t>(amax)));
+  int code[8];
+  quant_codes8<QMAX>(w, s32, code);
+  QuantChunk r{0, 0, f32_to_f16(s32)};
+  if constexpr (BITS == 8) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) (e < 4 ? r.lo : r.hi) |= (static_cast<uint32_t>(code[e]) & 0xffu) << (8 * (e & 3));
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      r.lo |= ((static_cast<uint32_t>(code[2 * j] + 8) | (static_cast<uint32_t>(code[2 * j + 1] + 8) << 4)) & 0xffu) << (8 * j);
+  }
+  return r;
+}
+
+// bf16(float(code) * float(scale)) of one chunk's 8 codes (INT8 in lo / hi, or INT4 nibbles
+// in lo): dequantize, engine/kv_tier_manager.py:34-41.  The product is exact.
+template <int BITS>
+__device__ __forceinline__ uint4 dequant_chunk(uint32_t lo, uint32_t hi, uint16_t scale16) {
+  const float sc = f16_to_f32(scale16);
+  int code[8];
+  if constexpr (BITS == 8) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) code[e] = static_cast<int8_t>(((e < 4 ? lo : hi) >> (8 * (e & 3))) & 0xffu);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t byte = (lo >> (8 * j)) & 0xffu;
+      code[2 * j] = static_cast<int>(byte & 0x0fu) - 8;
+      code[2 * j + 1] = static_cast<int>(byte >> 4) - 8;
+    }
+  }
+  uint32_t o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    o[e] = f32_to_bf16(static_cast<float>(code[2 * e]) * sc) |
+           (static_cast<uint32_t>(f32_to_bf16(static_cast<float>(code[2 * e + 1]) * sc)) << 16);
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 template <int G, int BITS, bool SRC8, int U = kSwapOutU>
 __global__ __launch_bounds__(kSwapThreads) void swap_out_kernel(
     CacheSet cs, int64_t c_bs, int64_t c_ts, int64_t c_hs, int64_t s_bs, int64_t s_ts, int64_t s_hs,
@@ -375,28 +430,11 @@ __global__ __launch_bounds__(kSwapThreads) void swap_out_kernel(
     } else if constexpr (BITS == 16) {
       *reinterpret_cast<uint4*>(qo) = make_uint4(x[u].x, x[u].y, x[u].z, x[u].w);
     } else {
-      constexpr int QMAX = BITS == 8 ? 127 : 7;
       const uint32_t w[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
-      uint32_t amax = 0;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) amax = max(amax, max(w[e] & 0x7fffu, (w[e] >> 16) & 0x7fffu));
-      amax = group_max_u32<G>(amax);
-      const float s32 = quant_scale<QMAX>(bf16_to_f32(static_cast<uint16_t>(amax)));
-      int code[8];
-      quant_codes8<QMAX>(w, s32, code);
-      if constexpr (BITS == 8) {
-        uint32_t b[2] = {0, 0};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) b[e / 4] |= (static_cast<uint32_t>(code[e]) & 0xffu) << (8 * (e & 3));
-        *reinterpret_cast<uint2*>(qo) = make_uint2(b[0], b[1]);
-      } else {  // even element in the low nibble, odd in the high one, both offset by +8
-        uint32_t b = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          b |= ((static_cast<uint32_t>(code[2 * j] + 8) | (static_cast<uint32_t>(code[2 * j + 1] + 8) << 4)) & 0xffu) << (8 * j);
-        *reinterpret_cast<uint32_t*>(qo) = b;
-      }
-      scale[idx / G] = f32_to_f16(s32);
+      const QuantChunk r = quant_chunk<G, BITS>(w);
+      if constexpr (BITS == 8) *reinterpret_cast<uint2*>(qo) = make_uint2(r.lo, r.hi);
+      else *reinterpret_cast<uint32_t*>(qo) = r.lo;
+      scale[idx / G] = r.scale;
     }
   }
 }
@@ -442,29 +480,117 @@ __global__ __launch_bounds__(kSwapThreads) void swap_in_kernel(
       *reinterpret_cast<uint4*>(static_cast<uint16_t*>(cache) + off) =
           make_uint4(r[u].x, r[u].y, r[u].z, r[u].w);
     } else {
-      const float sc = f16_to_f32(sv[u]);
-      int code[8];
-      if constexpr (BITS == 8) {
-        const uint32_t b[2] = {r[u].x, r[u].y};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) code[e] = static_cast<int8_t>((b[e / 4] >> (8 * (e & 3))) & 0xffu);
-      } else {
-        const uint32_t b = r[u];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t byte = (b >> (8 * j)) & 0xffu;
-          code[2 * j] = static_cast<int>(byte & 0x0fu) - 8;
-          code[2 * j + 1] = static_cast<int>(byte >> 4) - 8;
-        }
-      }
-      uint32_t o[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e)  // dtype(float(code) * float(scale)); the product is exact
-        o[e] = f32_to_bf16(static_cast<float>(code[2 * e]) * sc) |
-               (static_cast<uint32_t>(f32_to_bf16(static_cast<float>(code[2 * e + 1]) * sc)) << 16);
-      *reinterpret_cast<uint4*>(static_cast<uint16_t*>(cache) + off) = make_uint4(o[0], o[1], o[2], o[3]);
+      uint4 o;
+      if constexpr (BITS == 8) o = dequant_chunk<8>(r[u].x, r[u].y, sv[u]);
+      else o = dequant_chunk<4>(r[u], 0, sv[u]);
+      *reinterpret_cast<uint4*>(static_cast<uint16_t*>(cache) + off) = o;
     }
   }
+}
+
+// The codec over contiguous bf16 rows of D = 8G elements, its common case: the swap kernels'
+// slab scheme over chunk idx = row * G + c (the rows form one block of nchunk chunks).
+template <int G, int BITS, int U = kSwapOutU>
+__global__ __launch_bounds__(kSwapThreads) void quantize_rows_kernel(
+    const uint16_t* __restrict__ x, int nchunk, unsigned char* __restrict__ q,
+    uint16_t* __restrict__ scale) {
+  constexpr int kOut = SwapElt<BITS>::kBytes;
+  const int base = static_cast<int>(blockIdx.x) * (U * kSwapThreads);
+  uint4 xv[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    xv[u] = *reinterpret_cast<const uint4*>(x + static_cast<int64_t>(swap_chunk<G>(base, u, nchunk)) * 8);
+  __builtin_amdgcn_sched_barrier(0);  // as in swap_out_kernel
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int idx = swap_chunk<G>(base, u, nchunk);
+    const uint32_t w[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+    const QuantChunk r = quant_chunk<G, BITS>(w);
+    unsigned char* qo = q + static_cast<int64_t>(idx) * kOut;
+    if constexpr (BITS == 8) *reinterpret_cast<uint2*>(qo) = make_uint2(r.lo, r.hi);
+    else *reinterpret_cast<uint32_t*>(qo) = r.lo;
+    scale[idx / G] = r.scale;
+  }
+}
+
+template <int G, int BITS, int U = kSwapInU>
+__global__ __launch_bounds__(kSwapThreads) void dequantize_rows_kernel(
+    const unsigned char* __restrict__ q, const uint16_t* __restrict__ scale, int nchunk,
+    uint16_t* __restrict__ out) {
+  constexpr int kIn = SwapElt<BITS>::kBytes;
+  using In = typename SwapVec<kIn>::T;
+  const int base = static_cast<int>(blockIdx.x) * (U * kSwapThreads);
+  In r[U];
+  uint16_t sv[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int idx = swap_chunk<G>(base, u, nchunk);
+    r[u] = *reinterpret_cast<const In*>(q + static_cast<int64_t>(idx) * kIn);
+    sv[u] = scale[idx / G];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int idx = swap_chunk<G>(base, u, nchunk);
+    uint4 o;
+    if constexpr (BITS == 8) o = dequant_chunk<8>(r[u].x, r[u].y, sv[u]);
+    else o = dequant_chunk<4>(r[u], 0, sv[u]);
+    *reinterpret_cast<uint4*>(out + static_cast<int64_t>(idx) * 8) = o;
+  }
+}
+
+// Launches the row codec when the call fits it (bf16 rows, D = 8G with G a power of two up to
+// 64, aligned buffers, enough chunks to fill the GPU); returns false to leave the call to the
+// general kernels.
+bool launch_rows_codec(bool quant, int bits, const void* x, int64_t rows, int D, void* q,
+                       const void* scale, hipStream_t s) {
+  const int G = D / 8;
+  if (D % 8 != 0 || G > 64 || (G & (G - 1)) != 0) return false;
+  const int U = quant ? kSwapOutU : kSwapInU;
+  const int64_t nchunk = rows * G;
+  if (nchunk > INT32_MAX - U * kSwapThreads) return false;
+  const int64_t grid = (nchunk + U * kSwapThreads - 1) / (U * kSwapThreads);
+  if (grid < kSwapSmallGrid) return false;
+  const int qal = bits == 8 ? 8 : 4;
+  if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0 || (reinterpret_cast<uintptr_t>(q) % qal) != 0 ||
+      (reinterpret_cast<uintptr_t>(scale) & 1u) != 0)
+    return false;
+  const int n = static_cast<int>(nchunk);
+#define COOPT_RC(GV)                                                                               \
+  case GV:                                                                                         \
+    if (quant) {                                                                                   \
+      if (bits == 8)                                                                               \
+        hipLaunchKernelGGL((quantize_rows_kernel<GV, 8>), dim3(grid), dim3(kSwapThreads), 0, s,     \
+                           static_cast<const uint16_t*>(x), n, static_cast<unsigned char*>(q),     \
+                           static_cast<uint16_t*>(const_cast<void*>(scale)));                      \
+      else                                                                                         \
+        hipLaunchKernelGGL((quantize_rows_kernel<GV, 4>), dim3(grid), dim3(kSwapThreads), 0, s,     \
+                           static_cast<const uint16_t*>(x), n, static_cast<unsigned char*>(q),     \
+                           static_cast<uint16_t*>(const_cast<void*>(scale)));                      \
+    } else {                                                                                       \
+      if (bits == 8)                                                                               \
+        hipLaunchKernelGGL((dequantize_rows_kernel<GV, 8>), dim3(grid), dim3(kSwapThreads), 0, s,   \
+                           static_cast<const unsigned char*>(q), static_cast<const uint16_t*>(scale), \
+                           n, static_cast<uint16_t*>(const_cast<void*>(x)));                       \
+      else                                                                                         \
+        hipLaunchKernelGGL((dequantize_rows_kernel<GV, 4>), dim3(grid), dim3(kSwapThreads), 0, s,   \
+                           static_cast<const unsigned char*>(q), static_cast<const uint16_t*>(scale), \
+                           n, static_cast<uint16_t*>(const_cast<void*>(x)));                       \
+    }                                                                                              \
+    break;
+  switch (G) {
+    COOPT_RC(1)
+    COOPT_RC(2)
+    COOPT_RC(4)
+    COOPT_RC(8)
+    COOPT_RC(16)
+    COOPT_RC(32)
+    COOPT_RC(64)
+    default:
+      return false;
+  }
+#undef COOPT_RC
+  return true;
 }
 
 template <int BITS, bool I8>
@@ -741,8 +867,10 @@ extern "C" int coopt_quantize(int bits, int in_dtype, const void* x, int64_t row
   COOPT_REQUIRE(x && q && scale, "null pointer");
   COOPT_REQUIRE((reinterpret_cast<uintptr_t>(q) & 1u) == 0 || bits == 4, "q must be 2-byte aligned");
   coopt::clear_error();
-  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
   auto s = static_cast<hipStream_t>(stream);
+  if (in_dtype == COOPT_DT_BF16 && launch_rows_codec(true, bits, x, rows, D, q, scale, s))
+    return coopt::check_launch("coopt_quantize");
+  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
   auto* qp = static_cast<uint8_t*>(q);
   auto* sp = static_cast<uint16_t*>(scale);
 #define COOPT_Q(T, B) \
@@ -772,8 +900,11 @@ extern "C" int coopt_dequantize(int bits, const void* q, const void* scale, int6
   if (rows == 0) return COOPT_OK;
   COOPT_REQUIRE(q && scale && out, "null pointer");
   coopt::clear_error();
-  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
   auto s = static_cast<hipStream_t>(stream);
+  if (out_dtype == COOPT_DT_BF16 &&
+      launch_rows_codec(false, bits, out, rows, D, const_cast<void*>(q), scale, s))
+    return coopt::check_launch("coopt_dequantize");
+  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
   const auto* qp = static_cast<const uint8_t*>(q);
   const auto* sp = static_cast<const uint16_t*>(scale);
 #define COOPT_DQ(T, B) \

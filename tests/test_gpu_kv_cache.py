@@ -199,6 +199,36 @@ def test_codec_round_trip_bit_exact(dev, bits, dtype):
         assert torch.equal(y.cpu(), ref)
 
 
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("T,H,D", [(17431, 8, 128), (23, 8, 128), (34001, 8, 64)])
+def test_codec_row_kernels_bit_exact(dev, bits, T, H, D):
+    """bf16 rows of D = 8 * 2^k elements large enough for the row codec (several chunks per
+    thread; T * H not a multiple of its slab, so lanes wrap past the end) and one too small
+    for it: codes and scales equal to the reference lines run by torch on the GPU, and
+    dequantize equal to dtype(float(code) * float(scale)); an unaligned view takes the general
+    kernels and agrees."""
+    gen = torch.Generator(device=dev).manual_seed(T + bits)
+    x = bf16_kv(gen, T, H, D, dev)
+    x[0, 0] = 0  # an all-zero vector
+    q, s = M.quantize(x, bits)
+    rq, rs = reference_quantize_on_device(x, bits)
+    assert torch.equal(q, rq) and torch.equal(s, rs)
+    y = M.dequantize(q, s, bits, torch.bfloat16)
+    if bits == 4:
+        lo = (q & 0x0F).to(torch.int8) - 8
+        hi = (q >> 4).to(torch.int8) - 8
+        codes = torch.stack((lo, hi), dim=-1).flatten(-2)
+    else:
+        codes = q
+    assert torch.equal(y, (codes.float() * s.float().unsqueeze(-1)).to(torch.bfloat16))
+    # a view 2 bytes off 16-byte alignment is refused by the row codec
+    buf = torch.empty(x.numel() + 1, dtype=torch.bfloat16, device=dev)
+    xv = buf[1:].view_as(x)
+    xv.copy_(x)
+    q2, s2 = M.quantize(xv, bits)
+    assert torch.equal(q2, q) and torch.equal(s2, s)
+
+
 def test_codec_bits16_is_passthrough(dev):
     x = torch.randn(3, 128, device=dev).to(torch.bfloat16)
     q, s = M.quantize(x, 16)
