@@ -237,6 +237,21 @@ def test_sample_and_softmax(dev):
     assert tok_g.shape == (N,) and int(tok_g.min()) >= 0 and int(tok_g.max()) < V
 
 
+@pytest.mark.parametrize("dtype,V,pad", [(torch.float32, 128256, 4), (torch.float32, 999, 0),
+                                         (torch.bfloat16, 1001, 2), (torch.bfloat16, 128256, 8),
+                                         (torch.float32, 7, 1)])
+def test_softmax_layouts(dev, dtype, V, pad):
+    """softmax(logits / T) for vector-aligned rows, rows whose length leaves a tail, and row
+    strides that rule the vector loads out: within 1e-6 relative of the fp64 softmax."""
+    gen = torch.Generator(device=dev).manual_seed(V + pad)
+    base = (torch.randn(5, V + pad, generator=gen, device=dev) * 3).to(dtype)
+    x = base[:, :V]
+    probs = M.softmax(x, 0.8)
+    ref = torch.softmax(x.double().cpu() / torch.tensor(0.8, dtype=torch.float32).double(), -1)
+    assert torch.allclose(probs.double().cpu(), ref, rtol=1e-5, atol=1e-12)
+    assert torch.allclose(probs.double().sum(-1).cpu(), torch.ones(5, dtype=torch.float64), atol=1e-5)
+
+
 def test_verify_signature_with_generator(dev):
     gen = torch.Generator(device=dev).manual_seed(10)
     V = 1000
