@@ -1008,6 +1008,82 @@ __global__ __launch_bounds__(kSmThreads) void softmax_kernel(const void* x, int6
   }
 }
 
+// Probabilities of a sampling call (gamma_max = 0) from the row statistics its row_stats
+// launch left in the workspace: grid (element chunk, row).  A block issues its logit loads,
+// then one wave combines the row's chunk partials into (M, S) (max, then sum of
+// s_c exp(m_c - M), fp64), and every element becomes fp32(exp(x/T - M) / S) by the softmax
+// kernel's formula.  Each element is read once and written once, by a grid that fills the GPU.
+constexpr int kPrThreads = 256;
+constexpr int kPrGroups = 2;  // 8-element groups per thread
+constexpr int kPrChunk = kPrThreads * 8 * kPrGroups;
+
+template <bool BF16>
+__global__ __launch_bounds__(kPrThreads) void sample_probs_kernel(Args a, float* out,
+                                                                  int64_t out_stride, int vec_ok) {
+  __shared__ float sh_m;
+  __shared__ double sh_inv;
+  const int64_t r = blockIdx.y;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lo = static_cast<int>(blockIdx.x) * kPrChunk;
+  const int V8 = vec_ok ? a.V / 8 * 8 : 0;
+  float v[kPrGroups][8];
+  if (V8 > 0) {
+#pragma unroll
+    for (int g = 0; g < kPrGroups; ++g)
+      ld8<BF16>(a.tgt, r, a.tgt_stride, min(lo + (g * kPrThreads + tid) * 8, V8 - 8), v[g]);
+  }
+  if (tid < 64) {  // wave 0: the row's (M, S), its partials read in one round
+    constexpr int kPL = 4;  // partials per lane held in registers
+    const Partial1* p = a.ws.part1 + r * a.L.nch1;
+    const int n = a.L.nch1;
+    Partial1 q[kPL];
+#pragma unroll
+    for (int k = 0; k < kPL; ++k) q[k] = p[min(tid + 64 * k, n - 1)];
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kPL; ++k) m = fmaxf(m, q[k].m);  // a repeated partial changes no max
+    for (int c = tid + 64 * kPL; c < n; c += 64) m = fmaxf(m, p[c].m);
+    m = wave_max_f32(m);
+    double s = 0.0;
+#pragma unroll
+    for (int k = 0; k < kPL; ++k)
+      if (tid + 64 * k < n && q[k].s > 0.0) s += q[k].s * exp(static_cast<double>(q[k].m) - static_cast<double>(m));
+    for (int c = tid + 64 * kPL; c < n; c += 64) {
+      const Partial1 e = p[c];
+      if (e.s > 0.0) s += e.s * exp(static_cast<double>(e.m) - static_cast<double>(m));
+    }
+    s = wave_sum_f64(s);
+    if (tid == 0) {
+      sh_m = m;
+      sh_inv = 1.0 / s;
+    }
+  }
+  __syncthreads();
+  const float m_l2 = sh_m * kLog2e;
+  const double inv_s = sh_inv;
+  float* orow = out + r * out_stride;
+  if (V8 > 0) {
+#pragma unroll
+    for (int g = 0; g < kPrGroups; ++g) {
+      const int j = lo + (g * kPrThreads + tid) * 8;
+      if (j >= V8) continue;  // the loads above were clamped, not skipped
+      float pr[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        pr[e] = static_cast<float>(static_cast<double>(exp_shift(v[g][e] * a.inv_t, m_l2)) * inv_s);
+      float4* dst = reinterpret_cast<float4*>(orow + j);
+      dst[0] = make_float4(pr[0], pr[1], pr[2], pr[3]);
+      dst[1] = make_float4(pr[4], pr[5], pr[6], pr[7]);
+    }
+  }
+  // elements past the vector part (or every element of an unaligned row)
+  const int t0 = max(lo, V8), t1 = min(lo + kPrChunk, a.V);
+  for (int j = t0 + tid; j < t1; j += kPrThreads) {
+    const float xs = ld<BF16>(a.tgt, r, a.tgt_stride, j) * a.inv_t;
+    orow[j] = static_cast<float>(static_cast<double>(exp_shift(xs, m_l2)) * inv_s);
+  }
+}
+
 template <bool BF16>
 int launch_all(Args& a, bool greedy, hipStream_t s) {
   const dim3 g1(a.L.nch1, 2 * a.gmax + 1, a.B);
@@ -1198,4 +1274,41 @@ extern "C" int coopt_softmax(int logits_dtype, const void* logits, int64_t in_st
     hipLaunchKernelGGL(softmax_kernel<false>, dim3(static_cast<unsigned>(rows)), dim3(kSmThreads), 0, s,
                        logits, in_stride, V, inv_t, probs, out_stride, vec_ok);
   return coopt::check_launch("coopt_softmax");
+}
+
+extern "C" int coopt_sample_probs(int logits_dtype, const void* logits, int64_t in_stride, int B,
+                                  int V, float temperature, const void* workspace,
+                                  size_t workspace_bytes, float* probs, int64_t out_stride,
+                                  coopt_stream_t stream) {
+  COOPT_REQUIRE(logits_dtype == COOPT_DT_F32 || logits_dtype == COOPT_DT_BF16,
+                "logits_dtype must be F32 or BF16");
+  COOPT_REQUIRE(B >= 0 && B <= 65535 && V > 0 && in_stride >= V && out_stride >= V, "bad sizes");
+  COOPT_REQUIRE(temperature > 0.0f, "temperature must be > 0");
+  if (B == 0) return COOPT_OK;
+  COOPT_REQUIRE(logits && probs && workspace, "null pointer");
+  const size_t need = coopt_accept_sample_workspace(B, 0, V);
+  if (workspace_bytes < need) {
+    coopt::set_error("coopt_sample_probs: workspace too small");
+    return COOPT_EWORKSPACE;
+  }
+  coopt::clear_error();
+  const bool bf16 = logits_dtype == COOPT_DT_BF16;
+  Args a{};
+  a.tgt = logits;
+  a.tgt_stride = in_stride;
+  a.inv_t = 1.0f / temperature;
+  a.B = B;
+  a.gmax = 0;
+  a.V = V;
+  a.L = make_layout(B, 0, V);
+  carve(&a.ws, reinterpret_cast<uintptr_t>(const_cast<void*>(workspace)), B, 0, a.L);
+  const int vec_ok = V >= 8 && coopt::aligned16(logits) && in_stride % (bf16 ? 8 : 4) == 0 &&
+                     coopt::aligned16(probs) && out_stride % 4 == 0;
+  const dim3 grid(static_cast<unsigned>((V + kPrChunk - 1) / kPrChunk), static_cast<unsigned>(B));
+  auto s = static_cast<hipStream_t>(stream);
+  if (bf16)
+    hipLaunchKernelGGL(sample_probs_kernel<true>, grid, dim3(kPrThreads), 0, s, a, probs, out_stride, vec_ok);
+  else
+    hipLaunchKernelGGL(sample_probs_kernel<false>, grid, dim3(kPrThreads), 0, s, a, probs, out_stride, vec_ok);
+  return coopt::check_launch("coopt_sample_probs");
 }

@@ -177,8 +177,20 @@ def sample(logits: torch.Tensor, temperature: float, generator=None, uniforms=No
         return res.tokens[:, 0].long(), None
     if uniforms is None:
         uniforms = torch.rand(N, generator=generator, device=x.device)
-    res = accept(x, None, empty, temperature, u_resample=uniforms)
-    probs = softmax(x, temperature) if return_probs else None
+    if not return_probs:
+        res = accept(x, None, empty, temperature, u_resample=uniforms)
+        return res.tokens[:, 0].long(), None
+    # the probabilities come from the row statistics the draw leaves in its workspace
+    lib = _lib.load()
+    V = x.shape[1]
+    need = int(lib.coopt_accept_sample_workspace(N, 0, V))
+    ws = _WS.get(need, x.device)
+    res = accept(x, None, empty, temperature, u_resample=uniforms, workspace=ws)
+    probs = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+    _lib.check(lib.coopt_sample_probs(_lib.dt_code(x.dtype), _lib.ptr(x), x.stride(0), N, V,
+                                      float(temperature), _lib.ptr(ws),
+                                      ws.numel() * ws.element_size(), _lib.ptr(probs), V,
+                                      _lib.stream_handle(x.device)), "coopt_sample_probs")
     return res.tokens[:, 0].long(), probs
 
 

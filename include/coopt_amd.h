@@ -33,6 +33,7 @@
  *   coopt_kv_copy_blocks    buf[dst].copy_(buf[src]) per    engine/elastic.py:131 via
  *                           migrated block                  engine/block_manager.py:165-187
  *   coopt_softmax           torch.softmax(logits / T)       engine/spec_decode.py:16
+ *   coopt_sample_probs      the same, for rows just sampled engine/spec_decode.py:16
  *   coopt_rms_norm          vLLM rms_norm / fused_add_rms_norm  engine/model.py:234, 236, 249, 254
  *   coopt_rope              vLLM rotary_embedding (neox)    engine/model.py:239
  *   coopt_silu_mul          vLLM silu_and_mul               engine/model.py:251-252
@@ -357,6 +358,17 @@ int coopt_accept_sample_noalloc(int logits_dtype,
  */
 int coopt_softmax(int logits_dtype, const void* logits, int64_t in_stride, int64_t rows, int V,
                   float temperature, float* probs, int64_t out_stride, coopt_stream_t stream);
+
+/*
+ * The same probabilities for the rows a sampling call just drew from (engine/spec_decode.py:
+ * 16, the probs sample() returns next to its tokens): it reads the row statistics that a
+ * preceding coopt_accept_sample with gamma_max = 0 on the same logits, B, V, temperature and
+ * workspace left there, stream-ordered before this call, so each element is read once and the
+ * rows are spread over the whole GPU.  workspace_bytes >= coopt_accept_sample_workspace(B, 0, V).
+ */
+int coopt_sample_probs(int logits_dtype, const void* logits, int64_t in_stride, int B, int V,
+                       float temperature, const void* workspace, size_t workspace_bytes,
+                       float* probs, int64_t out_stride, coopt_stream_t stream);
 
 /*
  * Elementwise stages of the Llama forward around the verify path (the model the step

@@ -250,6 +250,11 @@ def test_softmax_layouts(dev, dtype, V, pad):
     ref = torch.softmax(x.double().cpu() / torch.tensor(0.8, dtype=torch.float32).double(), -1)
     assert torch.allclose(probs.double().cpu(), ref, rtol=1e-5, atol=1e-12)
     assert torch.allclose(probs.double().sum(-1).cpu(), torch.ones(5, dtype=torch.float64), atol=1e-5)
+    # sample()'s probabilities (coopt_sample_probs, from the draw's row statistics)
+    u = torch.rand(5, generator=gen, device=dev)
+    tok, sprobs = M.sample(x, 0.8, uniforms=u)
+    assert torch.allclose(sprobs.double().cpu(), ref, rtol=1e-5, atol=1e-12)
+    assert torch.equal(tok, M.sample(x, 0.8, uniforms=u, return_probs=False)[0])
 
 
 def test_verify_signature_with_generator(dev):
