@@ -200,8 +200,19 @@ def attention_setup(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128):
                 per_tok=per_tok)
 
 
+# MI355X's Infinity Cache (256 MB) holds a call's whole working set when it is small and the
+# same call repeats back to back; in the step, a layer's cache was last read a whole forward
+# earlier.  Cases rotate over enough copies of their cache to exceed twice that size.
+INFINITY_CACHE_BYTES = 256 << 20
+
+
+def cache_copies(nbytes):
+    return max(1, -(-2 * INFINITY_CACHE_BYTES // max(int(nbytes), 1)))
+
+
 def attention_case(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128, cpu_sample=0):
-    """Verify attention (coopt_verify_attention) over the cache of attention_setup."""
+    """Verify attention (coopt_verify_attention) over the cache of attention_setup, the calls
+    rotating over cache_copies() copies of it (one at the roofline shape)."""
     st = attention_setup(torch, M, dev, ctx, qlen, kv_dtype, seed, D)
     Hq, Hkv, B, seq, ctx = st["Hq"], st["Hkv"], st["B"], st["seq"], st["ctx"]
     kc, vc, ks, vs = st["caches"]
@@ -211,15 +222,23 @@ def attention_case(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128, cpu_sample=0
     ws = torch.empty(M.attention.workspace_bytes(B, Hq, Hkv, D, qlen, max_k), dtype=torch.uint8,
                      device=dev)
     nbytes = int(seq.sum()) * st["per_tok"] + 2 * B * qlen * Hq * D * 2
+    sets = [(kc, vc, ks, vs, table)]
+    for i in range(1, cache_copies(nbytes)):
+        o = attention_setup(torch, M, dev, ctx.tolist(), qlen, kv_dtype, seed + 1000 * i, D)
+        sets.append((*o["caches"], o["table"]))
+    turn = [0]
 
     def fn():
-        M.paged_attention(q, kc, vc, cu, sl, table, qlen, max_k, D ** -0.5, ks, vs, out, ws)
+        c = sets[turn[0] % len(sets)]
+        turn[0] += 1
+        M.paged_attention(q, c[0], c[1], cu, sl, c[4], qlen, max_k, D ** -0.5, c[2], c[3], out, ws)
 
     cpu_sample = cpu_sample if CPU_LEGS["on"] else 0
 
     res = {"kv": kv_dtype, "head_dim": D, "batch": B, "q_len": qlen, "ctx_min": int(ctx.min()),
-           "ctx_max": int(ctx.max()), "ctx_mean": float(ctx.mean())}
+           "ctx_max": int(ctx.max()), "ctx_mean": float(ctx.mean()), "cache_copies": len(sets)}
     res = rate(res, nbytes, *time_launches(torch, dev, fn))
+    M.paged_attention(q, kc, vc, cu, sl, table, qlen, max_k, D ** -0.5, ks, vs, out, ws)
     if cpu_sample:
         # the same call on the host cores over the first cpu_sample sequences, scaled to the
         # batch by their share of the keys
@@ -243,12 +262,12 @@ def attention_qkv_case(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128, hidden=4
     2 Hkv) D over B q_len rows), RoPE, the new rows' K/V written at key positions ctx ..
     ctx + q_len - 1, and the attention over the cache of attention_setup.  Algorithmic bytes:
     the K/V of every key (the new ones read back after their write), the partials once, the
-    new rows' K/V written, the RoPE table rows and the output."""
+    new rows' K/V written, the RoPE table rows and the output.  The calls rotate over
+    cache_copies() copies of the cache (the partials, as in the step, stay warm)."""
     import numpy as np
 
     st = attention_setup(torch, M, dev, ctx, qlen, kv_dtype, seed, D)
     Hq, Hkv, bs, B, seq, ctx = st["Hq"], st["Hkv"], st["bs"], st["B"], st["seq"], st["ctx"]
-    kc, vc, ks, vs = st["caches"]
     g = st["gen"]
     T, width = B * qlen, (Hq + 2 * Hkv) * D
     x = torch.randn(T, hidden, generator=g, device=dev).to(torch.bfloat16)
@@ -258,10 +277,13 @@ def attention_qkv_case(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128, hidden=4
     if not isinstance(part, M.fused.LinearPartials):
         raise RuntimeError("expected split-K partials from the qkv projection")
     pos_np = np.concatenate([np.arange(c, c + qlen) for c in ctx]).astype(np.int64)
-    tb = st["table_np"]
-    slot_np = np.concatenate([tb[b][np.arange(c, c + qlen) // bs] * bs + np.arange(c, c + qlen) % bs
-                              for b, c in enumerate(ctx)]).astype(np.int64)
-    pos, slots = torch.from_numpy(pos_np).to(dev), torch.from_numpy(slot_np).to(dev)
+    pos = torch.from_numpy(pos_np).to(dev)
+
+    def cache_set(o):  # caches, table and the new rows' slots of one copy
+        tb = o["table_np"]
+        slot_np = np.concatenate([tb[b][np.arange(c, c + qlen) // bs] * bs + np.arange(c, c + qlen) % bs
+                                  for b, c in enumerate(ctx)]).astype(np.int64)
+        return (*o["caches"], o["table"], torch.from_numpy(slot_np).to(dev))
     max_pos = st["max_k"] + 8
     inv = 500000.0 ** (-torch.arange(0, D // 2, dtype=torch.float64) * 2 / D)
     ang = torch.arange(max_pos, dtype=torch.float64)[:, None] * inv[None, :]
@@ -272,14 +294,22 @@ def attention_qkv_case(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128, hidden=4
     ws = torch.empty(M.attention.workspace_bytes(B, Hq, Hkv, D, qlen, st["max_k"]),
                      dtype=torch.uint8, device=dev)
 
-    def fn():
-        M.paged_attention_qkv(part, pos, cos, sin, slots, kc, vc, st["cu"], st["sl"], st["table"],
-                              qlen, st["max_k"], Hq, D ** -0.5, kv_dtype, ks, vs, out, ws)
-
     nbytes = (int(seq.sum()) * st["per_tok"] + part.ks * T * width * 4 + T * st["per_tok"]
               + T * D * 2 + T * Hq * D * 2)
+    sets = [cache_set(st)]
+    for i in range(1, cache_copies(nbytes)):
+        sets.append(cache_set(attention_setup(torch, M, dev, ctx.tolist(), qlen, kv_dtype,
+                                              seed + 1000 * i, D)))
+    turn = [0]
+
+    def fn():
+        kc, vc, ks, vs, table, slots = sets[turn[0] % len(sets)]
+        turn[0] += 1
+        M.paged_attention_qkv(part, pos, cos, sin, slots, kc, vc, st["cu"], st["sl"], table,
+                              qlen, st["max_k"], Hq, D ** -0.5, kv_dtype, ks, vs, out, ws)
+
     res = {"kv": kv_dtype, "head_dim": D, "batch": B, "q_len": qlen, "ctx": int(ctx.max()),
-           "qkv_partials": part.ks, "hidden": hidden}
+           "qkv_partials": part.ks, "hidden": hidden, "cache_copies": len(sets)}
     return rate(res, nbytes, *time_launches(torch, dev, fn))
 
 
