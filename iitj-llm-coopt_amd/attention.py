@@ -10,8 +10,10 @@ keys [0, seq_len - q_len + j] (causal mask aligned bottom-right, engine/model.py
 For INT8 caches (codes + fp16 per-token scales from reshape_and_cache_flash(..., "int8"))
 pass k_scale/v_scale; dequantisation is fused into the kernel.
 
-Supported: head_dim 64 or 128, (Hq/Hkv) * max_seqlen_q <= 64 (speculative verify and decode
-shapes); prefill-sized queries are outside this kernel's scope.
+Supported: head_dim 64 or 128, any q_len.  Items of up to 64 rows per KV head, (Hq/Hkv) *
+max_seqlen_q <= 64 (speculative verify and decode), take the tuned path; longer ones (the
+prefill chunks engine/engine.py:414-420 mixes into the same batch) run in query windows of
+64/(Hq/Hkv) rows, one block per window and KV head -- correct at any length, not tuned.
 """
 import math
 
@@ -199,7 +201,7 @@ def paged_attention_qkv(qkv, positions, cos, sin, slot_mapping, k_cache, v_cache
 
 def flash_attn_varlen_func(q, k, v, cu_seqlens_q, max_seqlen_q, seqused_k, max_seqlen_k,
                            softmax_scale=None, causal=True, block_table=None, fa_version=2,
-                           k_scale=None, v_scale=None, out=None):
+                           k_scale=None, v_scale=None, out=None, workspace=None):
     """Keyword-compatible with the vLLM call the reference makes (engine/model.py:244-247)."""
     if not causal:
         raise ValueError("only causal=True is supported (the reference always passes it)")
@@ -207,4 +209,4 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, max_seqlen_q, seqused_k, max_s
         raise ValueError("block_table is required: this is the paged-KV path")
     del fa_version
     return paged_attention(q, k, v, cu_seqlens_q, seqused_k, block_table, max_seqlen_q,
-                           max_seqlen_k, softmax_scale, k_scale, v_scale, out)
+                           max_seqlen_k, softmax_scale, k_scale, v_scale, out, workspace)

@@ -16,6 +16,9 @@
 // cross-workgroup fence is needed.  A ragged batch with more (sequence, KV head) items than
 // one round of blocks holds runs on a 1-D grid whose blocks rank the sequences by length and
 // take the items longest first (plan_item), so its long sequences do not start last.
+// Items of more than 64 rows (prefill chunks of a mixed batch) are cut into query windows of
+// 64/G query rows -- each window is itself a sequence of those rows over the keys its last
+// row sees -- and run one unsplit block per (window, KV head): correct at any length.
 //
 // MFMA layout (v_mfma_f32_16x16x32_{bf16,f16}; lane l, g = l/16, m = l%16):
 //   scores  S^T[key][row] = sum_d K[key][d] Q[row][d]     A = K, B = Q^T
@@ -93,6 +96,11 @@ struct AttnArgs {
   float* part_o;
   int B;
   int plan;  // blocks order the items longest first (plan_item)
+  // Query windows (nwin > 0): a sequence's rows are taken qwin at a time, window w being rows
+  // [w * qwin, (w + 1) * qwin) with the keys its last row sees -- on its own a sequence of
+  // those rows, so the bottom-right causal mask stays exact.  1-D grid, block x = ((b * nwin)
+  // + w) * Hkv + hkv, one split per window.
+  int qwin, nwin;
   // Fused qkv epilogue (coopt_verify_attention_qkv): qkv_mode 0 = q is given; 1 = bf16 qkv
   // projection rows; 2 = their fp32 split-K partials.  The block computes its own q rows
   // (RoPE'd, straight into LDS) and writes its KV head's new K/V to the cache first.
@@ -380,8 +388,10 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
         tab = rope_tab<GL>(a.cos, a.sin, a.tab_stride, p, a.max_pos, c);
       const uint4 yr = rope_chunk<GL>(xr, tab, c);
       if (!is_kv) {
-        const int r = hl * n + j;  // < R <= kRows
-        *reinterpret_cast<uint4*>(qsh + r * kQPitch + c * 16) = yr;
+        // rows past R (a sequence with more rows than max_seqlen_q) are not attended; their
+        // store would land past the Q rows
+        const int r = hl * n + j;
+        if (r < R) *reinterpret_cast<uint4*>(qsh + r * kQPitch + c * 16) = yr;
       } else if (slot >= 0 && slot < num_slots) {  // padding rows write nothing
         const int64_t blk = slot >> a.bs_shift;
         const int64_t off = slot & bs_mask;
@@ -988,6 +998,22 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
     hkv = static_cast<int>(blockIdx.x) % a.Hkv;
     sidx = 0;
     first_pages(b, sidx, pg0, pg1);
+  } else if (a.nwin > 0) {
+    const int x = static_cast<int>(blockIdx.x);
+    hkv = x % a.Hkv;
+    const int rest = x / a.Hkv;
+    b = rest / a.nwin;
+    const int w = rest - b * a.nwin;
+    sidx = 0;
+    const const_i32_ptr cuc = (const_i32_ptr)a.cu;
+    const const_i32_ptr slc = (const_i32_ptr)a.seq_lens;
+    const int c0 = cuc[b], c1 = cuc[b + 1], sl = slc[b];
+    first_pages(b, sidx, pg0, pg1);
+    const int nall = c1 - c0, j0 = w * a.qwin;
+    n = min(max(nall - j0, 0), a.qwin);
+    q0 = c0 + j0;
+    // keys [0, L) end where the window's last row's causal limit does
+    L = min(sl, a.max_seqlen_k) - (nall - j0 - n);
   } else {
     b = blockIdx.z;
     hkv = blockIdx.y;
@@ -1072,14 +1098,32 @@ int choose_split(int B, int Hkv, int max_seqlen_k, int waves) {
 // more (sequence, KV head) items than one round of blocks holds, none split, B <= kPlanSeqs --
 // a 1-D grid of B * Hkv blocks that order the items themselves (plan_item); otherwise the
 // grid (max_splits, Hkv, B) in order, where one round holds every item and order is moot.
+// Windowed launches (query windows, see AttnArgs): more than kMaxRows rows per KV head.
 struct AttnShape {
   bool plan;
   int split, max_splits;
+  int rmax;        // rows per (item, KV head): G * max_seqlen_q, or G * qwin when windowed
+  int qwin, nwin;  // windowed: rows per window and windows per sequence (else 0, 0)
 };
 
-AttnShape attn_shape(int B, int Hkv, int rmax, int max_seqlen_k) {
-  const int waves = waves_for((rmax + 15) / 16);
+constexpr int kMaxRows = 64;
+
+AttnShape attn_shape(int B, int G, int Hkv, int max_seqlen_q, int max_seqlen_k) {
   AttnShape s{};
+  if (G * static_cast<int64_t>(max_seqlen_q) > kMaxRows) {
+    // prefill-sized rows (a chunk of a mixed batch, a long catch-up): windows of kMaxRows / G
+    // rows, each one unsplit block -- correct at any length, not tuned for throughput
+    s.qwin = kMaxRows / G;
+    s.nwin = (max_seqlen_q + s.qwin - 1) / s.qwin;
+    s.rmax = G * s.qwin;
+    const int gran = 32 * waves_for((s.rmax + 15) / 16);
+    s.split = static_cast<int>((static_cast<int64_t>(max_seqlen_k) + gran - 1) / gran * gran);
+    s.max_splits = 1;
+    s.plan = false;
+    return s;
+  }
+  s.rmax = G * max_seqlen_q;
+  const int waves = waves_for((s.rmax + 15) / 16);
   s.split = choose_split(B, Hkv, max_seqlen_k, waves);
   s.max_splits = (max_seqlen_k + s.split - 1) / s.split;
   s.plan = B <= kPlanSeqs && static_cast<int64_t>(B) * Hkv > target_blocks(waves) &&
@@ -1148,10 +1192,12 @@ int launch_d(bool int8, bool sc, int RT, const AttnArgs& a, dim3 grid, hipStream
 
 extern "C" size_t coopt_verify_attention_workspace(int B, int Hq, int Hkv, int D, int max_seqlen_q,
                                                    int max_seqlen_k) {
-  if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv || max_seqlen_q <= 0 || max_seqlen_k <= 0) return 0;
-  const int rmax = (Hq / Hkv) * max_seqlen_q;
-  const AttnShape sh = attn_shape(B, Hkv, rmax, max_seqlen_k);
-  return attn_ws_layout(B, Hkv, D, rmax, sh.max_splits).total;
+  if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv || Hq / Hkv > kMaxRows || max_seqlen_q <= 0 ||
+      max_seqlen_k <= 0)
+    return 0;
+  const AttnShape sh = attn_shape(B, Hq / Hkv, Hkv, max_seqlen_q, max_seqlen_k);
+  if (sh.nwin > 0) return 256;  // one split per window: no partials
+  return attn_ws_layout(B, Hkv, D, sh.rmax, sh.max_splits).total;
 }
 
 namespace {
@@ -1198,7 +1244,7 @@ int verify_attention_impl(const char* who, const FusedQkv* fz, int kv_dtype, con
                "block_size must be a power of two >= 16");
   ATTN_REQUIRE(max_seqlen_q > 0 && max_seqlen_k > 0, "max_seqlen_q/k must be positive");
   const int G = Hq / Hkv;
-  ATTN_REQUIRE(G * max_seqlen_q <= 64, "(Hq/Hkv) * max_seqlen_q must be <= 64");
+  ATTN_REQUIRE(G <= kMaxRows, "Hq/Hkv must be <= 64");
   ATTN_REQUIRE(bt_stride >= (max_seqlen_k + block_size - 1) / block_size,
                "block_table narrower than ceil(max_seqlen_k / block_size)");
   if (B == 0) return COOPT_OK;
@@ -1258,8 +1304,14 @@ int verify_attention_impl(const char* who, const FusedQkv* fz, int kv_dtype, con
   a.out = static_cast<uint16_t*>(out);
   a.o_ts = o_tok_stride;
   a.o_hs = o_head_stride;
-  a.rmax = G * max_seqlen_q;
-  const AttnShape shape = attn_shape(B, Hkv, a.rmax, max_seqlen_k);
+  const AttnShape shape = attn_shape(B, G, Hkv, max_seqlen_q, max_seqlen_k);
+  // grid limits: 2^32 work-items along x, 65535 blocks along z
+  ATTN_REQUIRE(shape.nwin == 0 || static_cast<int64_t>(B) * shape.nwin * Hkv < (int64_t{1} << 24),
+               "too many query windows for one launch");
+  ATTN_REQUIRE(shape.nwin > 0 || B <= 65535, "batch must be <= 65535 sequences");
+  a.rmax = shape.rmax;
+  a.qwin = shape.qwin;
+  a.nwin = shape.nwin;
   a.split = shape.split;
   a.max_splits = shape.max_splits;
   a.B = B;
@@ -1303,7 +1355,8 @@ int verify_attention_impl(const char* who, const FusedQkv* fz, int kv_dtype, con
   coopt::clear_error();
 
   const int RT = (a.rmax + 15) / 16;
-  const dim3 grid = shape.plan ? dim3(B * Hkv) : dim3(a.max_splits, Hkv, B);
+  const dim3 grid = shape.nwin > 0 ? dim3(B * shape.nwin * Hkv)
+                    : (shape.plan ? dim3(B * Hkv) : dim3(a.max_splits, Hkv, B));
   auto s = static_cast<hipStream_t>(stream);
   // scale caches with consecutive tokens adjacent and 8-byte aligned groups of four
   const bool sc = int8 && s_tok_stride == 1 && s_blk_stride % 4 == 0 && s_head_stride % 4 == 0 &&
@@ -1344,9 +1397,10 @@ extern "C" int coopt_verify_attention_qkv_supported(int kv_dtype, int B, int Hq,
   if (kv_dtype != COOPT_DT_BF16 && kv_dtype != COOPT_DT_I8) return 0;
   if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv || max_seqlen_q <= 0 || max_seqlen_k <= 0) return 0;
   if (D != 64 && D != 128) return 0;
-  const int rmax = (Hq / Hkv) * max_seqlen_q;
-  if (!fused_ok(D, kv_dtype == COOPT_DT_I8, (rmax + 15) / 16)) return 0;
-  return attn_shape(B, Hkv, rmax, max_seqlen_k).max_splits == 1 ? 1 : 0;
+  const int G = Hq / Hkv;
+  if (static_cast<int64_t>(G) * max_seqlen_q > kMaxRows) return 0;
+  if (!fused_ok(D, kv_dtype == COOPT_DT_I8, (G * max_seqlen_q + 15) / 16)) return 0;
+  return attn_shape(B, G, Hkv, max_seqlen_q, max_seqlen_k).max_splits == 1 ? 1 : 0;
 }
 
 extern "C" int coopt_verify_attention_qkv(

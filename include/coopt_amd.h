@@ -236,8 +236,13 @@ int coopt_kv_copy_blocks(const int64_t* regions, int num_regions, const int64_t*
  *                           therefore not bit-equal to the bf16 path on the dequantised
  *                           cache; it stays within the INT8 tolerance of attention over it.
  *   block_table [B, bt_stride] int32; entries past ceil(L/block_size) are never read.
- *   Supported: D in {64, 128}; (Hq/Hkv) * max_seqlen_q <= 64; block_size a power of two >= 16;
- *   B * Hkv <= 131072.  Callers must keep seq_lens <= max_seqlen_k, q rows per sequence
+ *   Supported: D in {64, 128}; Hq/Hkv <= 64; block_size a power of two >= 16; B <= 65535.
+ *   Query rows: up to 64 rows per (sequence, KV head), i.e. (Hq/Hkv) * max_seqlen_q <= 64
+ *   (speculative verify and decode), run on the tuned path (contexts split over blocks).
+ *   Longer items -- the prefill chunks the engine mixes into one batch with its verify items
+ *   (engine/engine.py:414-420), or a long draft catch-up -- run in query windows of
+ *   64/(Hq/Hkv) rows, each window one block over the keys its last row sees: correct at any
+ *   length, not tuned for throughput (B * windows * Hkv < 2^24 blocks).  Callers must keep seq_lens <= max_seqlen_k, q rows per sequence
  *   <= max_seqlen_q and block ids in [0, num_blocks); the kernel clamps all three so a
  *   malformed call yields wrong rows but never an access outside its buffers.
  *   workspace: coopt_verify_attention_workspace() bytes (see above).

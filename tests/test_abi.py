@@ -90,7 +90,7 @@ def test_verify_attention_rejects_unsupported_shapes(lib):
                                           1 << 30, None)
     assert "head_dim" in _err(call(D=96))
     assert "multiple of Hkv" in _err(call(Hq=30))
-    assert "<= 64" in _err(call(mq=17))
+    assert "<= 64" in _err(call(Hq=130, Hkv=2))   # more query heads per KV head than rows
     assert "power of two" in _err(call(bs=24))
     assert ">= 16" in _err(call(bs=8))
     assert "narrower" in _err(call(bt=3))

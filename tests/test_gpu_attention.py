@@ -1,16 +1,20 @@
 """GPU parity: paged GQA verification attention vs oracle.paged (float64 closed form).
 
-Bar (north star): error <= 2e-2 with bf16 KV and <= 5e-2 with INT8 KV (against attention
-over dequantize(quantize(KV)) in bf16, eval/quality.py:48-52), where the error of an output
-element is |out - ref| / max(1, |ref|): the max-abs error for outputs of magnitude <= 1, and
-relative above that -- the x20 outliers of configs 2/4 make some outputs ~50, where one bf16
-ulp of the output alone is 0.25.  Plain max-abs is printed next to it.
+Bar (north star): 2e-2 max-abs with bf16 KV and 5e-2 with INT8 KV (against attention over
+dequantize(quantize(KV)) in bf16, eval/quality.py:48-52), on top of the output's own bf16
+rounding: every element must satisfy |out - ref| <= tol + 2 ulp_bf16(|ref|).  The x20
+outliers of configs 2/4 make some outputs ~50, where one bf16 ulp alone is 0.25, so a plain
+max-abs bar is out of reach for any bf16-output kernel; two ulps (the output's rounding, half
+an ulp, plus one and a half ulps of fp32 accumulation slack) is all the allowance a large
+output gets.  The excess over 2 ulps, the plain max-abs and the largest error in ulps are
+printed.
 """
 import numpy as np
 import pytest
 import torch
 
 import iitj_llm_coopt_amd as M
+from iitj_llm_coopt_amd.attention import workspace_bytes
 from oracle import paged as OP
 
 pytestmark = pytest.mark.gpu
@@ -19,6 +23,27 @@ TOL_BF16, TOL_INT8 = 2e-2, 5e-2
 
 def report(msg):
     print(msg, flush=True)
+
+
+def ulp_bf16(x):
+    """bf16's unit in the last place at |x|: 2^(floor(log2 |x|) - 7) (8 significant bits;
+    normal range, so |x| below 2^-126 counts as 2^-126)."""
+    a = np.maximum(np.abs(np.asarray(x, dtype=np.float64)), 2.0 ** -126)
+    return np.exp2(np.floor(np.log2(a)) - 7)
+
+
+def attn_error(out, ref):
+    """(excess, max-abs, max ulps) of out against ref: excess = max(|out - ref| - 2 ulp(ref)),
+    the quantity the tolerance bounds; ulps = the largest error in bf16 ulps among elements
+    with |ref| >= 1 (near 0 an ulp is too small to measure by)."""
+    out, ref = np.asarray(out, np.float64), np.asarray(ref, np.float64)
+    if out.size == 0:
+        return 0.0, 0.0, 0.0
+    d = np.abs(out - ref)
+    u = ulp_bf16(ref)
+    big = np.abs(ref) >= 1.0
+    ulps = float((d[big] / u[big]).max()) if big.any() else 0.0
+    return float((d - 2 * u).max()), float(d.max()), ulps
 
 
 class Pool:
@@ -81,17 +106,29 @@ class Pool:
         return OP.attention_seq(self.q[q0:q1].float().cpu().numpy(), K, V, self.D ** -0.5)
 
     def max_err(self, out, seqs=None):
-        """(scaled error, plain max-abs) over the given sequences."""
+        """(excess over 2 ulps, plain max-abs, max ulps) over the given sequences
+        (attn_error)."""
         seqs = range(len(self.ctx)) if seqs is None else seqs
-        err = mabs = 0.0
+        err, mabs, ulps = -np.inf, 0.0, 0.0
         o = out.float().cpu().numpy()
         for b in seqs:
             q0, q1 = int(self.cu[b]), int(self.cu[b + 1])
+            if q1 == q0:
+                continue
+            e, m, u = attn_error(o[q0:q1], self.oracle_seq(b))
+            err, mabs, ulps = max(err, e), max(mabs, m), max(ulps, u)
+        return max(err, 0.0), mabs, ulps
+
+    def scaled_err(self, out, seqs=None):
+        """max |out - ref| / max(1, |ref|) over the given sequences: a relative measure used
+        only to compare two kernels' accuracy on the same cache."""
+        seqs = range(len(self.ctx)) if seqs is None else seqs
+        o, err = out.float().cpu().numpy(), 0.0
+        for b in seqs:
+            q0, q1 = int(self.cu[b]), int(self.cu[b + 1])
             ref = self.oracle_seq(b)
-            d = np.abs(o[q0:q1] - ref)
-            err = max(err, float((d / np.maximum(1.0, np.abs(ref))).max()))
-            mabs = max(mabs, float(d.max()))
-        return err, mabs
+            err = max(err, float((np.abs(o[q0:q1] - ref) / np.maximum(1.0, np.abs(ref))).max()))
+        return err
 
 
 def test_strided_kv_check_shapes_and_block_major_view(dev):
@@ -113,8 +150,8 @@ def test_strided_kv_check_shapes_and_block_major_view(dev):
     assert torch.equal(a, b)
     ref = OP.attention(q.float().cpu().numpy(), kc.float().cpu().numpy(), vc.float().cpu().numpy(),
                        cu.cpu().numpy(), seq_lens.cpu().numpy(), table.cpu().numpy(), BS, D ** -0.5)
-    err = float(np.abs(a.float().cpu().numpy() - ref).max())
-    report(f"[strided] max-abs {err:.3g}")
+    err, mabs, ulps = attn_error(a.float().cpu().numpy(), ref)
+    report(f"[strided] excess {err:.3g} (max-abs {mabs:.3g}, {ulps:.2f} ulp)")
     assert err <= TOL_BF16
 
 
@@ -124,8 +161,8 @@ def test_config3_bf16_verify(dev):
     ctx = rng.integers(512, 4097, 32)
     pool = Pool(ctx, [5] * 32, 32, 8, 128, dev, "auto", seed=3)
     out = pool.run()
-    err, mabs = pool.max_err(out)
-    report(f"[config3] error {err:.3g} (max-abs {mabs:.3g})")
+    err, mabs, ulps = pool.max_err(out)
+    report(f"[config3] excess {err:.3g} (max-abs {mabs:.3g}, {ulps:.2f} ulp)")
     assert err <= TOL_BF16
 
 
@@ -140,8 +177,9 @@ def test_config4_int8_verify(dev, gamma):
     out = pool.run()
     assert bool(torch.isfinite(out.float()).all())
     seqs = list(range(0, 64, 4))
-    err, mabs = pool.max_err(out, seqs)
-    report(f"[config4 gamma={gamma}] error {err:.3g} (max-abs {mabs:.3g}) on {len(seqs)} seqs")
+    err, mabs, ulps = pool.max_err(out, seqs)
+    report(f"[config4 gamma={gamma}] excess {err:.3g} (max-abs {mabs:.3g}, {ulps:.2f} ulp) "
+           f"on {len(seqs)} seqs")
     assert err <= TOL_INT8
 
 
@@ -168,8 +206,8 @@ def test_int8_path_against_bf16_path_on_dequantised_cache(dev):
     a, b = pool.run(), _bf16_run(pool)
     d = ((a.float() - b.float()).abs() / b.float().abs().clamp(min=1.0)).max().item()
     ea, eb = pool.max_err(a)[0], pool.max_err(b)[0]
-    report(f"[int8 vs bf16 on dequantised cache] max {d:.3g}; oracle error int8 {ea:.3g} "
-           f"bf16 {eb:.3g}")
+    report(f"[int8 vs bf16 on dequantised cache] max {d:.3g}; excess over the oracle int8 "
+           f"{ea:.3g} bf16 {eb:.3g}")
     assert d <= 2.0 ** -5 and ea <= TOL_INT8 and eb <= TOL_INT8
 
 
@@ -185,9 +223,11 @@ def test_int8_path_exact_scales_at_least_as_accurate(dev):
         p2 = torch.where(f > 0, torch.exp2(torch.round(torch.log2(f.clamp(min=2.0 ** -14)))), f)
         sc.copy_(p2.to(torch.float16))
     a, b = pool.run(), _bf16_run(pool)
-    ea, eb = pool.max_err(a)[0], pool.max_err(b)[0]
-    report(f"[power-of-two scales] oracle error int8 {ea:.3g} bf16 {eb:.3g}")
-    assert ea <= eb * 1.05 + 1e-6 and ea <= TOL_INT8
+    ea, eb = pool.scaled_err(a), pool.scaled_err(b)
+    xa = pool.max_err(a)[0]
+    report(f"[power-of-two scales] oracle error (relative above 1) int8 {ea:.3g} bf16 {eb:.3g}; "
+           f"int8 excess over 2 ulps {xa:.3g}")
+    assert ea <= eb * 1.05 + 1e-6 and xa <= TOL_INT8
 
 
 @pytest.mark.parametrize("D", [128, 64])
@@ -217,8 +257,8 @@ def test_head_dim_64_decode_and_catch_up_shapes(dev, kv):
     ql = [1, 2, 1, 2, 1, 2, 1, 2]
     pool = Pool(ctx, ql, 32, 8, 64, dev, kv, seed=6)
     out = pool.run()
-    err, mabs = pool.max_err(out)
-    report(f"[D=64 {kv}] error {err:.3g} (max-abs {mabs:.3g})")
+    err, mabs, ulps = pool.max_err(out)
+    report(f"[D=64 {kv}] excess {err:.3g} (max-abs {mabs:.3g}, {ulps:.2f} ulp)")
     assert err <= (TOL_BF16 if kv == "auto" else TOL_INT8)
 
 
@@ -356,6 +396,49 @@ def test_ragged_batches_match_the_oracle(dev, case):
     assert torch.equal(out, again)
     live = [b for b in range(len(ctx)) if q_lens[b] > 0]
     seqs = live if len(live) <= 16 else live[::4]
-    err, mabs = pool.max_err(out, seqs)
-    report(f"[ragged {name}] error {err:.3g} (max-abs {mabs:.3g})")
+    err, mabs, ulps = pool.max_err(out, seqs)
+    report(f"[ragged {name}] excess {err:.3g} (max-abs {mabs:.3g}, {ulps:.2f} ulp)")
     assert err <= (TOL_INT8 if kv == "int8" else TOL_BF16)
+
+
+# Mixed batches as Engine.step builds them (engine/engine.py:414-420): prefill chunks of
+# hundreds of rows next to verify items (q_len gamma + 1) and decodes, in one call of the
+# attention at engine/model.py:244-247.  Items of more than 64 rows per KV head run in query
+# windows of 64 / (Hq / Hkv) rows.  (label, ctx, q_lens, Hq, Hkv, D, kv)
+MIXED = [
+    ("700-row chunks + verify items, bf16", [0, 300, 1100, 2000, 4000, 57],
+     [700, 700, 5, 5, 5, 1], 32, 8, 128, "auto"),
+    ("700-row chunks + verify items, int8", [0, 300, 1100, 2000, 4000, 57],
+     [700, 700, 5, 5, 5, 1], 32, 8, 128, "int8"),
+    ("draft head dim 64, long catch-ups", [10, 1100, 3000, 0], [64, 33, 5, 17], 32, 8, 64, "auto"),
+    ("draft head dim 64, long catch-ups, int8", [10, 1100, 3000, 0], [64, 33, 5, 17], 32, 8, 64,
+     "int8"),
+    ("one query head per KV head, 130 rows", [500, 20, 3000], [130, 1, 65], 8, 8, 128, "auto"),
+    ("8 query heads per KV head", [900, 0, 2500], [20, 9, 3], 32, 4, 128, "int8"),
+]
+
+
+@pytest.mark.parametrize("case", MIXED, ids=[c[0] for c in MIXED])
+def test_mixed_prefill_and_verify_batches_match_the_oracle(dev, case):
+    """Every row of every item against the float64 oracle (the ulp bar), and a second call
+    bit-identical."""
+    label, ctx, q_lens, Hq, Hkv, D, kv = case
+    pool = Pool(ctx, q_lens, Hq, Hkv, D, dev, kv, seed=41, outlier=0.01 if kv == "int8" else 0.0)
+    report(f"[mixed {label}] rows {sum(q_lens)} keys {int(pool.seq_lens.sum())}")
+    out = pool.run()
+    again = pool.run()
+    assert bool(torch.isfinite(out.float()).all())
+    assert torch.equal(out, again)
+    err, mabs, ulps = pool.max_err(out)
+    report(f"[mixed {label}] excess {err:.3g} (max-abs {mabs:.3g}, {ulps:.2f} ulp)")
+    assert err <= (TOL_INT8 if kv == "int8" else TOL_BF16)
+
+
+def test_windowed_call_needs_no_partials_workspace(dev):
+    """A windowed call runs every window unsplit: its workspace is the 256-byte minimum, and a
+    caller passing exactly that gets the same output as with a large workspace."""
+    pool = Pool([100, 2000], [200, 5], 32, 8, 128, dev, "auto", seed=43)
+    assert workspace_bytes(2, 32, 8, 128, 200, 2005) == 256
+    small = torch.empty(256, dtype=torch.uint8, device=dev)
+    big = torch.empty(1 << 20, dtype=torch.uint8, device=dev)
+    assert torch.equal(pool.run(workspace=small), pool.run(workspace=big))

@@ -1,7 +1,7 @@
 """GPU edge cases of the hot path: empty inputs, sequences without rows or without context,
 single-key sequences, one-sequence batches.  Same bars as the per-op tests: bit-exact for
-codes, copies and tokens; attention within the bf16 / INT8 tolerances of the float64 oracle
-(0 for rows whose visible range is empty, as oracle.paged.attention defines)."""
+codes, copies and tokens; attention within the bf16 / INT8 tolerances plus 2 bf16 ulps of the
+float64 oracle (0 for rows whose visible range is empty, as oracle.paged.attention defines)."""
 import numpy as np
 import pytest
 import torch
@@ -35,8 +35,8 @@ def test_attention_rowless_contextless_and_single_key_sequences(dev, kv, D):
     pool = Pool([0, 40, 0, 0, 200], [2, 0, 3, 1, 5], 32, 8, D, dev, kv, seed=11)
     out = pool.run()
     assert out.shape == (11, 32, D) and bool(torch.isfinite(out.float()).all())
-    err, mabs = pool.max_err(out, seqs=[0, 2, 3, 4])   # sequence 1 has no rows to check
-    report(f"[edges {kv} D={D}] error {err:.3g} (max-abs {mabs:.3g})")
+    err, mabs, ulps = pool.max_err(out, seqs=[0, 2, 3, 4])   # sequence 1 has no rows to check
+    report(f"[edges {kv} D={D}] excess {err:.3g} (max-abs {mabs:.3g}, {ulps:.2f} ulp)")
     assert err <= (TOL_INT8 if kv == "int8" else TOL_BF16)
 
 
