@@ -163,16 +163,20 @@ def require_cuda(*tensors):
 class WorkspaceCache:
     """Device scratch buffers, grown on demand and reused (the kernels need no initialised
     workspace).  One buffer per (device, stream): calls that overlap in time must not share
-    a workspace, and stream order keeps calls on one stream from overlapping."""
+    a workspace, and stream order keeps calls on one stream from overlapping.  An outgrown
+    buffer is kept alive, not freed: a HIP graph captured with it keeps its address."""
 
     def __init__(self):
         self._bufs = {}
+        self._retired = []
 
     def get(self, nbytes: int, device) -> torch.Tensor:
         dev = torch.device(device)
         key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
         buf = self._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
+            if buf is not None:
+                self._retired.append(buf)
             buf = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=dev)
             self._bufs[key] = buf
         return buf

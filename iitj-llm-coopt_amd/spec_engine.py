@@ -217,10 +217,17 @@ class HipOps:
         self.device = torch.device(device)
         self.fuse_qkv = fuse_qkv
         self._ws = {}
+        self._retired = []   # outgrown workspaces, kept alive for graphs that captured them
 
     def workspace(self, key, nbytes):
+        """A device buffer of at least nbytes for `key`.  A larger request replaces the buffer,
+        but the old one is kept alive: a graph captured earlier still writes through its
+        address (graphs of the smaller shapes keep using it, which is safe because replays
+        run in stream order)."""
         buf = self._ws.get(key)
         if buf is None or buf.numel() < nbytes:
+            if buf is not None:
+                self._retired.append(buf)
             buf = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=self.device)
             self._ws[key] = buf
         return buf
@@ -340,6 +347,12 @@ class SpecDecoder:
     (Bc, G) bucket with S_c = 2; a step that needs a longer catch-up runs eagerly, as the
     reference runs such draft batches outside its graphs.
 
+    The draft catch-up of a lagging sequence runs in one eager step of up to max_catchup
+    rows (S_c: the next power of two >= the largest lag - 1, capped there); a longer lag
+    takes several steps (engine/engine.py:365-372 bounds it by the step's token budget the
+    same way).  At more than 64 / (Hq / Hkv) rows the draft's attention runs in query windows.
+    At most max_steps steps run (the history and the block tables are sized for them).
+
     Random draws come from a uniform table (set_uniforms): step i reads row i of it.  Row
     layout, for the Bcap = max bucket slots and gamma_max:
       [0, gmax*Bcap)                   u_draft[i, b] at i*Bcap + b  (inverse-CDF draw of draft i)
@@ -352,7 +365,12 @@ class SpecDecoder:
                  prompt_len: int, max_steps: int, ops=None, target_kv="int8", draft_kv="auto",
                  temperature=1.0, block_size=16, seed=0, batch_buckets=None, max_catchup=64):
         dev = target.device
+        if int(max_catchup) < 2:
+            raise ValueError("max_catchup must be >= 2 (the graphs' catch-up stride)")
+        if int(max_steps) < 1:
+            raise ValueError("max_steps must be >= 1")
         self.t, self.d = target, draft
+        self.max_steps, self.steps_run = int(max_steps), 0
         self.P, self.T, self.gmax = prompt_len, temperature, gamma
         self.ops = ops or HipOps(dev)
         self.strides = target_strides(gamma)
@@ -384,6 +402,7 @@ class SpecDecoder:
         self.nu = Bc * (2 * gamma + 1)
         self.u = torch.zeros(self.nu, dtype=torch.float32, device=dev)
         self.u_ctr = torch.zeros((), **i64)
+        self.graphs = {}
         g = torch.Generator().manual_seed(seed + 17)
         self.set_uniforms(torch.rand((max_steps + 8, self.nu), generator=g))
         # accept outputs; the token rows are [Bc, S_t] per verify stride (contiguous)
@@ -404,7 +423,6 @@ class SpecDecoder:
         self.res = AcceptResult(self._acc_len, self._acc_tok[self.smax], self._margin)
         self._cu = {}
         self._row0 = {}
-        self.graphs = {}
         self.pool = None
         self.last_key = None
         self.B = batch                      # live sequences: slots [0, B)
@@ -426,12 +444,21 @@ class SpecDecoder:
 
     def set_uniforms(self, table):
         """table [rows, (2*gamma_max + 1) * Bcap] fp32 (layout in the class docstring); the next
-        step reads row 0 (graph replays included: the row index lives on the device)."""
+        step reads row 0, and a step past the last row raises.  A table with as many rows as
+        the current one is copied into it, so captured graphs keep reading the right memory
+        (their launches hold its address and row count); a table of another size replaces it
+        and drops the captured graphs, which are captured again on their next replay."""
         table = torch.as_tensor(table, dtype=torch.float32)
-        if table.dim() != 2 or table.shape[1] != self.nu:
-            raise ValueError(f"uniform table must be [rows, {self.nu}]")
-        self.u_table = table.to(self.hist.device).contiguous()
+        if table.dim() != 2 or table.shape[1] != self.nu or table.shape[0] < 1:
+            raise ValueError(f"uniform table must be [rows >= 1, {self.nu}]")
+        cur = getattr(self, "u_table", None)
+        if cur is not None and cur.shape == table.shape:
+            cur.copy_(table)
+        else:
+            self.u_table = table.to(self.hist.device).contiguous()
+            self.graphs.clear()
         self.u_ctr.zero_()
+        self.u_used = 0
 
     def set_gamma(self, gamma):
         """Draft length per live sequence (int or one per slot); 0 = plain decoding."""
@@ -621,8 +648,20 @@ class SpecDecoder:
         out = AcceptResult(self._s_len[:Bc], self.prop[i, :Bc].view(Bc, 1), self._s_margin[:Bc])
         self.ops.sample(self.draft_logits[:Bc, i], u, self.T, out=out)
 
+    def _check_room(self):
+        """Raises before a step the history, the block tables or the uniform table cannot
+        hold: the kernels would otherwise drop the history writes past max_len and reuse
+        uniform rows (the row index wraps)."""
+        if self.steps_run >= self.max_steps:
+            raise RuntimeError(f"max_steps ({self.max_steps}) steps have run; the decoder's "
+                               "history and block tables are sized for that many")
+        if self.u_used >= self.u_table.shape[0]:
+            raise RuntimeError(f"the uniform table's {self.u_table.shape[0]} rows are used up; "
+                               "call set_uniforms with a new table")
+
     def step(self):
         """One eager step (same device work as a graph replay, launched from the host)."""
+        self._check_room()
         key = self.bucket()
         self._step(*key)
         self._finish(key)
@@ -631,6 +670,8 @@ class SpecDecoder:
         Bc, S_t = key[0], key[2]
         self.res = AcceptResult(self._acc_len[:Bc], self._acc_tok[S_t][:Bc], self._margin[:Bc])
         self.last_key = key
+        self.steps_run += 1
+        self.u_used += 1
         self._advance_host(key[3])
 
     def capture(self, key=None):
@@ -663,6 +704,7 @@ class SpecDecoder:
     def replay(self):
         """One step through the captured graph of its bucket (captured on first use); steps
         whose draft catch-up needs more than 2 rows run eagerly."""
+        self._check_room()
         key = self.bucket()
         if key[3] != 2:
             return self.step()

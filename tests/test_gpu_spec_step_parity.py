@@ -11,8 +11,10 @@ oracle.step_check compares:
   * the oracle's own logits within LOGIT_TOL (relative to the largest logit) of the GPU's,
     and every cache entry the step wrote within KV_TOL, every other entry unchanged.
 Cases: tiny models with ragged gamma (0 .. gamma_max), a sequence made to lag by gamma 0 and
-then caught up (a stride-4 eager step), batch padding with dummy sequences, a retired
-sequence, greedy and sampled; and the config-5 widths (hidden 4096 / 2048, 32/8 heads, head
+then caught up (a stride-4 eager step), lags of 20 and 40 steps caught up on the default
+catch-up cap (a stride-64 eager step), batch padding with dummy sequences, a retired
+sequence, greedy and sampled, uniform tables set after capture, graphs of a small gamma
+replayed after the workspaces grew; and the config-5 widths (hidden 4096 / 2048, 32/8 heads, head
 dim 128 / 64, FFN 14336 / 8192, vocab 128256, INT8 target KV) at B=16, gamma 4, with two
 layers per model, through graph replays.
 """
@@ -36,11 +38,13 @@ def report(msg):
     print(msg, flush=True)
 
 
-def make(dev, tshape, dshape, B, gamma, P, steps, T, seed=0, std=0.02):
+def make(dev, tshape, dshape, B, gamma, P, steps, T, seed=0, std=0.02, catchup=16):
+    """catchup: SpecDecoder's max_catchup (None: the class default)."""
     t = RandomLlama(tshape, dev, seed=seed + 1, std=std)
     d = RandomLlama(dshape, dev, seed=seed + 2, std=std,
                     packed=("qkv", "o", "gate_up", "down", "lm_head"))
-    dec = SpecDecoder(t, d, B, gamma, P, steps, temperature=T, seed=seed, max_catchup=16)
+    kw = {} if catchup is None else {"max_catchup": catchup}
+    dec = SpecDecoder(t, d, B, gamma, P, steps, temperature=T, seed=seed, **kw)
     g = torch.Generator(device=dev).manual_seed(seed + 3)
     prompts = torch.randint(0, tshape.vocab, (B, P), generator=g, device=dev)
     dec.prefill(prompts, torch.rand(B, generator=g, device=dev))
@@ -129,3 +133,77 @@ def test_config5_widths_match_the_oracle_step(dev):
     for line in chk.log:
         report(f"  tie: {line}")
     assert s["accept_decisions"] >= 60 and s["diverged_sequences"] <= 1
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_long_lags_catch_up_on_the_default_path(dev, graph):
+    """The class default max_catchup (64): slot 1 spends 40 steps at gamma 0 and slot 2 the
+    last 20 of them, then both speculate again -- one eager step catches slot 1 up over 40
+    tokens and slot 2 over 20 (S_c 64: 256 draft rows per KV head, run in query windows by
+    the draft's attention), as engine/engine.py:365-372 does within its token budget; every
+    step against the oracle step, eagerly or with graph replays for the stride-2 steps."""
+    dec = make(dev, TINY_T, TINY_D, B=4, gamma=4, P=24, steps=48, T=1.0, seed=7, catchup=None)
+    assert dec.max_catchup == 64
+    chk = StepChecker(dec, logit_tol=LOGIT_TOL, kv_tol=KV_TOL)
+    sched = [[4, 0, 4, 3]] * 20 + [[4, 0, 0, 3]] * 20 + [[4, 4, 4, 4]] * 4
+    keys = []
+    s = checked_steps(dec, chk, sched, graph, keys)
+    report(f"[long lags graph={graph}] {s}; catch-up strides {sorted({k[3] for k in keys})}")
+    for line in chk.log:
+        report(f"  tie: {line}")
+    assert keys[40][3] == 64 and all(k[3] == 2 for i, k in enumerate(keys) if i != 40)
+    n, dc = dec.n.cpu().tolist(), dec.dc.cpu().tolist()
+    assert all(n[b] - dc[b] <= 2 for b in range(4))      # every sequence speculates again
+    assert s["draft_tokens"] > 100 and s["diverged_sequences"] <= 1
+
+
+def test_set_uniforms_after_capture_reaches_graph_replays(dev):
+    """A table set after the graphs were captured is what their replays read: two decoders
+    from the same state, one stepping eagerly and one through graphs captured before
+    set_uniforms, give the same histories."""
+    a = make(dev, TINY_T, TINY_D, B=6, gamma=4, P=24, steps=16, T=1.0, seed=9)
+    b = make(dev, TINY_T, TINY_D, B=6, gamma=4, P=24, steps=16, T=1.0, seed=9)
+    b.replay()
+    a.step()
+    torch.cuda.synchronize()
+    assert b.graphs
+    table = torch.rand(a.u_table.shape, generator=torch.Generator().manual_seed(123))
+    for d in (a, b):
+        d.set_uniforms(table)
+    assert b.graphs                                     # same shape: copied in place
+    for i in range(3):
+        a.step()
+        b.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(a.hist, b.hist) and torch.equal(a.n, b.n), i
+    # a table of another size replaces the old one and drops the graphs
+    b.set_uniforms(table[:4])
+    assert not b.graphs and b.u_table.shape[0] == 4
+
+
+def test_small_gamma_graph_replays_after_workspaces_grew(dev):
+    """set_gamma(1), replay, set_gamma(4), replay, set_gamma(1), replay: the gamma-1 graph was
+    captured before the accept and attention workspaces grew for gamma 4, and its replay
+    still matches an eager twin bit for bit (outgrown workspaces stay allocated)."""
+    a = make(dev, TINY_T, TINY_D, B=6, gamma=4, P=24, steps=16, T=1.0, seed=13)
+    b = make(dev, TINY_T, TINY_D, B=6, gamma=4, P=24, steps=16, T=1.0, seed=13)
+    for i, g in enumerate([1, 4, 1, 4, 1]):
+        for d in (a, b):
+            d.set_gamma(g)
+        a.step()
+        b.replay()
+        torch.cuda.synchronize()
+        _ = torch.randn(1 << 20, device=dev).sum().item()  # other allocations in between
+        Bc, G, S_t, _ = a.last_key
+        assert torch.equal(a.hist, b.hist) and torch.equal(a.n, b.n), i
+        assert torch.equal(a.target_logits[: Bc * S_t], b.target_logits[: Bc * S_t]), i
+
+
+def test_steps_past_max_steps_raise(dev):
+    dec = make(dev, TINY_T, TINY_D, B=2, gamma=2, P=8, steps=3, T=1.0, seed=15)
+    for _ in range(3):
+        dec.replay()
+    with pytest.raises(RuntimeError, match="max_steps"):
+        dec.replay()
+    with pytest.raises(RuntimeError, match="max_steps"):
+        dec.step()
