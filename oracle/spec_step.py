@@ -87,13 +87,16 @@ class Shape:
 
 class PagedCache:
     """One model's per-layer caches in the reference layout [NB, bs, Hkv, D] (bf16, or int8
-    codes with fp16 scales [NB, bs, Hkv]) and its per-slot block tables [slots, W]."""
+    codes with fp16 scales [NB, bs, Hkv]) and its per-slot block tables [slots, W].
+    value_dtype: the type INT8 entries are dequantised to before attention (bf16, as
+    dequantize() returns them; float32 for an fp32 reference forward)."""
 
-    def __init__(self, layers, block_table, block_size, kv_dtype):
+    def __init__(self, layers, block_table, block_size, kv_dtype, value_dtype=torch.bfloat16):
         self.layers = [list(L) for L in layers]       # (k, v, k_scale, v_scale) per layer
         self.block_table = np.asarray(block_table, dtype=np.int64)
         self.block_size = block_size
         self.kv_dtype = kv_dtype
+        self.value_dtype = value_dtype
         self.written = []                             # slots written since reset_log()
 
     def reset_log(self):
@@ -130,8 +133,8 @@ class PagedCache:
         blk = torch.from_numpy(s // self.block_size)
         off = torch.from_numpy(s % self.block_size)
         if self.kv_dtype == "int8":
-            K = (kc[blk, off].float() * ks[blk, off].float().unsqueeze(-1)).to(torch.bfloat16)
-            V = (vc[blk, off].float() * vs[blk, off].float().unsqueeze(-1)).to(torch.bfloat16)
+            K = (kc[blk, off].float() * ks[blk, off].float().unsqueeze(-1)).to(self.value_dtype)
+            V = (vc[blk, off].float() * vs[blk, off].float().unsqueeze(-1)).to(self.value_dtype)
             return K, V
         return kc[blk, off], vc[blk, off]
 
@@ -162,11 +165,13 @@ def attend(q, cache, layer, items, scale):
 
 class OracleLlama:
     """engine/model.py:181-218 on the CPU.  weights: embed, lm_head, norm and per layer
-    ln1, ln2, qkv [(H + 2 Hkv) D, hidden], o, gate_up [2 F, hidden], down -- row-major bf16."""
+    ln1, ln2, qkv [(H + 2 Hkv) D, hidden], o, gate_up [2 F, hidden], down -- row-major, in the
+    compute dtype (bf16 as the reference runs; float32 for a reference forward without bf16
+    roundings, whose RoPE tables are then float32 too)."""
 
-    def __init__(self, shape: Shape, weights: dict, max_pos: int):
+    def __init__(self, shape: Shape, weights: dict, max_pos: int, dtype=torch.bfloat16):
         self.s, self.w = shape, weights
-        self.cos, self.sin = rope_tables(shape.rope_theta, shape.head_dim, max_pos)
+        self.cos, self.sin = rope_tables(shape.rope_theta, shape.head_dim, max_pos, dtype)
         self.scale = 1.0 / math.sqrt(shape.head_dim)
 
     def forward(self, cache: PagedCache, items, all_logits):

@@ -17,6 +17,14 @@ step's row of the uniform table, copied to the host):
               127 * scale).
 A tolerance of None reports the largest difference without asserting on it (a deep model's
 bf16 rounding differences grow with depth; decisions are compared either way).
+
+noise_floor() (after after()) measures those differences against a float32 reference: the
+same step from the same state, teacher-forced on the same GPU logits, with the weights, the
+activations, RoPE tables and the bf16 caches' values in float32 (an INT8 cache keeps its
+codes: the format, not a rounding).  It returns the GPU's error against that reference next
+to the bf16 oracle's own -- the bf16 noise floor, the rule of the reference's
+tests/m4_correctness.py:146-151 (agree at least as well as two implementations of the same
+model agree with each other).
 The forward is not bit-reproducible across GEMM implementations (MFMA partial sums against a
 CPU GEMM), so logits and caches are compared with a tolerance and the decisions are compared
 bit-exactly from the same logits.
@@ -51,6 +59,7 @@ class StepChecker:
         self.dec = dec
         self.target = OS.OracleLlama(_shape(dec.t.s), _weights(dec.t), dec.max_len)
         self.draft = OS.OracleLlama(_shape(dec.d.s), _weights(dec.d), dec.max_len)
+        self.ref32 = None              # float32 reference models, built by noise_floor()
         self.logit_tol, self.kv_tol, self.tie = logit_tol, kv_tol, tie
         self.diverged = set()          # sequence ids no longer compared (a tie flipped)
         self.stats = Counter()
@@ -64,6 +73,8 @@ class StepChecker:
         hist = dec.hist.cpu()
         self.seqs = [OS.Seq(hist[b, :n[b]].tolist(), n[b] - 1, dc[b], dec.gamma[b])
                      for b in range(dec.B)]
+        self.seqs0 = [OS.Seq(list(x.tokens), x.num_computed, x.draft_computed, x.gamma)
+                      for x in self.seqs]
         self.ids = list(dec.seq_ids)
         self.pre = (_cache_copy(dec.tkv), _cache_copy(dec.dkv))
         self.counters = (int(dec.emitted), int(dec.drafted), int(dec.accepted))
@@ -89,6 +100,19 @@ class StepChecker:
         acc = dec.res.accepted_len.cpu().numpy()
         toks = dec.res.tokens.cpu().numpy()
         gmarg = dec.res.margin.cpu().numpy()
+        tc, dcch = self._caches(torch.bfloat16)
+        t0 = time.perf_counter()
+        rec, own = OS.step(self.seqs, self.target, self.draft, tc, dcch, dec.T, self.u_draft,
+                           self.u_acc, self.u_res, catchup_cap=S_c,
+                           logits_hook=self._hook(gpu_dl, gpu_tl))
+        secs = time.perf_counter() - t0
+        self._last = (rec, own, tc, dcch, gpu_dl, gpu_tl, S_c)
+        self._compare(rec, own, tc, dcch, gpu_dl, gpu_tl, gpu_dt, geff, acc, toks, gmarg, S_t)
+        return secs
+
+    @staticmethod
+    def _hook(gpu_dl, gpu_tl):
+        """Teacher forcing: the decisions are taken from the GPU step's logits."""
         n_drafts = Counter()
 
         def hook(stage, i, slots, mine):
@@ -97,17 +121,99 @@ class StepChecker:
                     n_drafts[b] += 1
                 return gpu_dl[slots, i]
             return torch.cat([gpu_tl[b, : n_drafts[b] + 1] for b in slots])
+        return hook
 
-        tc = OS.PagedCache([tuple(None if t is None else t.clone() for t in L) for L in self.pre[0]],
-                           dec.tkv.block_table.cpu().numpy(), dec.tkv.block_size, dec.tkv.kv_dtype)
-        dcch = OS.PagedCache([tuple(None if t is None else t.clone() for t in L) for L in self.pre[1]],
-                             dec.dkv.block_table.cpu().numpy(), dec.dkv.block_size, dec.dkv.kv_dtype)
-        t0 = time.perf_counter()
-        rec, own = OS.step(self.seqs, self.target, self.draft, tc, dcch, dec.T, self.u_draft,
-                           self.u_acc, self.u_res, catchup_cap=S_c, logits_hook=hook)
-        secs = time.perf_counter() - t0
-        self._compare(rec, own, tc, dcch, gpu_dl, gpu_tl, gpu_dt, geff, acc, toks, gmarg, S_t)
-        return secs
+    def _caches(self, dtype):
+        """Oracle caches holding the GPU's pre-step contents; dtype float32 widens the bf16
+        caches and dequantises INT8 entries to float32."""
+        dec = self.dec
+
+        def copy(t):
+            if t is None:
+                return None
+            return t.float() if (dtype == torch.float32 and t.dtype == torch.bfloat16) else t.clone()
+
+        return tuple(OS.PagedCache([tuple(copy(t) for t in L) for L in pre],
+                                   kv.block_table.cpu().numpy(), kv.block_size, kv.kv_dtype, dtype)
+                     for pre, kv in ((self.pre[0], dec.tkv), (self.pre[1], dec.dkv)))
+
+    def noise_floor(self):
+        """The last checked step against a float32 reference forward (see the module
+        docstring).  Returns {quantity: (GPU error, bf16 oracle error)} for the target and
+        draft logits (max |x - ref| / max |ref| and the RMS ratio ||x - ref|| / ||ref||), the
+        written KV entries (bf16 caches: max |x - ref| / max(1, |ref|) and RMS; INT8 caches:
+        dequantised, relative to each vector's range 127 * scale, max and RMS), and the
+        fraction of logit rows whose argmax differs from the reference's."""
+        dec = self.dec
+        rec16, own16, tc16, dc16, gpu_dl, gpu_tl, S_c = self._last
+        if self.ref32 is None:
+            def w32(model):
+                w = _weights(model)
+                f = lambda t: t.float()
+                return {"embed": f(w["embed"]), "lm_head": f(w["lm_head"]), "norm": f(w["norm"]),
+                        "layers": [{k: f(v) for k, v in L.items()} for L in w["layers"]]}
+            self.ref32 = (OS.OracleLlama(_shape(dec.t.s), w32(dec.t), dec.max_len, torch.float32),
+                          OS.OracleLlama(_shape(dec.d.s), w32(dec.d), dec.max_len, torch.float32))
+        seqs = [OS.Seq(list(x.tokens), x.num_computed, x.draft_computed, x.gamma) for x in self.seqs0]
+        tc32, dc32 = self._caches(torch.float32)
+        rec32, own32 = OS.step(seqs, self.ref32[0], self.ref32[1], tc32, dc32, dec.T, self.u_draft,
+                               self.u_acc, self.u_res, catchup_cap=S_c,
+                               logits_hook=self._hook(gpu_dl, gpu_tl))
+        assert [r.new for r in rec32] == [r.new for r in rec16], "teacher-forced decisions differ"
+        out = {}
+
+        def pair(key, gpu, o16, ref):
+            def errs(x):
+                d = (x - ref).abs()
+                return (float(d.max()) / max(float(ref.abs().max()), 1e-30),
+                        float(d.pow(2).sum().sqrt()) / max(float(ref.pow(2).sum().sqrt()), 1e-30),
+                        float((x.argmax(-1) != ref.argmax(-1)).float().mean()))
+            g, o = errs(gpu), errs(o16)
+            for i, name in enumerate(("max", "rms", "argmax_differs")):
+                prev = out.get(f"{key}_{name}", (0.0, 0.0))
+                out[f"{key}_{name}"] = (max(prev[0], g[i]), max(prev[1], o[i]))
+
+        for (stage, i), (slots, ref) in own32.items():
+            o16 = own16[(stage, i)][1]
+            if stage == "draft":
+                gpu = gpu_dl[slots, i]
+            else:
+                gpu = torch.cat([gpu_tl[b, : len(rec32[b].drafts) + 1] for b in slots])
+            pair("logits_" + stage, gpu, o16, ref)
+        post = (_cache_copy(dec.tkv), _cache_copy(dec.dkv))
+        for name, o16c, o32c, gpost in (("target", tc16, tc32, post[0]), ("draft", dc16, dc32, post[1])):
+            bs = o32c.block_size
+            written = np.unique(np.asarray(o32c.written, dtype=np.int64))
+            idx = torch.from_numpy(written)
+            flat = lambda t: t.reshape(t.shape[0] * bs, *t.shape[2:])[idx]
+            for li in range(len(gpost)):
+                if gpost[li][2] is None:      # bf16 cache: values
+                    for j in range(2):
+                        ref = flat(o32c.layers[li][j]).float()
+                        den = ref.abs().clamp(min=1.0)
+                        for who, x in (("gpu", flat(gpost[li][j]).float()),
+                                       ("o16", flat(o16c.layers[li][j]).float())):
+                            d = (x - ref).abs()
+                            e = (float((d / den).max()), float(d.pow(2).mean().sqrt()) /
+                                 max(float(ref.pow(2).mean().sqrt()), 1e-30))
+                            self._kv_acc(out, f"kv_{name}", who, e)
+                else:                         # INT8: dequantised, per vector range
+                    for j in range(2):
+                        rq, rs = flat(o32c.layers[li][j]).float(), flat(o32c.layers[li][j + 2]).float()
+                        ref = rq * rs.unsqueeze(-1)
+                        rng = (rs * 127).clamp(min=1e-6).unsqueeze(-1)
+                        for who, cc in (("gpu", gpost[li]), ("o16", o16c.layers[li])):
+                            x = flat(cc[j]).float() * flat(cc[j + 2]).float().unsqueeze(-1)
+                            d = (x - ref).abs() / rng
+                            e = (float(d.max()), float(d.pow(2).mean().sqrt()))
+                            self._kv_acc(out, f"kv_{name}", who, e)
+        return out
+
+    @staticmethod
+    def _kv_acc(out, key, who, e):
+        for i, name in enumerate(("max", "rms")):
+            g, o = out.get(f"{key}_{name}", (0.0, 0.0))
+            out[f"{key}_{name}"] = (max(g, e[i]), o) if who == "gpu" else (g, max(o, e[i]))
 
     def _flip(self, b, what, margin):
         self.stats["ties"] += 1
