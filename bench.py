@@ -162,11 +162,20 @@ def cpu_attention(torch, q, kc, vc, ks, vs, table, seq, qlen, seqs, D):
     return out
 
 
-def attention_setup(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128):
+def attention_setup(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128, outlier=0.01,
+                    layout="head"):
     """The paged cache of an attention case: len(ctx) sequences with ctx[b] cached tokens and
     q_len new rows each (seq_len = ctx + q_len), Hq 32 / Hkv 8, head size D, block size 16,
-    block tables a seeded permutation of a shared pool.  K/V are N(0,1) with 1% x20 outliers,
-    quantised on write for INT8."""
+    block tables a seeded permutation of a shared pool.  K/V are N(0,1), each element x20
+    with probability `outlier` (configs 2 and 4; config 3 is plain N(0,1)), quantised on write
+    for INT8.  layout: the caches' storage --
+      "head"   allocate_kv_cache: [NB, bs, Hkv, D] views of head-major storage (a head's 16
+               tokens of a block contiguous), scales likewise;
+      "token"  the reference's own per-layer caches, token-major [NB, bs, Hkv, D]
+               (engine/model.py:148-155), INT8 scales [NB, bs, Hkv] as quantize(cache[blocks])
+               lays them out (engine/kv_tier_manager.py:99);
+      "block"  a per-layer view buf[:, l, 0/1] of the elastic block-major buffer
+               [NB, 32, 2, bs, Hkv, D] (engine/elastic.py:74-77; bf16 only, as there)."""
     import numpy as np
 
     Hq, Hkv, bs = 32, 8, 16
@@ -182,13 +191,27 @@ def attention_setup(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128):
         table_np[b, :W[b]] = perm[o:o + W[b]]
         o += int(W[b])
     table = torch.from_numpy(table_np).to(dev)
-    kc, vc, ks, vs = M.allocate_kv_cache(nblk, bs, Hkv, D, kv_dtype, device=dev)
+    buf = None
+    if layout == "head":
+        kc, vc, ks, vs = M.allocate_kv_cache(nblk, bs, Hkv, D, kv_dtype, device=dev)
+    elif layout == "token":
+        cdt = torch.int8 if kv_dtype == "int8" else torch.bfloat16
+        kc = torch.zeros(nblk, bs, Hkv, D, dtype=cdt, device=dev)
+        vc = torch.zeros_like(kc)
+        ks = torch.zeros(nblk, bs, Hkv, dtype=torch.float16, device=dev) if kv_dtype == "int8" else None
+        vs = None if ks is None else torch.zeros_like(ks)
+    elif layout == "block" and kv_dtype == "auto":
+        buf, kl, vl = M.allocate_block_major_kv(nblk, 32, bs, Hkv, D, device=dev)
+        kc, vc, ks, vs = kl[13], vl[13], None, None     # one layer's strided views
+    else:
+        raise ValueError(f"no {layout} layout for {kv_dtype} caches")
     g = torch.Generator(device=dev).manual_seed(seed)
     slots = torch.arange(nblk * bs, device=dev)
     for lo in range(0, nblk * bs, 1 << 18):   # fill the pool in chunks
         hi = min(nblk * bs, lo + (1 << 18))
         kv = torch.randn(2, hi - lo, Hkv, D, generator=g, device=dev)
-        kv = torch.where(torch.rand(kv.shape, generator=g, device=dev) < 0.01, kv * 20, kv)
+        if outlier:
+            kv = torch.where(torch.rand(kv.shape, generator=g, device=dev) < outlier, kv * 20, kv)
         kv = kv.to(torch.bfloat16)
         M.reshape_and_cache_flash(kv[0], kv[1], kc, vc, slots[lo:hi], kv_dtype, ks, vs)
         del kv
@@ -197,7 +220,7 @@ def attention_setup(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128):
     per_tok = Hkv * D * 2 * 2 if kv_dtype == "auto" else Hkv * (2 * D + 2 * 2)
     return dict(Hq=Hq, Hkv=Hkv, bs=bs, ctx=ctx, B=B, seq=seq, table_np=table_np, table=table,
                 caches=(kc, vc, ks, vs), gen=g, cu=cu, sl=sl, max_k=int(seq.max()),
-                per_tok=per_tok)
+                per_tok=per_tok, buf=buf)
 
 
 # MI355X's Infinity Cache (256 MB) holds a call's whole working set when it is small and the
@@ -210,10 +233,11 @@ def cache_copies(nbytes):
     return max(1, -(-2 * INFINITY_CACHE_BYTES // max(int(nbytes), 1)))
 
 
-def attention_case(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128, cpu_sample=0):
+def attention_case(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128, cpu_sample=0, outlier=0.01,
+                   layout="head"):
     """Verify attention (coopt_verify_attention) over the cache of attention_setup, the calls
     rotating over cache_copies() copies of it (one at the roofline shape)."""
-    st = attention_setup(torch, M, dev, ctx, qlen, kv_dtype, seed, D)
+    st = attention_setup(torch, M, dev, ctx, qlen, kv_dtype, seed, D, outlier, layout)
     Hq, Hkv, B, seq, ctx = st["Hq"], st["Hkv"], st["B"], st["seq"], st["ctx"]
     kc, vc, ks, vs = st["caches"]
     table, cu, sl, max_k, g = st["table"], st["cu"], st["sl"], st["max_k"], st["gen"]
@@ -222,10 +246,11 @@ def attention_case(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128, cpu_sample=0
     ws = torch.empty(M.attention.workspace_bytes(B, Hq, Hkv, D, qlen, max_k), dtype=torch.uint8,
                      device=dev)
     nbytes = int(seq.sum()) * st["per_tok"] + 2 * B * qlen * Hq * D * 2
-    sets = [(kc, vc, ks, vs, table)]
+    sets = [(kc, vc, ks, vs, table, st["buf"])]
     for i in range(1, cache_copies(nbytes)):
-        o = attention_setup(torch, M, dev, ctx.tolist(), qlen, kv_dtype, seed + 1000 * i, D)
-        sets.append((*o["caches"], o["table"]))
+        o = attention_setup(torch, M, dev, ctx.tolist(), qlen, kv_dtype, seed + 1000 * i, D,
+                            outlier, layout)
+        sets.append((*o["caches"], o["table"], o["buf"]))
     turn = [0]
 
     def fn():
@@ -236,7 +261,8 @@ def attention_case(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128, cpu_sample=0
     cpu_sample = cpu_sample if CPU_LEGS["on"] else 0
 
     res = {"kv": kv_dtype, "head_dim": D, "batch": B, "q_len": qlen, "ctx_min": int(ctx.min()),
-           "ctx_max": int(ctx.max()), "ctx_mean": float(ctx.mean()), "cache_copies": len(sets)}
+           "ctx_max": int(ctx.max()), "ctx_mean": float(ctx.mean()), "cache_copies": len(sets),
+           "cache_layout": layout, "outliers": outlier}
     res = rate(res, nbytes, *time_launches(torch, dev, fn))
     M.paged_attention(q, kc, vc, cu, sl, table, qlen, max_k, D ** -0.5, ks, vs, out, ws)
     if cpu_sample:
@@ -314,11 +340,14 @@ def attention_qkv_case(torch, M, dev, ctx, qlen, kv_dtype, seed, D=128, hidden=4
 
 
 def accept_case(torch, M, dev, B, gamma, V, seed):
-    """Config-1 distribution: target N(0, 2^2), draft = target + N(0, 0.5^2), fp32 logits."""
+    """Config 1: target N(0, 2^2), draft = target + N(0, 0.5^2), fp32 logits; the draft tokens
+    sampled from the draft softmax at T = 1 (sample(), inverse CDF on seeded uniforms), so the
+    accept positions, and with them the rows decide reads, follow the config's mix."""
     g = torch.Generator(device=dev).manual_seed(seed)
     tl = torch.randn(B, gamma + 1, V, generator=g, device=dev) * 2
     dl = (tl[:, :gamma] + torch.randn(B, gamma, V, generator=g, device=dev) * 0.5).contiguous()
-    dt = torch.randint(0, V, (B, gamma), generator=g, device=dev)
+    ud = torch.rand(B * gamma, generator=g, device=dev)
+    dt = M.sample(dl.view(B * gamma, V), 1.0, uniforms=ud)[0].view(B, gamma).long()
     ua = torch.rand(B, gamma, generator=g, device=dev)
     ur = torch.rand(B, generator=g, device=dev)
     res = M.accept(tl, dl, dt, 1.0, ua, ur)
@@ -643,7 +672,13 @@ KERNEL_CASES = {
     "attention_int8": lambda t, M, d, s: attention_case(t, M, d, [8192] * 32, 5, "int8", s),
     "attention_bf16": lambda t, M, d, s: attention_case(t, M, d, [8192] * 32, 5, "auto", s),
     # config 3: bf16, B=32, ctx U[512, 4096], q_len 5
-    "attention_config3": lambda t, M, d, s: attention_case(t, M, d, config_ctx(s, 32, 512, 4096), 5, "auto", s, cpu_sample=32),
+    "attention_config3": lambda t, M, d, s: attention_case(t, M, d, config_ctx(s, 32, 512, 4096), 5, "auto", s, cpu_sample=32, outlier=0.0),
+    # the roofline shape on the reference's own cache layouts: token-major per-layer caches
+    # (engine/model.py:148-155) and a layer view of the block-major elastic buffer
+    # (engine/elastic.py:74-77, bf16)
+    "attention_int8_token_major": lambda t, M, d, s: attention_case(t, M, d, [8192] * 32, 5, "int8", s, layout="token"),
+    "attention_bf16_token_major": lambda t, M, d, s: attention_case(t, M, d, [8192] * 32, 5, "auto", s, layout="token"),
+    "attention_bf16_block_major": lambda t, M, d, s: attention_case(t, M, d, [8192] * 32, 5, "auto", s, layout="block"),
     # config 4: INT8, B=64, ctx U[4096, 16384], gamma 2 / 4 / 8
     "attention_config4_g2": lambda t, M, d, s: attention_case(t, M, d, config_ctx(s, 64, 4096, 16384), 3, "int8", s, cpu_sample=8),
     "attention_config4_g4": lambda t, M, d, s: attention_case(t, M, d, config_ctx(s, 64, 4096, 16384), 5, "int8", s, cpu_sample=8),
@@ -677,6 +712,16 @@ KERNEL_CASES = {
     "linear_m32_lm_head": lambda t, M, d, s: linear_case(t, M, d, 32, 128256, 2048, s, packed=True),
     "copy": lambda t, M, d, s: copy_case(t, M, d, s),
 }
+
+
+def layout_fracs(kern):
+    """The roofline call's fraction of 8 TB/s on each cache layout (allocate_kv_cache's
+    head-major storage, the reference's token-major caches, the elastic block-major view)."""
+    names = {"int8": {"head_major": "attention_int8", "token_major": "attention_int8_token_major"},
+             "bf16": {"head_major": "attention_bf16", "token_major": "attention_bf16_token_major",
+                      "block_major_view": "attention_bf16_block_major"}}
+    return {kv: {lay: round(kern[n]["frac"], 4) for lay, n in d.items() if n in kern}
+            for kv, d in names.items()}
 
 
 def run_kernel_cases(torch, M, dev, names, seed):
@@ -1019,7 +1064,8 @@ def main():
                                "no split-merge launch)",
                      "bytes_per_launch": att_i8["bytes"], "avg_launch_us": att_i8["avg_us"],
                      "traffic_source": "profiles/verify_attention_int8_b32_ctx8192.md "
-                                       "(rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)"},
+                                       "(rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
+                     "frac_by_cache_layout": layout_fracs(kern)},
         "cpu_baseline": cpu,
         "acceptance_rate": acc_rate,
         "tokens_per_step": emitted / args.steps,
