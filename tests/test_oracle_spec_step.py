@@ -1,9 +1,8 @@
-"""CPU: pins oracle.spec_step (the step the GPU step is checked against) and oracle.step_ops.
+"""CPU: pins oracle.spec_step (the step the GPU step is checked against).
 
 * Stages reduce to pinned oracle functions: attention == oracle.paged.attention (float64
   closed form), cache slots == oracle.paged.slot_mapping, the INT8 write ==
-  oracle.paged.kv_write_int8 (oracle.codec), and OracleOps.row_slots == slot_mapping with
-  padding and positions past the table.
+  oracle.paged.kv_write_int8 (oracle.codec).
 * Closed forms: RMSNorm of special vectors, RoPE as a rotation by pos * theta^(-2i/D) (the
   identity at position 0, pair norms kept), the RoPE tables of engine/model.py:120-124.
 * Invariant: a prompt forwarded in one item equals the same prompt forwarded one token at a
@@ -22,7 +21,6 @@ import torch
 from oracle import accept as OA
 from oracle import paged as OP
 from oracle import spec_step as OS
-from oracle.step_ops import OracleOps
 
 SHAPE = OS.Shape(hidden=64, heads=4, kv_heads=2, head_dim=16, vocab=40)
 
@@ -98,48 +96,8 @@ def test_attend_and_write_reduce_to_oracle_paged(kv):
         assert np.array_equal(c2.layers[0][2].numpy(), ksn)
 
 
-def test_step_ops_row_slots_and_attend_match_oracle_paged():
-    class KV:
-        block_size = 16
-        block_table = torch.from_numpy(np.random.default_rng(2).permutation(64)[:24].reshape(3, 8).astype(np.int32))
-    start = torch.tensor([0, 37, 120], dtype=torch.int64)
-    n_real = torch.tensor([2, 5, 0], dtype=torch.int64)
-    pos, slots, seq_lens = OracleOps().row_slots(KV, start, 6, n_real)
-    slots = slots.view(3, 6).numpy()
-    for b in range(3):
-        for j in range(6):
-            p = int(start[b]) + j
-            if j >= n_real[b] or p // 16 >= 8:
-                assert slots[b, j] == -1
-            else:
-                assert slots[b, j] == OP.slot_mapping(KV.block_table[b].numpy(), p, p + 1, 16)[0]
-    assert seq_lens.tolist() == [6, 43, 126] and pos[1].tolist() == list(range(37, 43))
-    # OracleOps.attend == oracle.paged.attention on an INT8 cache
-    g = torch.Generator().manual_seed(3)
-
-    class C:
-        block_size = 16
-        kv_dtype = "int8"
-        block_table = KV.block_table
-        layers = [(torch.randint(-127, 128, (64, 16, 2, 16), generator=g, dtype=torch.int8),
-                   torch.randint(-127, 128, (64, 16, 2, 16), generator=g, dtype=torch.int8),
-                   (torch.rand(64, 16, 2, generator=g) * 0.05).half(),
-                   (torch.rand(64, 16, 2, generator=g) * 0.05).half())]
-    cu = torch.tensor([0, 2, 7, 8], dtype=torch.int32)
-    lens = torch.tensor([40, 100, 1], dtype=torch.int32)
-    q = torch.randn(8, 4, 16, generator=g).to(torch.bfloat16)
-    got = OracleOps().attend(C, 0, q, (cu, lens, 5, 128), 0.25).float().numpy()
-    kc, vc, ks, vs = C.layers[0]
-    ref = OP.attention(q.float().numpy(), OP.dequantized_cache(kc.numpy(), ks.numpy()),
-                       OP.dequantized_cache(vc.numpy(), vs.numpy()), cu.numpy(), lens.numpy(),
-                       C.block_table.numpy(), 16, 0.25)
-    # the only rounding left is the bf16 output: half an ulp plus fp32 summation error
-    assert (np.abs(got - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-3).all()
-
-
 # ---- closed forms ------------------------------------------------------------------------------
 def test_rms_norm_closed_forms():
-    ops = OracleOps()
     w = torch.full((8,), 2.0, dtype=torch.bfloat16)
     # constant vector c: c / sqrt(c^2 + eps) ~= sign(c)
     for c in (0.5, -3.0, 100.0):
@@ -151,27 +109,19 @@ def test_rms_norm_closed_forms():
     r = 5.0 / math.sqrt(8)
     want = torch.tensor([[3 / r, 4 / r, 0, 0, 0, 0, 0, 0]]) * 2
     assert torch.allclose(OS.rms_norm(x, w, 0.0).float(), want, rtol=8e-3)
-    # the fused add + norm of OracleOps: residual += x, then the same norm
-    res = torch.tensor([[1.0, 2, 0, 0, 0, 0, 0, 0]], dtype=torch.bfloat16)
-    out = ops.rms_norm(torch.tensor([[2.0, 2, 0, 0, 0, 0, 0, 0]], dtype=torch.bfloat16), res, w, 0.0)
-    assert torch.equal(res, x) and torch.allclose(out.float(), want, rtol=8e-3)
 
 
 def test_rope_is_a_rotation_by_position_times_frequency():
     D, theta = 16, 500000.0
     cos, sin = OS.rope_tables(theta, D, 4096, dtype=torch.float32)
-    ops = OracleOps()
     for p in (0, 1, 7, 1000, 4095):
         for i in range(D // 2):
             e = torch.zeros(1, 1, D)
             e[0, 0, i] = 1.0
-            q, k = e.clone(), e.clone()
-            ops.rope(q, k, torch.tensor([p]), cos, sin)
             ang = p * theta ** (-2 * i / D)
             want = torch.zeros(D)
             want[i], want[i + D // 2] = math.cos(ang), math.sin(ang)
-            assert torch.allclose(q[0, 0], want, atol=1e-4) and torch.equal(q, k)
-            # the oracle Llama's bf16 form: q * cos + rotate_half(q) * sin
+            # the oracle Llama's form: q * cos + rotate_half(q) * sin
             r = e * cos[p] + OS.rotate_half(e) * sin[p]
             assert torch.allclose(r[0, 0], want, atol=1e-4)
     c16, s16 = OS.rope_tables(theta, D, 8)
