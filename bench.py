@@ -520,18 +520,20 @@ def kv_swap_in_all_case(torch, M, dev, seed, tokens=4096, layers=32, bits=8):
                 *time_launches(torch, dev, fn))
 
 
-def sample_case(torch, M, dev, seed, B=32, V=128256):
+def sample_case(torch, M, dev, seed, B=32, V=128256, probs=True):
     """The sample() drop-in (engine/spec_decode.py:12-17) at config 1's draft shape: fp32
     logits [B, V] at T = 1 -> one token per row by inverse CDF and the probability rows.
-    Algorithmic bytes: the logits read once and the probabilities written once."""
+    Algorithmic bytes: the logits read once and the probabilities written once.  probs=False:
+    tokens only, as the step draws its draft tokens (bf16 logits there), logits read once."""
     g = torch.Generator(device=dev).manual_seed(seed)
     x = torch.randn(B, V, generator=g, device=dev) * 2.0
     u = torch.rand(B, generator=g, device=dev)
 
     def fn():
-        M.sample(x, 1.0, uniforms=u)
+        M.sample(x, 1.0, uniforms=u, return_probs=probs)
 
-    return rate({"B": B, "V": V}, 2 * B * V * 4, *time_launches(torch, dev, fn))
+    return rate({"B": B, "V": V, "probs": probs}, (2 if probs else 1) * B * V * 4,
+                *time_launches(torch, dev, fn))
 
 
 def codec_case(torch, M, dev, seed, direction, rows=262144, D=128, bits=8):
@@ -702,6 +704,7 @@ KERNEL_CASES = {
     "kv_swap_in_4096tok_32layers": lambda t, M, d, s: kv_swap_in_all_case(t, M, d, s),
     "kv_tier_roundtrip": lambda t, M, d, s: kv_tier_case(t, M, d, s),
     "sample_b32": lambda t, M, d, s: sample_case(t, M, d, s),
+    "sample_tokens_b32": lambda t, M, d, s: sample_case(t, M, d, s, probs=False),
     "codec_quantize_64MiB": lambda t, M, d, s: codec_case(t, M, d, s, "quantize"),
     "codec_dequantize_64MiB": lambda t, M, d, s: codec_case(t, M, d, s, "dequantize"),
     "kv_migrate_256x2MiB": lambda t, M, d, s: migrate_case(t, M, d, s),

@@ -76,6 +76,7 @@ SIGNATURES = {
                                          _i, _i, _i, _p, _p, _p, _p]),
     "coopt_softmax": (_i, [_i, _p, _i64, _i64, _i, _f, _p, _i64, _p]),
     "coopt_sample_probs": (_i, [_i, _p, _i64, _i, _i, _f, _p, _sz, _p, _i64, _p]),
+    "coopt_sample": (_i, [_i, _p, _i64, _i, _i, _f, _p, _p, _p, _p, _i64, _p, _sz, _p]),
     "coopt_rms_norm": (_i, [_p, _p, _p, _p, _i64, _i, _f, _p]),
     "coopt_rope": (_i, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _i, _i, _i, _i, _i, _p]),
     "coopt_silu_mul": (_i, [_p, _p, _i64, _i, _p]),

@@ -77,11 +77,16 @@ __host__ __device__ inline int imin(int a, int b) { return a < b ? a : b; }
 // Launch 1 aims at ~512 blocks, i.e. as many elements per thread (up to kMaxPerThread, all
 // loads in flight at once) as the batch allows: at B = 8 that measured 28 us per call
 // against 34 us with 2048 smaller blocks.
+// gamma_max = 0 (a plain draw): chunks of at most kDrawChunk elements, the chunk the draw
+// block of launch 2 scans in registers (kDrawG 8-element groups a thread).
+constexpr int kDrawG = 4;
+constexpr int kDrawChunk = kThreads * 8 * kDrawG;  // 8192
+
 __host__ __device__ inline Layout make_layout(int B, int gmax, int V) {
   Layout L;
   const int rows = B * (2 * gmax + 1);
   int nch = ceil_div(512, rows > 0 ? rows : 1);
-  nch = imax(nch, ceil_div(V, kMaxChunk));
+  nch = imax(nch, ceil_div(V, gmax == 0 ? kDrawChunk : kMaxChunk));
   nch = imin(nch, imax(1, ceil_div(V, kMinChunk)));
   L.chunk1 = ceil_div(ceil_div(V, nch), 8) * 8;
   L.nch1 = ceil_div(V, L.chunk1);
@@ -382,7 +387,22 @@ __global__ __launch_bounds__(kThreads) void greedy_kernel(Args a) {
   __shared__ int argm[kMaxSlots];
   const int b = blockIdx.x;
   const int g = gamma_of(a, b);
-  if (static_cast<int>(threadIdx.x) <= g) argm[threadIdx.x] = combine_row(a, b, threadIdx.x, true).argmax;
+  // row slot i <= g by wave i % 4: lanes merge chunks lane, lane + 64, .. in order, then the
+  // wave merges lanes (first index on ties, as a serial merge in chunk order gives)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int i = wave; i <= g; i += kThreads / 64) {
+    const Partial1* p = a.ws.part1 + (static_cast<int64_t>(b) * (2 * a.gmax + 1) + i) * a.L.nch1;
+    float v = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int c = lane; c < a.L.nch1; c += 64) amax_merge(v, idx, p[c].m, p[c].idx);
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+      const float ov = __shfl_xor(v, m, 64);
+      const int oi = __shfl_xor(idx, m, 64);
+      amax_merge(v, idx, ov, oi);
+    }
+    if (lane == 0) argm[i] = idx;
+  }
   __syncthreads();
   if (threadIdx.x != 0) return;
   const int32_t* d = a.dtok + static_cast<int64_t>(b) * a.gmax;
@@ -1084,8 +1104,308 @@ __global__ __launch_bounds__(kPrThreads) void sample_probs_kernel(Args a, float*
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Launch 2 (sampling at gamma_max = 0: sample(), engine/spec_decode.py:12-17): the decision
+// and the chunk sums come from launch 1's partials, so one launch finishes the draw.
+// Per row, wave 0 combines the chunk partials into (M, S) and the chunk masses
+// P_c = s_c exp(m_c - M) / S (fp64); their prefix locates the chunk c* where the cumulative
+// probability crosses tau = u * sum(P_c).  Within c* the cumulative sum runs over the fp32
+// probabilities p_j = fp32(exp(x_j/T - M) / S) themselves (the values PROBS writes, and
+// select_kernel's weights), in fp64.  A chunk mass differs from the sum of its p_j by a few
+// 1e-7 of the total, so a draw within that of a chunk edge may land one element away from
+// the exact cumulative sum's -- inside the 1e-6 band such draws are reported in.
+// Grid (chunk, row): block c issues the loads of chunk c (kDrawG groups of 8 elements a
+// thread) before wave 0 combines the statistics, so no load waits on the decision; PROBS:
+// every block writes its chunk's probabilities; the block of chunk c* then draws from the
+// probabilities in its registers, and the other blocks are done.
+// ---------------------------------------------------------------------------------------
+constexpr int kPL = 8;  // chunk partials a lane of wave 0 keeps in registers
+
+// (M, 1 / S) of row b from its chunk partials, and with DRAW the crossing chunk: wave 0 only.
+// Rows of more than 64 * kPL chunks (vocabularies past 8M) read the rest again per pass.
+struct RowDraw {
+  float m;
+  double inv, total, tau, acc;
+  int chunk;
+};
+struct RowPartials {
+  Partial1 q[kPL];
+};
+// Issues wave 0's loads of row b's first 64 * kPL chunk partials.
+__device__ __forceinline__ void load_row_partials(const Args& a, int b, RowPartials& rp) {
+  const int lane = threadIdx.x & 63;
+  const Partial1* part = a.ws.part1 + static_cast<int64_t>(b) * a.L.nch1;
+  const int n = a.L.nch1, nk = (n + 63) / 64;
+  // unconditional loads of a clamped index keep the compiler's wait counts exact; chunks past
+  // the row are masked where row_draw reads them (a mask here would wait for the loads)
+  (void)nk;
+#pragma unroll
+  for (int k = 0; k < kPL; ++k) rp.q[k] = part[min(lane + 64 * k, n - 1)];
+}
+template <bool DRAW>
+__device__ __forceinline__ RowDraw row_draw(const Args& a, int b, float u, const RowPartials& rp) {
+  const int lane = threadIdx.x & 63;
+  const Partial1* part = a.ws.part1 + static_cast<int64_t>(b) * a.L.nch1;
+  const int n = a.L.nch1, nk = (n + 63) / 64;
+  Partial1 q[kPL];
+#pragma unroll
+  for (int k = 0; k < kPL; ++k) {
+    const bool in = k < nk && lane + 64 * k < n;
+    q[k].m = in ? rp.q[k].m : -INFINITY;
+    q[k].s = in ? rp.q[k].s : 0.0;
+    q[k].idx = -1;
+  }
+  auto far = [&](int k) {  // partial of chunk lane + 64 k, k >= kPL
+    return lane + 64 * k < n ? part[lane + 64 * k] : Partial1{-INFINITY, -1, 0.0};
+  };
+  float m = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < kPL; ++k) m = fmaxf(m, q[k].m);
+  for (int k = kPL; k < nk; ++k) m = fmaxf(m, far(k).m);
+  m = wave_max_f32_dpp(m);
+  auto mass_of = [&](const Partial1& x) {
+    return x.s > 0.0 ? x.s * exp(static_cast<double>(x.m) - static_cast<double>(m)) : 0.0;
+  };
+  double ms[kPL];
+  double S = 0.0;
+#pragma unroll
+  for (int k = 0; k < kPL; ++k) {
+    ms[k] = 0.0;
+    if (k < nk) {  // uniform
+      ms[k] = mass_of(q[k]);
+      S += ms[k];
+    }
+  }
+  for (int k = kPL; k < nk; ++k) S += mass_of(far(k));
+  S = wave_sum_f64_dpp(S);
+  RowDraw r{};
+  r.m = m;
+  r.inv = 1.0 / S;
+  if constexpr (DRAW) {
+    const double inv = r.inv;
+    double total = 0.0;
+#pragma unroll
+    for (int k = 0; k < kPL; ++k)
+      if (k < nk) total += ms[k] * inv;
+    for (int k = kPL; k < nk; ++k) total += mass_of(far(k)) * inv;
+    total = wave_sum_f64_dpp(total);
+    const double tau = static_cast<double>(u) * total;
+    // the first chunk with mass whose [prefix, prefix + P_c) holds tau; tau within rounding
+    // of the total: the last chunk with mass
+    double run = 0.0, acc = 0.0, acc_last = 0.0;
+    int chunk = -1, lastm = 0;
+    auto scan64 = [&](int k, double pc) {  // chunks 64 k .. 64 k + 63, this lane's mass pc
+      double ex;
+      const double in = wave_incl_scan_f64(pc, ex) + run;
+      ex = lane == 0 ? run : ex + run;
+      const uint64_t cr = __ballot(pc > 0.0 && ex <= tau && tau < in);
+      const uint64_t hm = __ballot(pc > 0.0);
+      if (chunk < 0 && cr) {
+        const int l = __builtin_ctzll(cr);
+        chunk = 64 * k + l;
+        acc = __shfl(ex, l, 64);
+      }
+      if (hm) {
+        const int l = 63 - __builtin_clzll(hm);
+        lastm = 64 * k + l;
+        acc_last = __shfl(ex, l, 64);
+      }
+      run = __shfl(in, 63, 64);
+    };
+#pragma unroll
+    for (int k = 0; k < kPL; ++k)
+      if (k < nk) scan64(k, ms[k] * inv);
+    for (int k = kPL; k < nk; ++k) scan64(k, mass_of(far(k)) * inv);
+    if (chunk < 0) {
+      chunk = lastm;
+      acc = acc_last;
+    }
+    r.total = total;
+    r.tau = tau;
+    r.acc = acc;
+    r.chunk = chunk;
+  }
+  return r;
+}
+
+template <bool BF16, bool PROBS>
+__global__ __launch_bounds__(kThreads) void sample_select_kernel(Args a, float* probs,
+                                                                 int64_t probs_stride, int vec_out) {
+  constexpr int kG = kDrawG;  // 8-element groups per thread
+  __shared__ float sh_m;
+  __shared__ double sh_inv, sh_total, sh_tau, sh_acc;
+  __shared__ int sh_chunk;
+  __shared__ double sh_pass[4][kG];
+  __shared__ double sh_scan[4];
+  __shared__ int sh_tok, sh_last;
+  __shared__ float sh_mg;
+  const int c = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t row = tgt_row(a, b, 0);
+  const float ures = a.u_res[b];
+  const int lo = c * a.L.chunk1, hi = min(a.V, lo + a.L.chunk1);
+  // group (it, t) covers elements lo + (it * kThreads + t) * 8 ..: pass it is the contiguous
+  // range [lo + it * kThreads * 8, +kThreads * 8) in thread order
+  float vals[kG * 8];
+  // a full chunk of aligned rows (readfirstlane: the compiler then knows the branch is
+  // uniform and keeps the two load paths apart, so no load waits for the other path's)
+  const bool full = __builtin_amdgcn_readfirstlane(a.vec_t && hi - lo == a.L.chunk1 ? 1 : 0) != 0;
+  if (full) {  // out-of-chunk groups re-load the chunk's first group (masked below)
+#pragma unroll
+    for (int it = 0; it < kG; ++it) {
+      const int j0 = lo + (it * kThreads + tid) * 8;
+      ld8<BF16>(a.tgt, row, a.tgt_stride, j0 < hi ? j0 : lo, vals + it * 8);
+    }
+  } else {
+#pragma unroll
+    for (int it = 0; it < kG; ++it)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int j = lo + (it * kThreads + tid) * 8 + e;
+        vals[it * 8 + e] = j < hi ? ld<BF16>(a.tgt, row, a.tgt_stride, j) : -INFINITY;
+      }
+  }
+  // the partials' loads go out right behind the chunk's (all in flight together)
+  RowPartials rp;
+  if (wave == 0) load_row_partials(a, b, rp);
+  if (tid == 0) {
+    sh_tok = 0x7fffffff;
+    sh_last = -1;
+    sh_mg = 0.0f;
+  }
+  if (wave == 0) {
+    const RowDraw r = row_draw<true>(a, b, ures, rp);
+    if (lane == 0) {
+      sh_m = r.m;
+      sh_inv = r.inv;
+      sh_total = r.total;
+      sh_tau = r.tau;
+      sh_acc = r.acc;
+      sh_chunk = r.chunk;
+    }
+  }
+  __syncthreads();
+  const bool draws = c == sh_chunk;  // uniform
+  if (!PROBS && !draws) return;
+  const float m_l2 = sh_m * kLog2e;
+  const double inv = sh_inv;
+  float* const pv = vals;  // the probabilities replace the logits in place
+#pragma unroll
+  for (int it = 0; it < kG; ++it)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int j = lo + (it * kThreads + tid) * 8 + e;
+      const float x = j < hi ? vals[it * 8 + e] : -INFINITY;
+      pv[it * 8 + e] = static_cast<float>(static_cast<double>(exp_shift(x * a.inv_t, m_l2)) * inv);
+    }
+  if constexpr (PROBS) {
+    float* orow = probs + static_cast<int64_t>(b) * probs_stride;
+#pragma unroll
+    for (int it = 0; it < kG; ++it) {
+      const int j0 = lo + (it * kThreads + tid) * 8;
+      const float* q = pv + it * 8;
+      if (vec_out && full) {
+        if (j0 < hi) {
+          float4* dst = reinterpret_cast<float4*>(orow + j0);
+          dst[0] = make_float4(q[0], q[1], q[2], q[3]);
+          dst[1] = make_float4(q[4], q[5], q[6], q[7]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (j0 + e < hi) orow[j0 + e] = q[e];
+      }
+    }
+    if (!draws) return;
+  }
+  // ---- the draw, in chunk c* ----
+  double gs[kG];
+  int last = -1;  // the last element with mass (fallback when tau lies past the element sum)
+#pragma unroll
+  for (int it = 0; it < kG; ++it) {
+    double d8 = 0.0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      d8 += static_cast<double>(pv[it * 8 + e]);
+      if (pv[it * 8 + e] > 0.0f) last = lo + (it * kThreads + tid) * 8 + e;
+    }
+    gs[it] = d8;
+    const double w = wave_sum_f64_dpp(d8);
+    if (lane == 0) sh_pass[wave][it] = w;
+  }
+  atomicMax(&sh_last, last);
+  __syncthreads();
+  const double tau = sh_tau, total = sh_total;
+  double run = sh_acc;
+  int pass = -1;
+  double pass_acc = 0.0;
+#pragma unroll
+  for (int it = 0; it < kG; ++it) {
+    const double T = ((sh_pass[0][it] + sh_pass[1][it]) + sh_pass[2][it]) + sh_pass[3][it];
+    if (pass < 0 && T > 0.0 && run <= tau && tau < run + T) {
+      pass = it;
+      pass_acc = run;
+    }
+    run += T;
+  }
+  bool claim = false;
+  int tok = -1;
+  float mg = 0.0f;
+  if (pass >= 0) {  // uniform
+    double g = 0.0;
+#pragma unroll
+    for (int it = 0; it < kG; ++it) g = it == pass ? gs[it] : g;
+    double excl, tot_unused;
+    const double incl = block_scan_f64(g, sh_scan, excl, tot_unused);
+    claim = g > 0.0 && pass_acc + excl <= tau && tau < pass_acc + incl;
+    if (claim) {
+      float w[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float x = 0.0f;
+#pragma unroll
+        for (int it = 0; it < kG; ++it) x = it == pass ? pv[it * 8 + e] : x;
+        w[e] = x;
+      }
+      const int j0 = lo + (pass * kThreads + tid) * 8;
+      double r = pass_acc + excl;
+      int lastw = -1;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const double wj = static_cast<double>(w[e]);
+        const double nxt = r + wj;
+        if (tok < 0) {
+          if (wj > 0.0) lastw = j0 + e;
+          if (nxt > tau && wj > 0.0) {
+            tok = j0 + e;
+            mg = static_cast<float>(fmin(tau - r, nxt - tau) / total);
+          }
+          r = nxt;
+        }
+      }
+      if (tok < 0) tok = lastw;  // rounding inside the group: its last element with mass
+      atomicMin(&sh_tok, tok);
+    }
+  }
+  __syncthreads();
+  if (claim && tok == sh_tok) sh_mg = mg;
+  __syncthreads();
+  if (tid == 0) {
+    int pick = sh_tok == 0x7fffffff ? -1 : sh_tok;
+    float pm = sh_mg;
+    if (pick < 0) {  // nobody claimed (tau past the chunk's element sum): its last element with mass
+      pick = sh_last >= 0 ? sh_last : lo;
+      pm = 0.0f;
+    }
+    a.out_tok[static_cast<int64_t>(b) * (a.gmax + 1)] = pick;
+    if (a.acc_len) a.acc_len[b] = 0;  // null for coopt_sample (tokens only)
+    if (a.margin) a.margin[b] = pm;
+  }
+}
+
+// probs: gamma_max = 0 only -- the softmax rows written by the draw's second launch.
 template <bool BF16>
-int launch_all(Args& a, bool greedy, hipStream_t s) {
+int launch_all(Args& a, bool greedy, hipStream_t s, float* probs = nullptr,
+               int64_t probs_stride = 0, int vec_out = 0) {
   const dim3 g1(a.L.nch1, 2 * a.gmax + 1, a.B);
   if (greedy)
     hipLaunchKernelGGL((row_stats_kernel<BF16, true>), g1, dim3(kThreads), 0, s, a);
@@ -1096,6 +1416,16 @@ int launch_all(Args& a, bool greedy, hipStream_t s) {
   if (greedy) {
     hipLaunchKernelGGL(greedy_kernel, dim3(a.B), dim3(kThreads), 0, s, a);
     return coopt::check_launch("coopt_accept_sample/greedy");
+  }
+  if (a.gmax == 0) {  // a plain draw: the decision and chunk sums follow from the partials
+    const dim3 grid(a.L.nch1, a.B);
+    if (probs)
+      hipLaunchKernelGGL((sample_select_kernel<BF16, true>), grid, dim3(kThreads), 0, s, a, probs,
+                         probs_stride, vec_out);
+    else
+      hipLaunchKernelGGL((sample_select_kernel<BF16, false>), grid, dim3(kThreads), 0, s, a,
+                         nullptr, 0, 0);
+    return coopt::check_launch("coopt_accept_sample/sample_select");
   }
   // rows of at most 16 chunk partials are combined by lane groups, one partial per thread
   const dim3 g2(a.L.nch2, a.B);
@@ -1274,6 +1604,43 @@ extern "C" int coopt_softmax(int logits_dtype, const void* logits, int64_t in_st
     hipLaunchKernelGGL(softmax_kernel<false>, dim3(static_cast<unsigned>(rows)), dim3(kSmThreads), 0, s,
                        logits, in_stride, V, inv_t, probs, out_stride, vec_ok);
   return coopt::check_launch("coopt_softmax");
+}
+
+extern "C" int coopt_sample(int logits_dtype, const void* logits, int64_t row_stride, int N, int V,
+                            float temperature, const float* uniforms, int32_t* tokens,
+                            float* margin, float* probs, int64_t probs_stride, void* workspace,
+                            size_t workspace_bytes, coopt_stream_t stream) {
+  COOPT_REQUIRE(logits_dtype == COOPT_DT_F32 || logits_dtype == COOPT_DT_BF16,
+                "logits_dtype must be F32 or BF16");
+  COOPT_REQUIRE(N >= 0 && N <= 65535 && V > 0 && row_stride >= V, "bad sizes");
+  COOPT_REQUIRE(temperature > 0.0f, "temperature must be > 0 (greedy rows: coopt_accept_sample)");
+  COOPT_REQUIRE(!probs || probs_stride >= V, "probs_stride < V");
+  if (N == 0) return COOPT_OK;
+  COOPT_REQUIRE(logits && uniforms && tokens && workspace, "null pointer");
+  const size_t need = coopt_accept_sample_workspace(N, 0, V);
+  if (workspace_bytes < need) {
+    coopt::set_error("coopt_sample: workspace too small");
+    return COOPT_EWORKSPACE;
+  }
+  coopt::clear_error();
+  const bool bf16 = logits_dtype == COOPT_DT_BF16;
+  Args a{};
+  a.tgt = logits;
+  a.tgt_stride = row_stride;
+  a.u_res = uniforms;
+  a.out_tok = tokens;
+  a.margin = margin;
+  a.inv_t = 1.0f / temperature;
+  a.vec_t = coopt::aligned16(logits) && row_stride % (bf16 ? 8 : 4) == 0;
+  a.B = N;
+  a.gmax = 0;
+  a.V = V;
+  a.L = make_layout(N, 0, V);
+  carve(&a.ws, reinterpret_cast<uintptr_t>(workspace), N, 0, a.L);
+  const int vec_out = probs != nullptr && coopt::aligned16(probs) && probs_stride % 4 == 0;
+  auto s = static_cast<hipStream_t>(stream);
+  return bf16 ? launch_all<true>(a, false, s, probs, probs_stride, vec_out)
+              : launch_all<false>(a, false, s, probs, probs_stride, vec_out);
 }
 
 extern "C" int coopt_sample_probs(int logits_dtype, const void* logits, int64_t in_stride, int B,

@@ -157,6 +157,20 @@ __device__ __forceinline__ float wave_min_f32_dpp(float v) {
   return fminf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// Wave-wide fp32 maximum, every lane the same result (DPP and permlane swaps: no LDS round
+// trips, unlike a shuffle reduction).
+__device__ __forceinline__ float wave_max_f32_dpp(float v) {
+  v = fmaxf(v, dpp_f32<dpp::kXor1>(v));
+  v = fmaxf(v, dpp_f32<dpp::kXor2>(v));
+  v = fmaxf(v, dpp_f32<dpp::kRowHalfMirror>(v));
+  v = fmaxf(v, dpp_f32<dpp::kRowMirror>(v));
+  typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+  u2 r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // Inclusive fp64 prefix sum over the wave's lanes (lane 0 first): Hillis-Steele within each
 // 16-lane row, then the row totals carried forward with the row broadcasts.  `excl` gets the
 // previous lane's inclusive value (+0.0 in lane 0), bit for bit.

@@ -180,18 +180,22 @@ def sample(logits: torch.Tensor, temperature: float, generator=None, uniforms=No
     if not return_probs:
         res = accept(x, None, empty, temperature, u_resample=uniforms)
         return res.tokens[:, 0].long(), None
-    # the probabilities come from the row statistics the draw leaves in its workspace
+    # tokens and probabilities from one draw (coopt_sample: the row statistics, then one
+    # launch that writes the probabilities and draws from them)
     lib = _lib.load()
     V = x.shape[1]
     need = int(lib.coopt_accept_sample_workspace(N, 0, V))
     ws = _WS.get(need, x.device)
-    res = accept(x, None, empty, temperature, u_resample=uniforms, workspace=ws)
+    u = uniforms.to(device=x.device, dtype=torch.float32).contiguous()
+    if u.numel() < N:
+        raise ValueError("uniforms must have one entry per row")
+    tokens = torch.empty(N, dtype=torch.int32, device=x.device)
     probs = torch.empty(x.shape, dtype=torch.float32, device=x.device)
-    _lib.check(lib.coopt_sample_probs(_lib.dt_code(x.dtype), _lib.ptr(x), x.stride(0), N, V,
-                                      float(temperature), _lib.ptr(ws),
-                                      ws.numel() * ws.element_size(), _lib.ptr(probs), V,
-                                      _lib.stream_handle(x.device)), "coopt_sample_probs")
-    return res.tokens[:, 0].long(), probs
+    _lib.check(lib.coopt_sample(_lib.dt_code(x.dtype), _lib.ptr(x), x.stride(0), N, V,
+                                float(temperature), _lib.ptr(u), _lib.ptr(tokens), None,
+                                _lib.ptr(probs), V, _lib.ptr(ws), ws.numel() * ws.element_size(),
+                                _lib.stream_handle(x.device)), "coopt_sample")
+    return tokens.long(), probs
 
 
 def verify(target_logits: torch.Tensor, draft_tokens, draft_probs, temperature: float,

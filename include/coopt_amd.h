@@ -34,6 +34,8 @@
  *                           migrated block                  engine/block_manager.py:165-187
  *   coopt_softmax           torch.softmax(logits / T)       engine/spec_decode.py:16
  *   coopt_sample_probs      the same, for rows just sampled engine/spec_decode.py:16
+ *   coopt_sample            spec_decode.sample (tokens      engine/spec_decode.py:12-17
+ *                           and probabilities) at T > 0
  *   coopt_rms_norm          vLLM rms_norm / fused_add_rms_norm  engine/model.py:234, 236, 249, 254
  *   coopt_rope              vLLM rotary_embedding (neox)    engine/model.py:239
  *   coopt_silu_mul          vLLM silu_and_mul               engine/model.py:251-252
@@ -374,6 +376,19 @@ int coopt_softmax(int logits_dtype, const void* logits, int64_t in_stride, int64
 int coopt_sample_probs(int logits_dtype, const void* logits, int64_t in_stride, int B, int V,
                        float temperature, const void* workspace, size_t workspace_bytes,
                        float* probs, int64_t out_stride, coopt_stream_t stream);
+
+/*
+ * sample(logits, T) at T > 0 (engine/spec_decode.py:12-17) in two launches: tokens[r] is the
+ * inverse-CDF draw of uniforms[r] from softmax(logits[r] * (1/T)), the same rule and margin as
+ * coopt_accept_sample with gamma_max = 0 (which runs these launches too), and with probs
+ * non-NULL the probabilities are written by the same second launch (one read of the logits
+ * per launch, one write of the probabilities).  margin may be NULL.
+ * workspace_bytes >= coopt_accept_sample_workspace(N, 0, V).
+ */
+int coopt_sample(int logits_dtype, const void* logits, int64_t row_stride, int N, int V,
+                 float temperature, const float* uniforms, int32_t* tokens, float* margin,
+                 float* probs, int64_t probs_stride, void* workspace, size_t workspace_bytes,
+                 coopt_stream_t stream);
 
 /*
  * Elementwise stages of the Llama forward around the verify path (the model the step

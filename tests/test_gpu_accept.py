@@ -250,11 +250,39 @@ def test_softmax_layouts(dev, dtype, V, pad):
     ref = torch.softmax(x.double().cpu() / torch.tensor(0.8, dtype=torch.float32).double(), -1)
     assert torch.allclose(probs.double().cpu(), ref, rtol=1e-5, atol=1e-12)
     assert torch.allclose(probs.double().sum(-1).cpu(), torch.ones(5, dtype=torch.float64), atol=1e-5)
-    # sample()'s probabilities (coopt_sample_probs, from the draw's row statistics)
+    # sample()'s probabilities (coopt_sample: written by the launch that draws)
     u = torch.rand(5, generator=gen, device=dev)
     tok, sprobs = M.sample(x, 0.8, uniforms=u)
     assert torch.allclose(sprobs.double().cpu(), ref, rtol=1e-5, atol=1e-12)
     assert torch.equal(tok, M.sample(x, 0.8, uniforms=u, return_probs=False)[0])
+
+
+@pytest.mark.parametrize("N,V", [(1, 128256), (3, 128256), (2, 300000), (40, 50000)])
+def test_sample_rows_of_many_chunks(dev, N, V):
+    """sample() draws (coopt_sample) where one row spans more chunks than a wave has lanes
+    (1 row of 128256: 125 chunks; 2 of 300000: 293), and a batch of many rows: tokens against
+    the oracle's inverse CDF over the exactly rounded softmax (a differing row must be a tie
+    on the oracle's side), probabilities within 1e-5 relative, and tokens equal to a
+    gamma_max = 0 accept call's."""
+    gen = torch.Generator(device=dev).manual_seed(N * 7 + V)
+    x = torch.randn(N, V, generator=gen, device=dev) * 2.5
+    u = torch.rand(N, generator=gen, device=dev)
+    tok, probs = M.sample(x, 1.0, uniforms=u)
+    ref_tok, ref_p = OA.sample(x.cpu().numpy(), 1.0, u.cpu().numpy())
+    _, _, ref_m = OA.accept_batch(x.cpu().numpy()[:, None], None, np.zeros((N, 0), np.int32),
+                                  1.0, None, u.cpu().numpy())
+    t = tok.cpu().numpy()
+    for i in range(N):
+        if t[i] != ref_tok[i]:
+            report(f"[sample N={N} V={V}] row {i}: kernel {t[i]} oracle {ref_tok[i]} "
+                   f"oracle margin {ref_m[i]:.3g}")
+            assert ref_m[i] < TIE, f"row {i} differs outside a tie"
+    assert torch.allclose(probs.cpu(), torch.from_numpy(ref_p), rtol=1e-5, atol=1e-12)
+    res = M.accept(x, None, torch.empty((N, 0), dtype=torch.int32, device=dev), 1.0,
+                   u_resample=u)
+    assert torch.equal(res.tokens[:, 0].long(), tok)
+    assert int((res.accepted_len != 0).sum()) == 0
+    report(f"[sample N={N} V={V}] {int((t == ref_tok).sum())}/{N} rows equal to the oracle")
 
 
 def test_verify_signature_with_generator(dev):
