@@ -190,13 +190,24 @@ __device__ __forceinline__ T wave_shfl_xor(T v, int mask) {
   return __shfl_xor(v, mask, COOPT_WAVE);
 }
 
-// Max over aligned groups of `G` consecutive lanes (G a power of two <= 64).
+// Max over aligned groups of `G` consecutive lanes (G a power of two <= 64), every lane of a
+// group the same result: DPP inside a 16-lane row (quad swaps, then the half-row and row
+// mirrors), permlane swaps across rows -- VALU exchanges, no LDS round trip per step.
 template <int G>
 __device__ __forceinline__ uint32_t group_max_u32(uint32_t v) {
-#pragma unroll
-  for (int m = 1; m < G; m <<= 1) {
-    uint32_t o = __shfl_xor(v, m, COOPT_WAVE);
-    v = o > v ? o : v;
+  static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "G must be a power of two <= 64");
+  auto mx = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
+  if constexpr (G >= 2) v = mx(v, dpp_u32<dpp::kXor1>(v));
+  if constexpr (G >= 4) v = mx(v, dpp_u32<dpp::kXor2>(v));
+  if constexpr (G >= 8) v = mx(v, dpp_u32<dpp::kRowHalfMirror>(v));
+  if constexpr (G >= 16) v = mx(v, dpp_u32<dpp::kRowMirror>(v));
+  if constexpr (G >= 32) {
+    const u32x2_pl_t r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = mx(r[0], r[1]);
+  }
+  if constexpr (G >= 64) {
+    const u32x2_pl_t r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    v = mx(r[0], r[1]);
   }
   return v;
 }

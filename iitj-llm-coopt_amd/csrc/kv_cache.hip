@@ -292,8 +292,8 @@ struct CacheSet {
 // Nothing in a slab branches: a load under a branch is waited for where the branch joins,
 // and the compiler sinks a load into the branch of its only store.  So a chunk index past
 // the block stands for the same chunk of the block's first vector (its G-lane group stays
-// whole) and that lane stores the same bytes as the lane that owns the chunk, and every lane
-// of a vector stores its (identical) scale.
+// whole) and that lane stores the same bytes as the lane that owns the chunk; a vector's
+// scale is stored by its chunk-0 lane (a store under a branch holds nothing up).
 // Chunk idx of a block is (token t, head h, chunk c) with idx = (t * Hkv + h) * G + c, the
 // order of the swapped rows, so the swapped side is read or written contiguously.
 constexpr int kSwapThreads = 256;
@@ -333,13 +333,14 @@ __device__ __forceinline__ QuantChunk quant_chunk(const uint32_t (&w)[4]) {
   for (int e = 0; e < 4; ++e) amax = max(amax, max(w[e] & 0x7fffu, (w[e] >> 16) & 0x7fffu));
   amax = group_max_u32<G>(amax);
   const float s32 = quant_scale<QMAX>(bf16_to_f32(static_cast<uint16_t>(amax)));
-  int code[8];
-  quant_codes8<QMAX>(w, s32, code);
   QuantChunk r{0, 0, f32_to_f16(s32)};
   if constexpr (BITS == 8) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) (e < 4 ? r.lo : r.hi) |= (static_cast<uint32_t>(code[e]) & 0xffu) << (8 * (e & 3));
+    const uint2 p = quant_pack8_i8(w, s32);
+    r.lo = p.x;
+    r.hi = p.y;
   } else {
+    int code[8];
+    quant_codes8<QMAX>(w, s32, code);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       r.lo |= ((static_cast<uint32_t>(code[2 * j] + 8) | (static_cast<uint32_t>(code[2 * j + 1] + 8) << 4)) & 0xffu) << (8 * j);
@@ -398,7 +399,7 @@ __global__ __launch_bounds__(kSwapThreads) void swap_out_kernel(
       if constexpr (kOut == 16) *reinterpret_cast<uint4*>(qo) = make_uint4(0, 0, 0, 0);
       else if constexpr (kOut == 8) *reinterpret_cast<uint2*>(qo) = make_uint2(0, 0);
       else *reinterpret_cast<uint32_t*>(qo) = 0;
-      if (BITS != 16) scale[idx / G] = 0;
+      if (BITS != 16 && idx % G == 0) scale[idx / G] = 0;
     }
     return;
   }
@@ -426,7 +427,7 @@ __global__ __launch_bounds__(kSwapThreads) void swap_out_kernel(
     unsigned char* qo = q + static_cast<int64_t>(idx) * kOut;
     if constexpr (SRC8) {
       *reinterpret_cast<uint2*>(qo) = make_uint2(x[u].x, x[u].y);
-      scale[idx / G] = xs[u];
+      if (idx % G == 0) scale[idx / G] = xs[u];
     } else if constexpr (BITS == 16) {
       *reinterpret_cast<uint4*>(qo) = make_uint4(x[u].x, x[u].y, x[u].z, x[u].w);
     } else {
@@ -434,7 +435,7 @@ __global__ __launch_bounds__(kSwapThreads) void swap_out_kernel(
       const QuantChunk r = quant_chunk<G, BITS>(w);
       if constexpr (BITS == 8) *reinterpret_cast<uint2*>(qo) = make_uint2(r.lo, r.hi);
       else *reinterpret_cast<uint32_t*>(qo) = r.lo;
-      scale[idx / G] = r.scale;
+      if (idx % G == 0) scale[idx / G] = r.scale;
     }
   }
 }
@@ -509,7 +510,7 @@ __global__ __launch_bounds__(kSwapThreads) void quantize_rows_kernel(
     unsigned char* qo = q + static_cast<int64_t>(idx) * kOut;
     if constexpr (BITS == 8) *reinterpret_cast<uint2*>(qo) = make_uint2(r.lo, r.hi);
     else *reinterpret_cast<uint32_t*>(qo) = r.lo;
-    scale[idx / G] = r.scale;
+    if (idx % G == 0) scale[idx / G] = r.scale;
   }
 }
 

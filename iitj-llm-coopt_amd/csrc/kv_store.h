@@ -62,6 +62,40 @@ __device__ __forceinline__ void quant_codes8(const uint32_t (&w)[4], float s32, 
     code[e] = static_cast<int>(fminf(fmaxf(r[e], -static_cast<float>(QMAX)), static_cast<float>(QMAX)));
 }
 
+// quant_codes8<127> of the 8 bf16 elements in w[0..3], returned as the packed INT8 codes
+// (element e in byte e % 4 of word e / 4).  The code is formed in the low byte of a float:
+// for |r| <= 127, fp32(r + 1.5 * 2^23) rounds r to the nearest integer, ties to even (the
+// sum lies in [2^23, 2^24), where the ulp is 1) and holds it, two's complement, in the low
+// mantissa bits, so one add replaces rint, the float-to-int conversion and the masking.
+// q is clamped to +-127 before rounding, which for integer bounds equals clamping the
+// rounded value.  Same codes as quant_codes8<127>, ties and non-finite inputs included.
+__device__ __forceinline__ uint2 quant_pack8_i8(const uint32_t (&w)[4], float s32) {
+  constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23
+  const float r32 = __builtin_amdgcn_rcpf(s32);
+  float x[8], f[8];
+  bool near = false;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    x[e] = bf16_to_f32(static_cast<uint16_t>(w[e / 2] >> (16 * (e & 1))));
+    const float q = fminf(fmaxf(x[e] * r32, -127.0f), 127.0f);
+    f[e] = q + kMagic;
+    near |= fabsf(q - (f[e] - kMagic)) >= 0.5f - kNearTie;
+  }
+  if (near) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = fminf(fmaxf(x[e] / s32, -127.0f), 127.0f) + kMagic;
+  }
+  uint32_t b[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) b[e] = __float_as_uint(f[e]);
+  // bytes 0 of four words: perm selects from {hi:lo} (lo bytes 0-3, hi bytes 4-7); 0x0c = 0
+  const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u) |
+                      __builtin_amdgcn_perm(b[3], b[2], 0x04000c0cu);
+  const uint32_t hi = __builtin_amdgcn_perm(b[5], b[4], 0x0c0c0400u) |
+                      __builtin_amdgcn_perm(b[7], b[6], 0x04000c0cu);
+  return make_uint2(lo, hi);
+}
+
 // ---------------------------------------------------------------------------------------
 // KV write.  One lane per 16-byte chunk (8 bf16) of a (token, head) vector; G = D/8 lanes
 // (an aligned power-of-two group inside the wave) cover one vector, and each lane handles
@@ -93,17 +127,8 @@ __device__ __forceinline__ void store_kv_chunk(uint4 kr, uint4 vr, void* kc, voi
     vmax = group_max_u32<G>(vmax);
     const float ksc = quant_scale<127>(bf16_to_f32(static_cast<uint16_t>(kmax)));
     const float vsc = quant_scale<127>(bf16_to_f32(static_cast<uint16_t>(vmax)));
-    int kcode[8], vcode[8];
-    quant_codes8<127>(kw, ksc, kcode);
-    quant_codes8<127>(vw, vsc, vcode);
-    uint32_t kq[2] = {0, 0}, vq[2] = {0, 0};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      kq[i / 4] |= (static_cast<uint32_t>(kcode[i]) & 0xffu) << (8 * (i & 3));
-      vq[i / 4] |= (static_cast<uint32_t>(vcode[i]) & 0xffu) << (8 * (i & 3));
-    }
-    *reinterpret_cast<uint2*>(static_cast<int8_t*>(kc) + c_off) = make_uint2(kq[0], kq[1]);
-    *reinterpret_cast<uint2*>(static_cast<int8_t*>(vc) + c_off) = make_uint2(vq[0], vq[1]);
+    *reinterpret_cast<uint2*>(static_cast<int8_t*>(kc) + c_off) = quant_pack8_i8(kw, ksc);
+    *reinterpret_cast<uint2*>(static_cast<int8_t*>(vc) + c_off) = quant_pack8_i8(vw, vsc);
     if (c == 0) {
       ks[s_off] = f32_to_f16(ksc);
       vs[s_off] = f32_to_f16(vsc);
