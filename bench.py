@@ -832,9 +832,15 @@ def summarize(paths):
         d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
         trace.setdefault(key, []).append(d)
     if trace:
+        # every launch shape of the library's kernels and the GEMMs; torch's own set-up kernels
+        # (fills, copies, random draws) only among the first ten by total time
+        ranked = sorted(trace.items(), key=lambda kv: -sum(kv[1]))
+        shown = [kv for i, kv in enumerate(ranked)
+                 if i < 10 or not kv[0][0].startswith(("at::", "__amd_rocclr", "elementwise_kernel",
+                                                       "c10::", "std::"))]
         print("| kernel | grid (threads) | wg | calls | avg us | min us | max us | total ms |")
         print("|---|---|---|---|---|---|---|---|")
-        for (k, grid, wg), ds in sorted(trace.items(), key=lambda kv: -sum(kv[1]))[:40]:
+        for (k, grid, wg), ds in shown:
             print(f"| `{k}` | {grid} | {wg} | {len(ds)} | {sum(ds) / len(ds):.1f} | "
                   f"{min(ds):.1f} | {max(ds):.1f} | {sum(ds) / 1e3:.2f} |")
     agg = {}
