@@ -299,6 +299,9 @@ struct CacheSet {
 constexpr int kSwapThreads = 256;
 constexpr int kSwapOutU = 4;
 constexpr int kSwapInU = 2;
+// Two-chunks-a-lane forms (INT8 out of bf16): pairs per thread of swap_out and of the codec.
+constexpr int kSwapPairOutU = 4;
+constexpr int kCodecPairU = 2;
 constexpr int64_t kSwapSmallGrid = 2048;
 
 template <int N>
@@ -346,6 +349,29 @@ __device__ __forceinline__ QuantChunk quant_chunk(const uint32_t (&w)[4]) {
       r.lo |= ((static_cast<uint32_t>(code[2 * j] + 8) | (static_cast<uint32_t>(code[2 * j + 1] + 8) << 4)) & 0xffu) << (8 * j);
   }
   return r;
+}
+
+// INT8 codes of two adjacent chunks (16 elements, words of a and b) of a vector covered by
+// G2 lanes, two chunks a lane: the codes and scale quant_chunk<2 G2, 8> gives the two chunks'
+// lanes, as one 16-byte word.  Every lane of the group must call it together.
+struct QuantPair {
+  uint4 codes;
+  uint16_t scale;
+};
+template <int G2>
+__device__ __forceinline__ QuantPair quant_pair8(const uint4& a, const uint4& b) {
+  const uint32_t w0[4] = {a.x, a.y, a.z, a.w};
+  const uint32_t w1[4] = {b.x, b.y, b.z, b.w};
+  uint32_t amax = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    amax = max(amax, max(w0[e] & 0x7fffu, (w0[e] >> 16) & 0x7fffu));
+    amax = max(amax, max(w1[e] & 0x7fffu, (w1[e] >> 16) & 0x7fffu));
+  }
+  amax = group_max_u32<G2>(amax);
+  const float s32 = quant_scale<127>(bf16_to_f32(static_cast<uint16_t>(amax)));
+  const uint2 p0 = quant_pack8_i8(w0, s32), p1 = quant_pack8_i8(w1, s32);
+  return QuantPair{make_uint4(p0.x, p0.y, p1.x, p1.y), f32_to_f16(s32)};
 }
 
 // bf16(float(code) * float(scale)) of one chunk's 8 codes (INT8 in lo / hi, or INT4 nibbles
@@ -440,6 +466,53 @@ __global__ __launch_bounds__(kSwapThreads) void swap_out_kernel(
   }
 }
 
+// swap_out of bf16 caches at 8 bits with two chunks a lane (G2 = G / 2 lanes a vector): a lane
+// loads 32 contiguous bytes of its vector and stores its 16 codes as one 16-byte word.  Same
+// slab scheme, wrap rule and output as swap_out_kernel<2 G2, 8, false>.  32 layers' K and V of
+// a 4096-token sequence: 179 -> 163 us against one chunk a lane.
+template <int G2, int U = kSwapPairOutU>
+__global__ __launch_bounds__(kSwapThreads) void swap_out_pair_kernel(
+    CacheSet cs, int64_t c_bs, int64_t c_ts, int64_t c_hs, const int64_t* __restrict__ ids,
+    int slabs, int bs, int Hkv, int64_t num_blocks, unsigned char* __restrict__ q,
+    uint16_t* __restrict__ scale, int64_t q_stride, int64_t s_stride) {
+  const uint16_t* __restrict__ cache = static_cast<const uint16_t*>(cs.c[blockIdx.y]);
+  const int i = static_cast<int>(blockIdx.x) / slabs;
+  const int base = (static_cast<int>(blockIdx.x) - i * slabs) * (U * kSwapThreads);
+  const int per_blk = bs * Hkv;
+  const int npair = per_blk * G2;
+  const int64_t vec0 = static_cast<int64_t>(i) * per_blk;
+  q += blockIdx.y * q_stride + vec0 * G2 * 16;
+  scale += blockIdx.y * s_stride + vec0;
+  const int64_t blk = ids[i];
+  if (blk < 0 || blk >= num_blocks) {  // uniform: the block's rows read as zeros
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int idx = swap_chunk<G2>(base, u, npair);
+      *reinterpret_cast<uint4*>(q + static_cast<int64_t>(idx) * 16) = make_uint4(0, 0, 0, 0);
+      if (idx % G2 == 0) scale[idx / G2] = 0;
+    }
+    return;
+  }
+  uint4 xa[U], xb[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int idx = swap_chunk<G2>(base, u, npair);
+    const int v = idx / G2, c = idx % G2;
+    const int t = v / Hkv, h = v - t * Hkv;
+    const uint16_t* src = cache + blk * c_bs + t * c_ts + h * c_hs + c * 16;
+    xa[u] = *reinterpret_cast<const uint4*>(src);
+    xb[u] = *reinterpret_cast<const uint4*>(src + 8);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // as in swap_out_kernel
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int idx = swap_chunk<G2>(base, u, npair);
+    const QuantPair r = quant_pair8<G2>(xa[u], xb[u]);
+    *reinterpret_cast<uint4*>(q + static_cast<int64_t>(idx) * 16) = r.codes;
+    if (idx % G2 == 0) scale[idx / G2] = r.scale;
+  }
+}
+
 template <int G, int BITS, bool DST8, int U = kSwapInU>
 __global__ __launch_bounds__(kSwapThreads) void swap_in_kernel(
     const unsigned char* __restrict__ q, const uint16_t* __restrict__ scale, int64_t q_stride,
@@ -514,6 +587,30 @@ __global__ __launch_bounds__(kSwapThreads) void quantize_rows_kernel(
   }
 }
 
+// quantize_rows_kernel at 8 bits with two chunks a lane (G2 = D / 16 lanes a row, 16-byte
+// code stores), over pair idx = row * G2 + c.  64 MiB of bf16 rows: 23.4 -> 22.1 us.
+template <int G2, int U = kCodecPairU>
+__global__ __launch_bounds__(kSwapThreads) void quantize_rows_pair_kernel(
+    const uint16_t* __restrict__ x, int npair, unsigned char* __restrict__ q,
+    uint16_t* __restrict__ scale) {
+  const int base = static_cast<int>(blockIdx.x) * (U * kSwapThreads);
+  uint4 xa[U], xb[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint16_t* src = x + static_cast<int64_t>(swap_chunk<G2>(base, u, npair)) * 16;
+    xa[u] = *reinterpret_cast<const uint4*>(src);
+    xb[u] = *reinterpret_cast<const uint4*>(src + 8);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // as in swap_out_kernel
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int idx = swap_chunk<G2>(base, u, npair);
+    const QuantPair r = quant_pair8<G2>(xa[u], xb[u]);
+    *reinterpret_cast<uint4*>(q + static_cast<int64_t>(idx) * 16) = r.codes;
+    if (idx % G2 == 0) scale[idx / G2] = r.scale;
+  }
+}
+
 template <int G, int BITS, int U = kSwapInU>
 __global__ __launch_bounds__(kSwapThreads) void dequantize_rows_kernel(
     const unsigned char* __restrict__ q, const uint16_t* __restrict__ scale, int nchunk,
@@ -557,6 +654,23 @@ bool launch_rows_codec(bool quant, int bits, const void* x, int64_t rows, int D,
       (reinterpret_cast<uintptr_t>(scale) & 1u) != 0)
     return false;
   const int n = static_cast<int>(nchunk);
+  if (quant && bits == 8 && G >= 2 && (reinterpret_cast<uintptr_t>(q) & 15u) == 0) {
+    // two chunks a lane (16-byte code stores); 16-byte aligned codes
+    const int np = n / 2;
+    const dim3 g2(static_cast<unsigned>((np + kCodecPairU * kSwapThreads - 1) / (kCodecPairU * kSwapThreads)));
+    const uint16_t* xp = static_cast<const uint16_t*>(x);
+    unsigned char* qp = static_cast<unsigned char*>(q);
+    uint16_t* sp = static_cast<uint16_t*>(const_cast<void*>(scale));
+    switch (G / 2) {
+      case 1: hipLaunchKernelGGL((quantize_rows_pair_kernel<1>), g2, dim3(kSwapThreads), 0, s, xp, np, qp, sp); return true;
+      case 2: hipLaunchKernelGGL((quantize_rows_pair_kernel<2>), g2, dim3(kSwapThreads), 0, s, xp, np, qp, sp); return true;
+      case 4: hipLaunchKernelGGL((quantize_rows_pair_kernel<4>), g2, dim3(kSwapThreads), 0, s, xp, np, qp, sp); return true;
+      case 8: hipLaunchKernelGGL((quantize_rows_pair_kernel<8>), g2, dim3(kSwapThreads), 0, s, xp, np, qp, sp); return true;
+      case 16: hipLaunchKernelGGL((quantize_rows_pair_kernel<16>), g2, dim3(kSwapThreads), 0, s, xp, np, qp, sp); return true;
+      case 32: hipLaunchKernelGGL((quantize_rows_pair_kernel<32>), g2, dim3(kSwapThreads), 0, s, xp, np, qp, sp); return true;
+      default: break;
+    }
+  }
 #define COOPT_RC(GV)                                                                               \
   case GV:                                                                                         \
     if (quant) {                                                                                   \
@@ -609,6 +723,33 @@ int launch_swap(bool out, int G, const CacheSet& cs, int n, int64_t c_bs, int64_
   const int64_t slabs = (chunks + U * kSwapThreads - 1) / (U * kSwapThreads);
   COOPT_REQUIRE(chunks <= INT32_MAX && static_cast<int64_t>(nid) * slabs <= INT32_MAX,
                 "swap too large for one launch");
+  if constexpr (BITS == 8 && !I8) {
+    // bf16 caches out at 8 bits, launches large enough for U > 1 chunks a thread and 16-byte
+    // aligned rows: two chunks a lane (swap_out_pair_kernel)
+    if (out && U != 1 && G >= 2 && (reinterpret_cast<uintptr_t>(q) & 15u) == 0) {
+      const int64_t sl2 = (chunks / 2 + kSwapPairOutU * kSwapThreads - 1) / (kSwapPairOutU * kSwapThreads);
+      const dim3 g2(static_cast<unsigned>(nid * sl2), static_cast<unsigned>(n));
+      const int s2 = static_cast<int>(sl2);
+      unsigned char* qp = static_cast<unsigned char*>(q);
+      uint16_t* sp = static_cast<uint16_t*>(scale);
+#define COOPT_SWP(GV)                                                                             \
+  case GV:                                                                                        \
+    hipLaunchKernelGGL((swap_out_pair_kernel<GV / 2>), g2, dim3(kSwapThreads), 0, stream, cs, c_bs, \
+                       c_ts, c_hs, ids, s2, bs, Hkv, num_blocks, qp, sp, q_stride, s_stride);      \
+    return coopt::check_launch("coopt_kv_swap_out");
+      switch (G) {
+        COOPT_SWP(2)
+        COOPT_SWP(4)
+        COOPT_SWP(8)
+        COOPT_SWP(16)
+        COOPT_SWP(32)
+        COOPT_SWP(64)
+        default:
+          break;
+      }
+#undef COOPT_SWP
+    }
+  }
   const dim3 grid(static_cast<unsigned>(nid * slabs), static_cast<unsigned>(n));
   const int sl = static_cast<int>(slabs);
 #define COOPT_SW_U(GV, UO, UI)                                                                    \

@@ -229,6 +229,29 @@ def test_codec_row_kernels_bit_exact(dev, bits, T, H, D):
     assert torch.equal(q2, q) and torch.equal(s2, s)
 
 
+@pytest.mark.parametrize("T,D", [(30001, 128), (40001, 64), (140001, 16)])
+def test_codec_int8_codes_at_8_byte_alignment(dev, T, D):
+    """INT8 codes written to an 8-byte- but not 16-byte-aligned buffer (the C-ABI allows it):
+    the row codec's one-chunk-a-lane form, equal to the 16-byte-store form an aligned buffer
+    gets and to the reference lines."""
+    from iitj_llm_coopt_amd import _lib
+
+    gen = torch.Generator(device=dev).manual_seed(D)
+    x = bf16_kv(gen, T, 8, D, dev)   # enough rows for the row codec at every D
+    q, s = M.quantize(x, 8)
+    rq, rs = reference_quantize_on_device(x, 8)
+    assert torch.equal(q, rq) and torch.equal(s, rs)
+    buf = torch.zeros(q.numel() + 16, dtype=torch.int8, device=dev)
+    assert buf.data_ptr() % 16 == 0
+    q8 = buf[8:8 + q.numel()].view_as(q)
+    s8 = torch.empty_like(s)
+    lib = _lib.load()
+    _lib.check(lib.coopt_quantize(8, _lib.DT_BF16, _lib.ptr(x), x.numel() // D, D, _lib.ptr(q8),
+                                  _lib.ptr(s8), _lib.stream_handle(dev)), "coopt_quantize")
+    assert torch.equal(q8, q) and torch.equal(s8, s)
+    assert not buf[:8].any() and not buf[8 + q.numel():].any()
+
+
 def test_codec_bits16_is_passthrough(dev):
     x = torch.randn(3, 128, device=dev).to(torch.bfloat16)
     q, s = M.quantize(x, 16)

@@ -270,3 +270,26 @@ def test_wide_swap_matches_reference_lines(dev, kv, bits, H, D):
         one, _, one_s, _ = M.allocate_kv_cache(NB, BS, H, D, kv, device=dev)
         M.swap_in_blocks(q[i], None if s is None else s[i], bits, ids, one, one_s)
         assert torch.equal(tgt[i].view(torch.uint8), one.view(torch.uint8)), i
+
+
+@pytest.mark.parametrize("H,D", [(8, 128), (3, 128)])
+def test_wide_swap_out_into_8_byte_aligned_rows(dev, H, D):
+    """bf16 caches out at 8 bits into a buffer 8 bytes off 16-byte alignment (the C-ABI allows
+    8): the one-chunk-a-lane kernel, equal to the two-chunks-a-lane form an aligned buffer
+    gets (16-byte code stores), which the reference-line test above checks."""
+    NB, BS, n = 48, 16, 64
+    ids = torch.from_numpy(np.random.default_rng(D + H).permutation(NB)[:40].astype(np.int64)).to(dev)
+    ids[5] = -1
+    caches = []
+    for i in range(n):
+        kc, _, _, _ = M.allocate_kv_cache(NB, BS, H, D, "auto", device=dev)
+        kc.copy_(kv_values((NB, BS, H, D), dev, seed=500 + i))
+        caches.append(kc)
+    q, s = M.swap_out_caches(caches, ids, 8)
+    buf = torch.zeros(q.numel() + 16, dtype=torch.int8, device=dev)
+    assert buf.data_ptr() % 16 == 0
+    q8 = buf[8:8 + q.numel()].view(q.shape)
+    q2, s2 = M.swap_out_caches(caches, ids, 8, out=q8)
+    assert q2.data_ptr() % 16 == 8
+    assert torch.equal(q2, q) and torch.equal(s2, s)
+    assert not buf[:8].any() and not buf[8 + q.numel():].any()
