@@ -96,6 +96,29 @@ __device__ __forceinline__ uint2 quant_pack8_i8(const uint32_t (&w)[4], float s3
   return make_uint2(lo, hi);
 }
 
+// INT8 codes of two adjacent chunks (16 elements, words of a and b) of a vector covered by
+// G2 lanes, two chunks a lane: the codes and scale quant_chunk<2 G2, 8> gives the two chunks'
+// lanes, as one 16-byte word.  Every lane of the group must call it together.
+struct QuantPair {
+  uint4 codes;
+  uint16_t scale;
+};
+template <int G2>
+__device__ __forceinline__ QuantPair quant_pair8(const uint4& a, const uint4& b) {
+  const uint32_t w0[4] = {a.x, a.y, a.z, a.w};
+  const uint32_t w1[4] = {b.x, b.y, b.z, b.w};
+  uint32_t amax = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    amax = max(amax, max(w0[e] & 0x7fffu, (w0[e] >> 16) & 0x7fffu));
+    amax = max(amax, max(w1[e] & 0x7fffu, (w1[e] >> 16) & 0x7fffu));
+  }
+  amax = group_max_u32<G2>(amax);
+  const float s32 = quant_scale<127>(bf16_to_f32(static_cast<uint16_t>(amax)));
+  const uint2 p0 = quant_pack8_i8(w0, s32), p1 = quant_pack8_i8(w1, s32);
+  return QuantPair{make_uint4(p0.x, p0.y, p1.x, p1.y), f32_to_f16(s32)};
+}
+
 // ---------------------------------------------------------------------------------------
 // KV write.  One lane per 16-byte chunk (8 bf16) of a (token, head) vector; G = D/8 lanes
 // (an aligned power-of-two group inside the wave) cover one vector, and each lane handles

@@ -118,6 +118,34 @@ def test_kv_write_int8_config2_bit_exact(dev):
     report(f"[kv-int8] T={T}: codes+scales bit-exact vs torch-on-GPU and oracle")
 
 
+@pytest.mark.parametrize("D", [128, 64])
+def test_kv_write_int8_into_8_byte_aligned_rows(dev, D):
+    """INT8 caches whose rows are 8- but not 16-byte aligned (a view 8 bytes into a buffer,
+    which the C-ABI allows) and aligned ones: both equal the reference lines, and nothing
+    outside the written rows changes."""
+    NB, BS, H, T = 32, 16, 8, 300
+    gen = torch.Generator(device=dev).manual_seed(D)
+    k, v = bf16_kv(gen, T, H, D, dev), bf16_kv(gen, T, H, D, dev)
+    slots = torch.randperm(NB * BS, generator=gen, device=dev)[:T]
+    rq_k, rs_k = reference_quantize_on_device(k, 8)
+    rq_v, rs_v = reference_quantize_on_device(v, 8)
+    n = NB * BS * H * D
+    for shift in (0, 8):
+        kbuf = torch.zeros(n + 16, dtype=torch.int8, device=dev)
+        vbuf = torch.zeros(n + 16, dtype=torch.int8, device=dev)
+        kc = kbuf[shift:shift + n].view(NB, BS, H, D)
+        vc = vbuf[shift:shift + n].view(NB, BS, H, D)
+        assert kc.data_ptr() % 16 == shift
+        ks = torch.zeros(NB, BS, H, dtype=torch.float16, device=dev)
+        vs = torch.zeros_like(ks)
+        M.reshape_and_cache_flash(k, v, kc, vc, slots, "int8", ks, vs)
+        blk, off = slots // BS, slots % BS
+        assert torch.equal(kc[blk, off], rq_k) and torch.equal(vc[blk, off], rq_v), shift
+        assert torch.equal(ks[blk, off], rs_k) and torch.equal(vs[blk, off], rs_v), shift
+        assert int((kc != 0).sum()) == int((rq_k != 0).sum()), shift
+        assert not kbuf[:shift].any() and not kbuf[shift + n:].any(), shift
+
+
 def test_kv_write_int8_edge_vectors(dev):
     """zeros -> scale 0 and codes 0; amax 127 -> scale exactly 1 and .5 ties to even;
     a single x20 outlier crushes the rest; |x| = amax -> +-127."""
