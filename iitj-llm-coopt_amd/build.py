@@ -26,6 +26,10 @@ ARCH = "gfx950"
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # the first 16 dwords of a kernel's scalar arguments arrive in SGPRs, so a kernel's first
+    # loads do not wait for a kernel-argument load (a compatibility prologue loads them where
+    # the firmware does not preload)
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall", "-Wno-unused-function", "-Wno-unknown-pragmas",
 ]
 

@@ -49,6 +49,10 @@ struct LinArgs {
   int force_part;    // write fp32 partials even for a single K slice
 };
 
+// linear_kernel's scalar arguments, in order, from a LinArgs
+#define LIN_ARGS(a) (a).x, (a).ldx, (a).w, (a).ldw, (a).M, (a).N, (a).K, (a).kt, (a).y, (a).ldy, \
+                    (a).part, (a).force_part
+
 __device__ __forceinline__ f32x4_t mfma_bf16(u32x4_t a, u32x4_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
@@ -62,8 +66,15 @@ __device__ __forceinline__ u32x4_t ldg16(const uint16_t* p) {
 // PF: K steps of W in flight per wave (even); PK: W is tile-packed; SILU: W is a gate_up
 // weight packed with gate and up tiles interleaved (coopt_linear_pack_gate_up), K is not
 // split, and the output is silu(gate) * up (F = N / 2 columns) instead of the projection.
+// The arguments are scalars, not a LinArgs by value: the first sixteen kernel-argument dwords
+// (x through ldy) are then preloaded into SGPRs (the build's kernarg-preload option), so the
+// first X / W loads do not wait for a kernel-argument load; part and force_part, needed only
+// at the end, load from the segment.
 template <int MT, int NW, int WAVES, int PF, bool PK, bool SILU = false>
-__global__ __launch_bounds__(64 * WAVES) void linear_kernel(LinArgs a) {
+__global__ __launch_bounds__(64 * WAVES) void linear_kernel(
+    const uint16_t* x, int64_t ldx, const uint16_t* w, int64_t ldw, int M, int N, int K, int kt,
+    uint16_t* y, int64_t ldy, float* part, int force_part) {
+  const LinArgs a{x, ldx, w, ldw, M, N, K, kt, y, ldy, part, force_part};
   static_assert(!SILU || (PK && NW == 1 && WAVES % 2 == 0), "gate / up tile pairs per wave pair");
   static_assert(PF % 2 == 0, "the step loop is unrolled by PF and alternates X buffers");
   constexpr int kThreads = 64 * WAVES;
@@ -318,9 +329,9 @@ void launch_cfg(const Plan& p, const LinArgs& a, bool packed, hipStream_t s) {
   const int cols = WAVES * NW * 16;
   const dim3 grid((a.N + cols - 1) / cols, p.ks);
   if (packed)
-    hipLaunchKernelGGL((linear_kernel<MT, NW, WAVES, PF, true>), grid, dim3(64 * WAVES), 0, s, a);
+    hipLaunchKernelGGL((linear_kernel<MT, NW, WAVES, PF, true>), grid, dim3(64 * WAVES), 0, s, LIN_ARGS(a));
   else
-    hipLaunchKernelGGL((linear_kernel<MT, NW, WAVES, PF, false>), grid, dim3(64 * WAVES), 0, s, a);
+    hipLaunchKernelGGL((linear_kernel<MT, NW, WAVES, PF, false>), grid, dim3(64 * WAVES), 0, s, LIN_ARGS(a));
 }
 
 template <int MT>
@@ -442,7 +453,7 @@ void launch_silu(int F, const LinArgs& a, hipStream_t s) {
   // the weight read clamped tiles and write nothing (their columns are >= F)
   const int rows = 16 * WAVES;
   hipLaunchKernelGGL((linear_kernel<MT, 1, WAVES, 2, true, true>), dim3((2 * F + rows - 1) / rows, 1),
-                     dim3(64 * WAVES), 0, s, a);
+                     dim3(64 * WAVES), 0, s, LIN_ARGS(a));
 }
 
 }  // namespace

@@ -117,6 +117,14 @@ struct AttnArgs {
   const int64_t* slots;
 };
 
+// verify_attn_kernel's leading scalar arguments: the fields its first load round needs (row
+// range, key count, the first tile's pages) and the launch mode (0 a grid of (split, KV head,
+// sequence), 1 ordered items (plan), 2 query windows).  As scalars ahead of the AttnArgs they are
+// preloaded into SGPRs (the build's kernarg-preload option), so that round does not wait for a
+// kernel-argument load; the rest of AttnArgs loads alongside it.
+#define ATTN_LEAD(a) (a).cu, (a).seq_lens, (a).bt, (a).bt_stride, (a).split, (a).bs_shift, \
+                     ((a).plan ? 1 : ((a).nwin > 0 ? 2 : 0))
+
 // Partials of a fused epilogue are reduced with a compile-time slice bound (every load
 // unconditional, see Partials4); launches with more slices are rejected on the host.
 constexpr int kQkvMaxSlices = 4;
@@ -244,7 +252,9 @@ __device__ void plan_item(const AttnArgs& a, int lane, int* out) {
 // (a run-time choice of input made the compiler wait for every earlier load where the two
 // input paths joined).
 template <int D, bool INT8, int RT, bool SC, int FUSED>
-__global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(
+    const int32_t* cu_p, const int32_t* sl_p, const int32_t* bt_p, int64_t bt_stride, int split,
+    int bs_shift, int mode, AttnArgs a) {
   using Raw = RawTile<D, INT8>;
   constexpr int kWaves = waves_for(RT);
   constexpr int kBlock = 64 * kWaves;
@@ -286,15 +296,15 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
   // the wave-uniform page lookups be scalar loads, which do not wait behind (or drain) the
   // wave's outstanding K/V vector loads.
   typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
-  const int64_t bt_last = a.bt_stride - 1;
+  const int64_t bt_last = bt_stride - 1;
   // The pages of the wave's first tile of piece sidx of sequence b, looked up before L is
   // known: they are used only if that tile is full, i.e. all its keys are < L, where no
   // clamp to L - 1 applies (the index is kept inside the table row regardless).
   auto first_pages = [&](int b, int sidx, int32_t& p0, int32_t& p1) {
-    const const_i32_ptr tb = (const_i32_ptr)(a.bt + static_cast<int64_t>(b) * a.bt_stride);
-    const int kb = sidx * a.split + wave * kTileKeys;
-    p0 = tb[min<int64_t>(kb >> a.bs_shift, bt_last)];
-    p1 = tb[min<int64_t>((kb + 16) >> a.bs_shift, bt_last)];
+    const const_i32_ptr tb = (const_i32_ptr)(bt_p + static_cast<int64_t>(b) * bt_stride);
+    const int kb = sidx * split + wave * kTileKeys;
+    p0 = tb[min<int64_t>(kb >> bs_shift, bt_last)];
+    p1 = tb[min<int64_t>((kb + 16) >> bs_shift, bt_last)];
   };
 
   // One piece: keys [sidx * split, min(L, (sidx + 1) * split)) of (sequence b, KV head hkv)
@@ -302,17 +312,17 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
   // the wave's first tile (first_pages).
   auto run_piece = [&](const int b, const int hkv, const int sidx, const int q0, const int n,
                        const int L, const int32_t pg0, const int32_t pg1) {
-  const const_i32_ptr table = (const_i32_ptr)(a.bt + static_cast<int64_t>(b) * a.bt_stride);
-  const int k_begin = sidx * a.split;
+  const const_i32_ptr table = (const_i32_ptr)(bt_p + static_cast<int64_t>(b) * bt_stride);
+  const int k_begin = sidx * split;
   const int64_t first_pg0 = clamp_page(pg0, a.num_blocks);
   const int64_t first_pg1 = clamp_page(pg1, a.num_blocks);
   if (n <= 0) return;
-  const int nsplit = L > 0 ? (L + a.split - 1) / a.split : 1;
+  const int nsplit = L > 0 ? (L + split - 1) / split : 1;
   if (sidx >= nsplit) return;
   const int R = min(min(a.G * n, kRows), a.rmax);
-  const int k_end = min(L, k_begin + a.split);
+  const int k_end = min(L, k_begin + split);
 
-  const int bs_mask = (1 << a.bs_shift) - 1;
+  const int bs_mask = (1 << bs_shift) - 1;
 
   // ---- Q rows (into LDS by stage_q, once the first tile's loads are issued), causal limits ----
   // Row r of the block is query head hkv*G + r/n at query row j = r % n; rows >= R are 0.
@@ -342,7 +352,7 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
     const int nq = a.G * n, nvec = nq + n;
     const int Hq = a.G * a.Hkv;
     const int width = (Hq + 2 * a.Hkv) * D;
-    const int64_t num_slots = a.num_blocks << a.bs_shift;
+    const int64_t num_slots = a.num_blocks << bs_shift;
     for (int base = 0; base < nvec * GL; base += kBlock) {  // uniform trip count
       const int lid = base + tid;
       const int vi = lid / GL, c = lid % GL;
@@ -393,7 +403,7 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
         const int r = hl * n + j;
         if (r < R) *reinterpret_cast<uint4*>(qsh + r * kQPitch + c * 16) = yr;
       } else if (slot >= 0 && slot < num_slots) {  // padding rows write nothing
-        const int64_t blk = slot >> a.bs_shift;
+        const int64_t blk = slot >> bs_shift;
         const int64_t off = slot & bs_mask;
         store_kv_chunk<GL, INT8>(yr, vr, const_cast<void*>(a.kc), const_cast<void*>(a.vc),
                                  blk * a.c_bs + off * a.c_ts + hkv * a.c_hs + c * 8,
@@ -464,7 +474,7 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
   // of key kb (sub-tile 0) and of key kb + 16 (sub-tile 1); keys past the end are clamped to
   // L - 1, which stays in the page of its 16-key sub-tile.
   auto page_of = [&](int key) {
-    return clamp_page(table[min(key, L - 1) >> a.bs_shift], a.num_blocks);
+    return clamp_page(table[min(key, L - 1) >> bs_shift], a.num_blocks);
   };
 
   // Issue every load of tile `t` (pages pg0/pg1).  Page bases are wave-uniform (scalar);
@@ -988,7 +998,7 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
   // outside the pool) inside its buffers: such calls give wrong rows, never stray accesses.
   int b, hkv, sidx, q0, n, L;
   int32_t pg0, pg1;
-  if (a.plan) {
+  if (mode == 1) {  // a.plan
     if (wave == 0) plan_item(a, lane, sm_plan);
     __syncthreads();
     b = __builtin_amdgcn_readfirstlane(sm_plan[0]);
@@ -998,15 +1008,15 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
     hkv = static_cast<int>(blockIdx.x) % a.Hkv;
     sidx = 0;
     first_pages(b, sidx, pg0, pg1);
-  } else if (a.nwin > 0) {
+  } else if (mode == 2) {  // a.nwin > 0
     const int x = static_cast<int>(blockIdx.x);
     hkv = x % a.Hkv;
     const int rest = x / a.Hkv;
     b = rest / a.nwin;
     const int w = rest - b * a.nwin;
     sidx = 0;
-    const const_i32_ptr cuc = (const_i32_ptr)a.cu;
-    const const_i32_ptr slc = (const_i32_ptr)a.seq_lens;
+    const const_i32_ptr cuc = (const_i32_ptr)cu_p;
+    const const_i32_ptr slc = (const_i32_ptr)sl_p;
     const int c0 = cuc[b], c1 = cuc[b + 1], sl = slc[b];
     first_pages(b, sidx, pg0, pg1);
     const int nall = c1 - c0, j0 = w * a.qwin;
@@ -1022,8 +1032,8 @@ __global__ __launch_bounds__(64 * waves_for(RT), 1) void verify_attn_kernel(Attn
     // count and the first tile's pages, and the kernel-argument lines the Q / K / V (or
     // epilogue) addressing reads.  The empty asm keeps these loads from being spread over the
     // code that uses them, each behind a wait of its own.
-    const const_i32_ptr cuc = (const_i32_ptr)a.cu;
-    const const_i32_ptr slc = (const_i32_ptr)a.seq_lens;
+    const const_i32_ptr cuc = (const_i32_ptr)cu_p;
+    const const_i32_ptr slc = (const_i32_ptr)sl_p;
     const int c0 = cuc[b], c1 = cuc[b + 1], sl = slc[b];
     first_pages(b, sidx, pg0, pg1);
     const void* line4 = FUSED != 0 ? static_cast<const void*>(a.slots) : static_cast<const void*>(a.q);
@@ -1159,21 +1169,21 @@ int launch_rt(int RT, const AttnArgs& a, dim3 grid, hipStream_t s) {
     const bool part = a.qkv_mode == 2;
     if constexpr (fused_ok(D, INT8, 2)) {
       if (RT == 2) {
-        if (part) hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 2, SC, 2>), grid, dim3(64 * waves_for(2)), 0, s, a);
-        else hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 2, SC, 1>), grid, dim3(64 * waves_for(2)), 0, s, a);
+        if (part) hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 2, SC, 2>), grid, dim3(64 * waves_for(2)), 0, s, ATTN_LEAD(a), a);
+        else hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 2, SC, 1>), grid, dim3(64 * waves_for(2)), 0, s, ATTN_LEAD(a), a);
       }
     }
     if (RT == 1) {
-      if (part) hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 1, SC, 2>), grid, dim3(64 * waves_for(1)), 0, s, a);
-      else hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 1, SC, 1>), grid, dim3(64 * waves_for(1)), 0, s, a);
+      if (part) hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 1, SC, 2>), grid, dim3(64 * waves_for(1)), 0, s, ATTN_LEAD(a), a);
+      else hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 1, SC, 1>), grid, dim3(64 * waves_for(1)), 0, s, ATTN_LEAD(a), a);
     }
     return coopt::check_launch("coopt_verify_attention_qkv");  // one split: no merge launch
   }
   switch (RT) {
-    case 1: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 1, SC, 0>), grid, dim3(64 * waves_for(1)), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 2, SC, 0>), grid, dim3(64 * waves_for(2)), 0, s, a); break;
-    case 3: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 3, SC, 0>), grid, dim3(64 * waves_for(3)), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 4, SC, 0>), grid, dim3(64 * waves_for(4)), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 1, SC, 0>), grid, dim3(64 * waves_for(1)), 0, s, ATTN_LEAD(a), a); break;
+    case 2: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 2, SC, 0>), grid, dim3(64 * waves_for(2)), 0, s, ATTN_LEAD(a), a); break;
+    case 3: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 3, SC, 0>), grid, dim3(64 * waves_for(3)), 0, s, ATTN_LEAD(a), a); break;
+    case 4: hipLaunchKernelGGL((verify_attn_kernel<D, INT8, 4, SC, 0>), grid, dim3(64 * waves_for(4)), 0, s, ATTN_LEAD(a), a); break;
     default: return COOPT_EINVAL;
   }
   int rc = coopt::check_launch("coopt_verify_attention");
