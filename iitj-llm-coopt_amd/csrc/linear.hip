@@ -314,11 +314,23 @@ Plan plan_for(int M, int N, int K) {
   // 16 row tiles, or 4 row tiles with 4 column tiles per wave, exceed two waves' registers
   // per SIMD (they spilled to scratch): 4-wave blocks, one wave per SIMD, hold them.
   if (p.mt == 16 || (p.mt == 4 && p.nw == 4)) p.waves = 4;
-  const int cols = p.waves * p.nw * 16;
-  const int nb = (N + cols - 1) / cols;
   const int steps = K / kKB;
-  int ks = 1;
-  while (ks < 16 && nb * ks * 2 <= 256 && steps / (ks * 2) >= 4) ks *= 2;
+  auto split_for = [&](int waves) {  // K splits for `waves` waves of p.nw column tiles
+    const int nb = (N + waves * p.nw * 16 - 1) / (waves * p.nw * 16);
+    int k = 1;
+    while (k < 16 && nb * k * 2 <= 256 && steps / (k * 2) >= 4) k *= 2;
+    return k;
+  };
+  int ks = split_for(p.waves);
+  // 160 rows: 7 waves (112 columns) where that fills more of the 256 CUs than 8 do -- the
+  // target's qkv, N = 6144: 55 x 4 = 220 workgroups against 48 x 4 = 192, 22.2 -> 20.5 us
+  if (p.mt == 10 && p.nw == 1 && p.waves == 8) {
+    const int k7 = split_for(7);
+    if (((N + 111) / 112) * k7 > ((N + 127) / 128) * ks && ((N + 111) / 112) * k7 <= 256) {
+      p.waves = 7;
+      ks = k7;
+    }
+  }
   p.kt = ((steps + ks - 1) / ks) * kKB;
   p.ks = (K + p.kt - 1) / p.kt;
   return p;
@@ -349,6 +361,9 @@ void launch_mt(const Plan& p, const LinArgs& a, bool packed, hipStream_t s) {
         return;
       }
       if (p.waves == 4) return launch_cfg<MT, 1, 4, 2>(p, a, packed, s);
+    }
+    if constexpr (MT == 10) {
+      if (p.waves == 7) return launch_cfg<MT, 1, 7, 2>(p, a, packed, s);
     }
     launch_cfg<MT, 1, 8, 2>(p, a, packed, s);
   }
