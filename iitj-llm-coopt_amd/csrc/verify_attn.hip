@@ -200,13 +200,19 @@ struct RawTile {
   u32x2_t vs[2];         // INT8: fp16 scales of the lane's V keys 4g..4g+3 of each sub-tile
 };
 
+// A lane's V words of one key.  The 8- and 16-byte forms (16 lanes: one whole 128- or 256-byte
+// key row) are nontemporal loads: V is read once per call, and on MI355X the streaming hint
+// raised the rate at every measured shape (bf16 ctx 8192 189 -> 172 us, INT8 107 -> 103 us,
+// ragged config 3 70.5 -> 67.4 us).  K keeps plain loads: one K load instruction covers half
+// of each of its 16 rows' 128-byte lines, and with the hint config 3 went to 77 us.  The
+// 4-byte form (INT8 at D 64, also half a line per instruction) stays plain, unmeasured.
 template <int N>
 __device__ __forceinline__ void load_words(const unsigned char* p, uint32_t* dst) {
   if constexpr (N == 4) {
-    const u32x4_t x = *reinterpret_cast<const u32x4_t*>(p);
+    const u32x4_t x = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
     dst[0] = x[0]; dst[1] = x[1]; dst[2] = x[2]; dst[3] = x[3];
   } else if constexpr (N == 2) {
-    const u32x2_t x = *reinterpret_cast<const u32x2_t*>(p);
+    const u32x2_t x = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
     dst[0] = x[0]; dst[1] = x[1];
   } else {
     dst[0] = *reinterpret_cast<const uint32_t*>(p);
