@@ -376,6 +376,15 @@ __device__ __forceinline__ uint4 dequant_chunk(uint32_t lo, uint32_t hi, uint16_
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// 16 bytes of a bf16 cache read by swap_out, with the nontemporal hint: the blocks are read
+// once.  Alternated with plain loads on MI355X, 32 layers' swap_out went 164-167 -> 160-162 us;
+// the row quantiser, which reads its input the same way, went 22.0 -> 23.1 us with the hint
+// and keeps plain loads.
+__device__ __forceinline__ uint4 ld16_stream(const uint16_t* p) {
+  typedef uint32_t u32x4_v __attribute__((ext_vector_type(4)));
+  return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4_v*>(p)));
+}
+
 template <int G, int BITS, bool SRC8, int U = kSwapOutU>
 __global__ __launch_bounds__(kSwapThreads) void swap_out_kernel(
     CacheSet cs, int64_t c_bs, int64_t c_ts, int64_t c_hs, int64_t s_bs, int64_t s_ts, int64_t s_hs,
@@ -418,7 +427,7 @@ __global__ __launch_bounds__(kSwapThreads) void swap_out_kernel(
       x[u] = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(cache) + off);
       xs[u] = cscale[blk * s_bs + t * s_ts + h * s_hs];
     } else {
-      x[u] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(cache) + off);
+      x[u] = ld16_stream(static_cast<const uint16_t*>(cache) + off);
     }
   }
   // keeps the scheduler from moving each load down to its store (the copying forms have no
@@ -477,8 +486,8 @@ __global__ __launch_bounds__(kSwapThreads) void swap_out_pair_kernel(
     const int v = idx / G2, c = idx % G2;
     const int t = v / Hkv, h = v - t * Hkv;
     const uint16_t* src = cache + blk * c_bs + t * c_ts + h * c_hs + c * 16;
-    xa[u] = *reinterpret_cast<const uint4*>(src);
-    xb[u] = *reinterpret_cast<const uint4*>(src + 8);
+    xa[u] = ld16_stream(src);
+    xb[u] = ld16_stream(src + 8);
   }
   __builtin_amdgcn_sched_barrier(0);  // as in swap_out_kernel
 #pragma unroll
