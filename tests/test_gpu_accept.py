@@ -285,6 +285,41 @@ def test_sample_rows_of_many_chunks(dev, N, V):
     report(f"[sample N={N} V={V}] {int((t == ref_tok).sum())}/{N} rows equal to the oracle")
 
 
+@pytest.mark.parametrize("dtype,N,V", [(torch.float32, 12, 128256), (torch.bfloat16, 5, 50001)])
+def test_sample_probs_reads_the_statistics_of_a_gamma0_accept(dev, dtype, N, V):
+    """coopt_sample_probs: sample()'s probabilities (engine/spec_decode.py:16) for rows a
+    gamma_max = 0 accept call just drew from, built from the row statistics that call left in
+    its workspace.  Within 1e-5 relative of the fp64 softmax and of coopt_sample's own
+    probabilities; a short workspace and T <= 0 are refused."""
+    from iitj_llm_coopt_amd import _lib
+    lib = _lib.load()
+    gen = torch.Generator(device=dev).manual_seed(N + V)
+    x = (torch.randn(N, V, generator=gen, device=dev) * 2.5).to(dtype)
+    u = torch.rand(N, generator=gen, device=dev)
+    T = 0.9
+    need = int(lib.coopt_accept_sample_workspace(N, 0, V))
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    M.accept(x, None, torch.empty((N, 0), dtype=torch.int32, device=dev), T, u_resample=u,
+             workspace=ws)
+    probs = torch.full((N, V), -1.0, dtype=torch.float32, device=dev)
+    stream = _lib.stream_handle(dev)
+    _lib.check(lib.coopt_sample_probs(_lib.dt_code(dtype), _lib.ptr(x), x.stride(0), N, V, T,
+                                      _lib.ptr(ws), need, _lib.ptr(probs), V, stream),
+               "coopt_sample_probs")
+    ref = torch.softmax(x.double().cpu() / torch.tensor(T, dtype=torch.float32).double(), -1)
+    assert torch.allclose(probs.double().cpu(), ref, rtol=1e-5, atol=1e-12)
+    _, sprobs = M.sample(x, T, uniforms=u)
+    assert torch.allclose(probs, sprobs, rtol=1e-5, atol=1e-12)
+    rc = lib.coopt_sample_probs(_lib.dt_code(dtype), _lib.ptr(x), x.stride(0), N, V, T,
+                                _lib.ptr(ws), need - 1, _lib.ptr(probs), V, stream)
+    assert rc == _lib.COOPT_EWORKSPACE
+    rc = lib.coopt_sample_probs(_lib.dt_code(dtype), _lib.ptr(x), x.stride(0), N, V, 0.0,
+                                _lib.ptr(ws), need, _lib.ptr(probs), V, stream)
+    assert rc == _lib.COOPT_EINVAL
+    report(f"[sample_probs {dtype} N={N} V={V}] max |probs - fp64| "
+           f"{(probs.double().cpu() - ref).abs().max().item():.3g}")
+
+
 def test_verify_signature_with_generator(dev):
     gen = torch.Generator(device=dev).manual_seed(10)
     V = 1000
